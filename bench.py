@@ -1,0 +1,208 @@
+#!/usr/bin/env python3
+"""Tree-sparse attention forward benchmark on one MI355X.
+
+Workload (default): the Llama-3-8B verification step -- B=1, 32 query / 8 KV
+heads, head_dim 128, bf16, 4096-token prefix, 64-node EAGLE tree (depth 6,
+top-8), BLOCK_M=16, BLOCK_N=64.  Synthetic N(0,1) inputs (seed 42).
+
+A step is one forward call (split-KV kernel + combine kernel) over the whole
+batch with the metadata already on the device, as benchmark.py:228-237 times
+the reference kernel.  The K steps run inside one captured HIP graph so host
+launch overhead cannot starve the GPU, and they cycle through enough
+independent K/V copies (>= 512 MiB) that every call reads its K/V from HBM
+rather than from the 256 MB Infinity Cache.
+
+value      = K/V bytes per call * K / timed seconds  (TB/s, whole call)
+roofline   = the split-KV kernel alone: K/V bytes / its average duration,
+             measured with HIP events recorded around it inside the graph,
+             against 8 TB/s HBM
+cpu_baseline = the fp32 dense+mask oracle (benchmark.py:8-35 restated) on the
+             host cores, over a bounded sample of calls
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "eagle3-tree-sparse-flashattn_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "tree-attn fwd µs + achieved HBM TB/s, 8B shape, 4k prefix, 64-node tree"
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _traffic(workload: str):
+    """HBM bytes per split-kernel launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", "split_kernel_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(workload)
+        return None if rec is None else float(rec["bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def cpu_baseline(w, q, k, v, mask, seconds: float):
+    import torch
+
+    from oracle.attn_oracle import dense_mask_attention
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    t0 = time.perf_counter()
+    dense_mask_attention(q, k, v, mask, w.prefix_len, head_chunk=8)
+    t1 = time.perf_counter() - t0
+    n = max(1, min(1000, int(seconds / max(t1, 1e-6))))
+    t0 = time.perf_counter()
+    for _ in range(n):
+        dense_mask_attention(q, k, v, mask, w.prefix_len, head_chunk=8)
+    dt = (time.perf_counter() - t0) / n
+    return {
+        "value": w.kv_bytes() / dt / 1e12,
+        "unit": "TB/s",
+        "us_per_call": dt * 1e6,
+        "cores": cores,
+        "kind": "port",
+        "sample": f"{n} full calls of the fp32 dense+mask oracle on the same inputs (torch CPU, {cores} threads)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default=None)
+    ap.add_argument("--cold-mib", type=int, default=512, help="K/V bytes cycled through (defeats the MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}); "
+              "the forward shards by (batch, kv head) with no exchange -- run one process per GPU.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from tsfa import _lib, configs
+    import tree_sparse_flashattn as tsf
+
+    w = configs.WORKLOADS[args.workload or configs.HEADLINE]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    q, k, v = configs.make_qkv(w)
+    mask = configs.make_tree_mask(w)
+    kvb = w.kv_bytes()
+    copies = max(1, min(64, math.ceil(args.cold_mib * 2 ** 20 / kvb)))
+    qd = q.to(dev)
+    ks = [k.to(dev) for _ in range(copies)]
+    vs = [v.to(dev) for _ in range(copies)]
+    if w.per_sequence:
+        meta = tsf.prepare_tree_sparse_metadata_batched(mask.to(dev), w.prefix_len, w.block_m, w.block_n)
+    else:
+        meta = tsf.prepare_tree_sparse_metadata(mask.to(dev), w.prefix_len, w.block_m, w.block_n)
+    out = torch.empty_like(qd)
+    plan = _lib.fwd_plan(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len, w.head_dim)
+    lib = _lib.load()
+
+    def call(i):
+        tsf.tree_sparse_attention_fwd(qd, ks[i % copies], vs[i % copies], meta, out=out)
+
+    _log(f"[bench] {w.name}: warmup {args.warmup}, steps {args.steps}, K/V copies {copies}, plan {plan}")
+    for i in range(max(1, args.warmup)):
+        call(i)
+    torch.cuda.synchronize()
+
+    steps = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for b, e in ev:  # materialise the underlying hipEvent_t handles
+        b.record()
+        e.record()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call(0)  # allocator warm-up on the capture stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(steps):
+                _lib.check("tsfa_fwd_set_split_events",
+                           lib.tsfa_fwd_set_split_events(ev[i][0].cuda_event, ev[i][1].cuda_event))
+                call(i)
+        _lib.check("tsfa_fwd_set_split_events", lib.tsfa_fwd_set_split_events(None, None))
+    torch.cuda.synchronize()
+    graph.replay()  # warm replay (graph upload)
+    torch.cuda.synchronize()
+
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    graph.replay()
+    t_end.record()
+    torch.cuda.synchronize()
+    total_ms = t_start.elapsed_time(t_end)
+    split_ms = [b.elapsed_time(e) for b, e in ev]
+    split_avg_s = sum(split_ms) / len(split_ms) / 1e3
+    per_call_s = total_ms / 1e3 / steps
+    _log(f"[bench] {steps} calls in {total_ms:.3f} ms: {per_call_s * 1e6:.2f} us/call, "
+         f"split kernel avg {split_avg_s * 1e6:.2f} us (min {min(split_ms) * 1e3:.2f} us)")
+
+    achieved_gbps = kvb / split_avg_s / 1e9
+    traffic = _traffic(w.name)
+    result = {
+        "metric": METRIC,
+        "value": round(kvb / per_call_s / 1e12, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per_call_s * 1e3, 6),
+        "us_per_call": round(per_call_s * 1e6, 3),
+        "tokens_per_s": round(w.batch * w.tree_len / per_call_s, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16"}[w.dtype],
+        "data": "synthetic N(0,1) q/k/v, seeded EAGLE draft tree; metadata built on the device beforehand",
+        "config": {
+            "workload": w.name,
+            "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
+            "prefix_len": w.prefix_len, "tree_len": w.tree_len, "block_m": w.block_m, "block_n": w.block_n,
+            "kv_bytes_per_call": kvb, "kv_copies_cycled": copies, "plan": plan, "timing": "hip graph of all steps",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "tsfa::fwd::split_kernel",
+            "achieved": round(achieved_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "split_kernel_us": round(split_avg_s * 1e6, 3),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        _log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(w, q, k, v, mask, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

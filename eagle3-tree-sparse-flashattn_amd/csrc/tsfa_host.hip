@@ -1,0 +1,54 @@
+// Host-side utilities of libtsfa: version, status strings and a per-device
+// cache of the attributes the forward planner needs.
+
+#include <atomic>
+
+#include "tsfa_internal.h"
+
+namespace tsfa {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+std::atomic<int> g_max_lds[kMaxDevices];
+
+int current_device(int* dev) {
+  if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kMaxDevices) return TSFA_ERR_DEVICE;
+  return TSFA_OK;
+}
+
+int cached_attr(std::atomic<int>* cache, hipDeviceAttribute_t attr, int* out) {
+  int dev = 0;
+  if (current_device(&dev) != TSFA_OK) return TSFA_ERR_DEVICE;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, attr, dev) != hipSuccess || v <= 0) return TSFA_ERR_DEVICE;
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  *out = v;
+  return TSFA_OK;
+}
+
+}  // namespace
+
+int device_cu_count(int* out) { return cached_attr(g_cu_count, hipDeviceAttributeMultiprocessorCount, out); }
+
+int device_max_lds_per_block(int* out) {
+  return cached_attr(g_max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, out);
+}
+
+}  // namespace tsfa
+
+extern "C" int tsfa_version(void) { return 1; }
+
+extern "C" const char* tsfa_status_string(int status) {
+  switch (status) {
+    case TSFA_OK: return "ok";
+    case TSFA_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case TSFA_ERR_UNSUPPORTED: return "unsupported configuration";
+    case TSFA_ERR_WORKSPACE: return "workspace missing or too small";
+    case TSFA_ERR_LAUNCH: return "kernel launch failed";
+    case TSFA_ERR_DEVICE: return "no usable HIP device";
+    default: return "unknown status";
+  }
+}

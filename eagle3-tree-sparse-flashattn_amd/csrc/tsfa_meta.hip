@@ -1,0 +1,246 @@
+// Tree-sparse metadata builder on the GPU: tiling, ZERO/FULL/MIXED
+// classification, CSR construction and row-major int32 bitset packing.
+//
+// Output is bit-exact with prepare_tree_sparse_metadata
+// (tree_sparse_flashattn.py:67-160) applied per sequence:
+//   * blocks are visited row-major (q-block, then tree block; :103-108);
+//   * a block with no set bit is ZERO and absent (:113-114);
+//   * FULL iff every element of the block CLIPPED to q_len is set (:116-124),
+//     with a 0 placeholder in the offset array;
+//   * otherwise MIXED: the block zero-padded to block_m x block_n is packed
+//     with bit i of word w = flat[32w+i], flat = r*block_n + c (:44-64), and
+//     its offset is the running payload cursor (:125-134);
+//   * row_ptr is the running nnz count (:136).
+//
+// Two launches per call: `classify` (one workgroup per block and sequence)
+// packs words and counts bits; `compact` (one workgroup per sequence) scans
+// the block classes and scatters the CSR arrays and MIXED payload.
+
+#include "tsfa_internal.h"
+
+namespace tsfa {
+
+namespace {
+
+constexpr int kMetaThreads = 256;
+
+enum : int8_t { kZero = 0, kFull = 1, kMixed = 2 };
+
+struct MetaGeom {
+  int q_len, block_m, block_n, nqb, ntb, words;  // words = W per block
+  int64_t cap;                                   // nqb * ntb
+};
+
+__global__ __launch_bounds__(kMetaThreads) void classify_kernel(
+    const uint8_t* __restrict__ mask, int64_t seq_stride, int64_t row_stride, MetaGeom g,
+    int8_t* __restrict__ cls, int32_t* __restrict__ words) {
+  const int blk = blockIdx.x;  // qb * ntb + tb
+  const int seq = blockIdx.y;
+  const int qb = blk / g.ntb, tb = blk - qb * g.ntb;
+  const int q0 = qb * g.block_m, k0 = tb * g.block_n;
+  const int h = min(g.block_m, g.q_len - q0);
+  const int w = min(g.block_n, g.q_len - k0);
+  const uint8_t* m = mask + seq * seq_stride + (int64_t)q0 * row_stride + k0;
+  int32_t* out = words + ((int64_t)seq * g.cap + blk) * g.words;
+  const int64_t n_flat = (int64_t)g.block_m * g.block_n;
+
+  int ones = 0;
+  for (int wi = threadIdx.x; wi < g.words; wi += kMetaThreads) {
+    int64_t flat = (int64_t)wi * 32;
+    int r = (int)(flat / g.block_n);
+    int c = (int)(flat - (int64_t)r * g.block_n);
+    uint32_t word = 0;
+    for (int i = 0; i < 32 && flat + i < n_flat; ++i) {
+      if (r < h && c < w && m[(int64_t)r * row_stride + c] != 0) word |= 1u << i;
+      if (++c == g.block_n) { c = 0; ++r; }
+    }
+    out[wi] = (int32_t)word;
+    ones += __popc(word);
+  }
+
+  __shared__ int red[kMetaThreads / 64];
+  for (int off = 32; off > 0; off >>= 1) ones += __shfl_xor(ones, off);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ones;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int total = 0;
+    for (int i = 0; i < kMetaThreads / 64; ++i) total += red[i];
+    int8_t c = kZero;
+    if (total > 0) c = (total == h * w) ? kFull : kMixed;
+    cls[(int64_t)seq * g.cap + blk] = c;
+  }
+}
+
+// Block-wide exclusive scan of (a, b) pairs; returns the totals.
+__device__ inline void scan2(int a, int b, int* ex_a, int* ex_b, int* tot_a, int* tot_b) {
+  __shared__ int sa[kMetaThreads], sb[kMetaThreads];
+  const int t = threadIdx.x;
+  sa[t] = a;
+  sb[t] = b;
+  __syncthreads();
+  for (int off = 1; off < kMetaThreads; off <<= 1) {
+    int va = (t >= off) ? sa[t - off] : 0;
+    int vb = (t >= off) ? sb[t - off] : 0;
+    __syncthreads();
+    sa[t] += va;
+    sb[t] += vb;
+    __syncthreads();
+  }
+  *ex_a = sa[t] - a;
+  *ex_b = sb[t] - b;
+  *tot_a = sa[kMetaThreads - 1];
+  *tot_b = sb[kMetaThreads - 1];
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kMetaThreads) void compact_kernel(
+    MetaGeom g, const int8_t* __restrict__ cls, const int32_t* __restrict__ words,
+    int32_t* __restrict__ src_of_rank, int32_t* __restrict__ row_ptr, int32_t* __restrict__ col_idx,
+    int8_t* __restrict__ blk_type, int32_t* __restrict__ payload, int32_t* __restrict__ offset,
+    int32_t* __restrict__ counts) {
+  const int seq = blockIdx.x;
+  const int64_t nb = g.cap;
+  const int8_t* c = cls + seq * nb;
+  const int per = (int)((nb + kMetaThreads - 1) / kMetaThreads);
+  const int64_t i0 = min((int64_t)threadIdx.x * per, nb);
+  const int64_t i1 = min(i0 + per, nb);
+
+  int nz = 0, mx = 0;
+  for (int64_t i = i0; i < i1; ++i) {
+    nz += c[i] != kZero;
+    mx += c[i] == kMixed;
+  }
+  int nz_base, mx_base, nnz, n_mixed;
+  scan2(nz, mx, &nz_base, &mx_base, &nnz, &n_mixed);
+
+  int32_t* rp = row_ptr + (int64_t)seq * (g.nqb + 1);
+  int32_t* ci = col_idx + seq * nb;
+  int8_t* bt = blk_type + seq * nb;
+  int32_t* of = offset + seq * nb;
+  int32_t* sr = src_of_rank + seq * nb;
+  for (int64_t i = i0; i < i1; ++i) {
+    const int qb = (int)(i / g.ntb), tb = (int)(i - (int64_t)qb * g.ntb);
+    if (tb == 0) rp[qb] = nz_base;
+    const int8_t k = c[i];
+    if (k == kZero) continue;
+    ci[nz_base] = tb;
+    bt[nz_base] = (k == kFull) ? TSFA_FULL_BLOCK : TSFA_MIXED_BLOCK;
+    if (k == kMixed) {
+      of[nz_base] = mx_base * g.words;
+      sr[mx_base] = (int32_t)i;
+      ++mx_base;
+    } else {
+      of[nz_base] = 0;
+    }
+    ++nz_base;
+  }
+  if (threadIdx.x == 0) {
+    rp[g.nqb] = nnz;
+    counts[2 * seq] = nnz;
+    counts[2 * seq + 1] = n_mixed;
+  }
+  __syncthreads();  // src_of_rank complete (workgroup-scope fence + barrier)
+
+  const int64_t total = (int64_t)n_mixed * g.words;
+  const int32_t* wsrc = words + seq * nb * g.words;
+  int32_t* pl = payload + seq * nb * g.words;
+  for (int64_t e = threadIdx.x; e < total; e += kMetaThreads) {
+    const int64_t r = e / g.words, wi = e - r * g.words;
+    pl[e] = wsrc[(int64_t)sr[r] * g.words + wi];
+  }
+}
+
+__global__ void pack_bits_kernel(const uint8_t* __restrict__ bits, int64_t n_bits, int32_t* __restrict__ words,
+                                 int64_t n_words) {
+  const int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (wi >= n_words) return;
+  uint32_t word = 0;
+  for (int i = 0; i < 32; ++i) {
+    const int64_t f = wi * 32 + i;
+    if (f < n_bits && bits[f] != 0) word |= 1u << i;
+  }
+  words[wi] = (int32_t)word;
+}
+
+bool meta_geom(int q_len, int block_m, int block_n, MetaGeom* g) {
+  g->q_len = q_len;
+  g->block_m = block_m;
+  g->block_n = block_n;
+  g->nqb = ceil_div(q_len, block_m);
+  g->ntb = ceil_div(q_len, block_n);
+  const int64_t words = ((int64_t)block_m * block_n + 31) / 32;
+  g->cap = (int64_t)g->nqb * g->ntb;
+  if (words > INT32_MAX || g->cap * words > INT32_MAX) return false;  // int32 payload offsets
+  g->words = (int)words;
+  return true;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
+}  // namespace tsfa
+
+using namespace tsfa;
+
+extern "C" int tsfa_meta_check_args(int n_seq, int q_len, int block_m, int block_n) {
+  if (block_m <= 0 || block_n <= 0 || n_seq < 0 || q_len < 0) return TSFA_ERR_INVALID_ARGUMENT;
+  MetaGeom g;
+  if (!meta_geom(q_len, block_m, block_n, &g)) return TSFA_ERR_UNSUPPORTED;
+  if ((int64_t)n_seq * g.cap * g.words > ((int64_t)1 << 40)) return TSFA_ERR_UNSUPPORTED;
+  if (n_seq > 65535) return TSFA_ERR_UNSUPPORTED;  // grid.y
+  return TSFA_OK;
+}
+
+extern "C" size_t tsfa_meta_workspace_bytes(int n_seq, int q_len, int block_m, int block_n) {
+  if (tsfa_meta_check_args(n_seq, q_len, block_m, block_n) != TSFA_OK) return 0;
+  MetaGeom g;
+  meta_geom(q_len, block_m, block_n, &g);
+  const size_t nb = (size_t)n_seq * g.cap;
+  return align256(nb) + align256(nb * g.words * 4) + align256(nb * 4);
+}
+
+extern "C" int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int64_t mask_row_stride,
+                               int n_seq, int q_len, int block_m, int block_n, int32_t* row_ptr,
+                               int32_t* col_idx, int8_t* blk_type, int32_t* payload, int32_t* offset,
+                               int32_t* counts, void* workspace, size_t workspace_bytes,
+                               tsfa_stream_t stream_) {
+  int st = tsfa_meta_check_args(n_seq, q_len, block_m, block_n);
+  if (st != TSFA_OK) return st;
+  if (n_seq == 0) return TSFA_OK;
+  if (row_ptr == nullptr || counts == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  MetaGeom g;
+  meta_geom(q_len, block_m, block_n, &g);
+  const size_t need = tsfa_meta_workspace_bytes(n_seq, q_len, block_m, block_n);
+  if (g.cap > 0 && (workspace == nullptr || workspace_bytes < need)) return TSFA_ERR_WORKSPACE;
+  if (g.cap > 0 && (mask == nullptr || col_idx == nullptr || blk_type == nullptr || payload == nullptr ||
+                    offset == nullptr))
+    return TSFA_ERR_INVALID_ARGUMENT;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const size_t nb = (size_t)n_seq * g.cap;
+  int8_t* cls = static_cast<int8_t*>(workspace);
+  int32_t* words = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb));
+  int32_t* src_of_rank =
+      reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb) + align256(nb * g.words * 4));
+  if (g.cap > 0) {
+    if (g.cap > INT32_MAX) return TSFA_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(classify_kernel, dim3((unsigned)g.cap, (unsigned)n_seq), dim3(kMetaThreads), 0, stream,
+                       mask, mask_seq_stride, mask_row_stride, g, cls, words);
+    if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  }
+  hipLaunchKernelGGL(compact_kernel, dim3((unsigned)n_seq), dim3(kMetaThreads), 0, stream, g, cls, words,
+                     src_of_rank, row_ptr, col_idx, blk_type, payload, offset, counts);
+  if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  return TSFA_OK;
+}
+
+extern "C" int tsfa_pack_bits(const uint8_t* bits, int64_t n_bits, int32_t* words, tsfa_stream_t stream_) {
+  if (n_bits < 0) return TSFA_ERR_INVALID_ARGUMENT;
+  const int64_t n_words = (n_bits + 31) / 32;
+  if (n_words == 0) return TSFA_OK;
+  if (bits == nullptr || words == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  if (n_words > ((int64_t)1 << 31)) return TSFA_ERR_UNSUPPORTED;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const unsigned grid = (unsigned)((n_words + 255) / 256);
+  hipLaunchKernelGGL(pack_bits_kernel, dim3(grid), dim3(256), 0, stream, bits, n_bits, words, n_words);
+  return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+}

@@ -1,0 +1,319 @@
+"""Tree-sparse FlashAttention for MI355X: the metadata protocol and forward.
+
+Drop-in for the reference module ``tree_sparse_flashattn.py`` (same public
+names, argument meaning and errors).  Everything here is host plumbing around
+libtsfa.so (hand-written HIP for gfx950): the metadata builder and the
+forward run on the GPU; there is no CPU fallback.
+
+Public API (reference citations):
+  FULL_BLOCK, MIXED_BLOCK                  tree_sparse_flashattn.py:11-12
+  TreeSparseMetadata                       tree_sparse_flashattn.py:15-41
+  _pack_block_mask_to_int32                tree_sparse_flashattn.py:44-64
+  prepare_tree_sparse_metadata             tree_sparse_flashattn.py:67-160
+  block_sparse_tree_fwd_kernel[grid](...)  tree_sparse_flashattn.py:163-339
+Extensions (no reference counterpart):
+  BatchedTreeSparseMetadata / prepare_tree_sparse_metadata_batched: one tree
+  per sequence; slice b is bit-identical to prepare_tree_sparse_metadata of
+  tree b.
+  tree_sparse_attention_fwd: allocate O and launch with either record.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional
+
+import torch
+
+from tsfa import _lib
+
+FULL_BLOCK = 0
+MIXED_BLOCK = 1
+
+
+@dataclass
+class TreeSparseMetadata:
+    """Compressed tree-block metadata for sparse verification attention.
+
+    Attributes (tree_sparse_flashattn.py:15-41):
+        row_ptr: CSR row pointer over Q blocks, int32 [n_q_blocks + 1].
+        col_idx: CSR column indices of tree KV blocks, int32 [nnz_blocks].
+        blk_type: FULL(0) or MIXED(1) per nnz block, int8 [nnz_blocks].
+        mixed_mask_payload: packed MIXED bitsets, int32 [n_mixed * ceil(BM*BN/32)].
+        mixed_mask_offset: payload offset per nnz block (0 for FULL), int32
+            [nnz_blocks]; EMPTY when there is no MIXED block.
+        n_q_blocks, n_tree_blocks, block_m, block_n, prefix_len: ints.
+    """
+
+    row_ptr: torch.Tensor
+    col_idx: torch.Tensor
+    blk_type: torch.Tensor
+    mixed_mask_payload: torch.Tensor
+    mixed_mask_offset: torch.Tensor
+    n_q_blocks: int
+    n_tree_blocks: int
+    block_m: int
+    block_n: int
+    prefix_len: int
+
+
+@dataclass
+class BatchedTreeSparseMetadata:
+    """One tree per sequence, in capacity layout (cap = n_q_blocks*n_tree_blocks).
+
+    row_ptr [B, n_q_blocks+1]; col_idx, blk_type, mixed_mask_offset [B, cap];
+    mixed_mask_payload [B, cap*W]; nnz[b] / n_mixed[b] entries of sequence b are
+    valid.  ``sequence(b)`` returns the reference-shaped record of tree b.
+    """
+
+    row_ptr: torch.Tensor
+    col_idx: torch.Tensor
+    blk_type: torch.Tensor
+    mixed_mask_payload: torch.Tensor
+    mixed_mask_offset: torch.Tensor
+    nnz: List[int]
+    n_mixed: List[int]
+    n_q_blocks: int
+    n_tree_blocks: int
+    block_m: int
+    block_n: int
+    prefix_len: int
+
+    @property
+    def words_per_block(self) -> int:
+        return (self.block_m * self.block_n + 31) // 32
+
+    def sequence(self, b: int) -> TreeSparseMetadata:
+        nnz, nmx, w = self.nnz[b], self.n_mixed[b], self.words_per_block
+        return TreeSparseMetadata(
+            row_ptr=self.row_ptr[b],
+            col_idx=self.col_idx[b, :nnz],
+            blk_type=self.blk_type[b, :nnz],
+            mixed_mask_payload=self.mixed_mask_payload[b, : nmx * w],
+            mixed_mask_offset=self.mixed_mask_offset[b, :nnz] if nmx > 0 else self.mixed_mask_offset[b, :0],
+            n_q_blocks=self.n_q_blocks,
+            n_tree_blocks=self.n_tree_blocks,
+            block_m=self.block_m,
+            block_n=self.block_n,
+            prefix_len=self.prefix_len,
+        )
+
+
+def _hip_device(t: torch.Tensor) -> torch.device:
+    if t.is_cuda:
+        return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("the tree-sparse metadata builder runs on a HIP device; none is available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _pack_block_mask_to_int32(mask_2d: torch.Tensor) -> torch.Tensor:
+    """Pack a bool [BLOCK_M, BLOCK_N] block row-major into int32 words.
+
+    Bit i of word w is flat[32w + i] (tree_sparse_flashattn.py:44-64); the
+    result lives on the input's device.
+    """
+    dev = _hip_device(mask_2d)
+    flat = mask_2d.reshape(-1).to(device=dev, dtype=torch.bool).contiguous().view(torch.uint8)
+    n_bits = flat.numel()
+    out = torch.zeros(((n_bits + 31) // 32,), dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check("tsfa_pack_bits", _lib.load().tsfa_pack_bits(_lib.ptr(flat), n_bits, _lib.ptr(out),
+                                                               _lib.stream_handle(dev)))
+    return out.to(mask_2d.device)
+
+
+def _meta_build(masks_u8: torch.Tensor, block_m: int, block_n: int, dev: torch.device):
+    """Run tsfa_meta_build over [n_seq, q_len, q_len] uint8 masks on `dev`."""
+    lib = _lib.load()
+    n_seq, q_len = masks_u8.shape[0], masks_u8.shape[1]
+    _lib.check("prepare_tree_sparse_metadata", lib.tsfa_meta_check_args(n_seq, q_len, block_m, block_n))
+    nqb = (q_len + block_m - 1) // block_m
+    ntb = (q_len + block_n - 1) // block_n
+    words = (block_m * block_n + 31) // 32
+    cap = nqb * ntb
+    i32 = dict(dtype=torch.int32, device=dev)
+    row_ptr = torch.empty((n_seq, nqb + 1), **i32)
+    col_idx = torch.empty((n_seq, cap), **i32)
+    blk_type = torch.empty((n_seq, cap), dtype=torch.int8, device=dev)
+    payload = torch.empty((n_seq, cap * words), **i32)
+    offset = torch.empty((n_seq, cap), **i32)
+    counts = torch.empty((n_seq, 2), **i32)
+    ws_bytes = lib.tsfa_meta_workspace_bytes(n_seq, q_len, block_m, block_n)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib.tsfa_meta_build(_lib.ptr(masks_u8), masks_u8.stride(0), masks_u8.stride(1), n_seq, q_len,
+                                 block_m, block_n, _lib.ptr(row_ptr), _lib.ptr(col_idx), _lib.ptr(blk_type),
+                                 _lib.ptr(payload), _lib.ptr(offset), _lib.ptr(counts), _lib.ptr(ws), ws_bytes,
+                                 _lib.stream_handle(dev))
+    _lib.check("prepare_tree_sparse_metadata", st)
+    return row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb
+
+
+def _masks_u8(tree_masks: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    m = tree_masks.to(device=dev)
+    if m.dtype != torch.bool:
+        m = m != 0  # nonzero -> visible, NaN included (tree_sparse_flashattn.py:90)
+    if m.stride(-1) != 1:
+        m = m.contiguous()
+    return m.view(torch.uint8)
+
+
+def prepare_tree_sparse_metadata(
+    tree_mask: torch.Tensor,
+    prefix_len: int,
+    BLOCK_M: int,
+    BLOCK_N: int,
+) -> TreeSparseMetadata:
+    """Generate CSR + tri-state metadata for block-sparse tree attention.
+
+    Same contract as tree_sparse_flashattn.py:67-160: ``tree_mask`` is a
+    [q_len, q_len] tensor of any dtype (nonzero = visible); ValueError for a
+    non-square mask or non-positive block sizes.  The tensors come back on the
+    mask's device (a CPU mask is processed on the current HIP device and the
+    result copied back).
+    """
+    if tree_mask.ndim != 2 or tree_mask.shape[0] != tree_mask.shape[1]:
+        raise ValueError("tree_mask must be shape [q_len, q_len].")
+    if BLOCK_M <= 0 or BLOCK_N <= 0:
+        raise ValueError("BLOCK_M and BLOCK_N must be positive.")
+    dev = _hip_device(tree_mask)
+    masks = _masks_u8(tree_mask, dev).unsqueeze(0)
+    row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N, dev)
+    nnz, n_mixed = (int(x) for x in counts[0].tolist())
+    words = (BLOCK_M * BLOCK_N + 31) // 32
+    out_dev = tree_mask.device
+    return TreeSparseMetadata(
+        row_ptr=row_ptr[0].to(out_dev),
+        col_idx=col_idx[0, :nnz].to(out_dev),
+        blk_type=blk_type[0, :nnz].to(out_dev),
+        mixed_mask_payload=payload[0, : n_mixed * words].to(out_dev),
+        mixed_mask_offset=(offset[0, :nnz] if n_mixed > 0 else offset[0, :0]).to(out_dev),
+        n_q_blocks=nqb,
+        n_tree_blocks=ntb,
+        block_m=BLOCK_M,
+        block_n=BLOCK_N,
+        prefix_len=prefix_len,
+    )
+
+
+def prepare_tree_sparse_metadata_batched(
+    tree_masks: torch.Tensor,
+    prefix_len: int,
+    BLOCK_M: int,
+    BLOCK_N: int,
+) -> BatchedTreeSparseMetadata:
+    """Per-sequence metadata for [B, q_len, q_len] masks, built in one launch."""
+    if tree_masks.ndim != 3 or tree_masks.shape[1] != tree_masks.shape[2]:
+        raise ValueError("tree_masks must be shape [batch, q_len, q_len].")
+    if BLOCK_M <= 0 or BLOCK_N <= 0:
+        raise ValueError("BLOCK_M and BLOCK_N must be positive.")
+    dev = _hip_device(tree_masks)
+    masks = _masks_u8(tree_masks, dev)
+    row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N, dev)
+    cnt = counts.cpu()
+    return BatchedTreeSparseMetadata(
+        row_ptr=row_ptr, col_idx=col_idx, blk_type=blk_type, mixed_mask_payload=payload,
+        mixed_mask_offset=offset, nnz=[int(x) for x in cnt[:, 0]], n_mixed=[int(x) for x in cnt[:, 1]],
+        n_q_blocks=nqb, n_tree_blocks=ntb, block_m=BLOCK_M, block_n=BLOCK_N, prefix_len=prefix_len)
+
+
+def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_strides, strides, sm_scale,
+                batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks,
+                gqa_group_size, block_m, block_n, head_dim):
+    lib = _lib.load()
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a HIP device tensor")
+    dev = q.device
+    for name, t in (("row_ptr", row_ptr), ("col_idx", col_idx), ("blk_type", blk_type),
+                    ("mixed_mask_payload", payload), ("mixed_mask_offset", offset)):
+        if t.device != dev:
+            raise ValueError(f"{name} must be on {dev} (move the metadata to the device first)")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype):
+        raise NotImplementedError("q, k, v and o must share one dtype")
+    dt = _lib.dtype_code(q.dtype)
+    args = (batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks,
+            gqa_group_size, block_m, block_n, head_dim, dt)
+    _lib.check("block_sparse_tree_fwd_kernel", lib.tsfa_fwd_check_args(*args))
+    ws_bytes = lib.tsfa_fwd_workspace_bytes(batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
+                                            head_dim)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib.tsfa_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(row_ptr), _lib.ptr(col_idx),
+                          _lib.ptr(blk_type), _lib.ptr(payload), _lib.ptr(offset), _lib.i64_array(meta_strides),
+                          _lib.i64_array(strides), float(sm_scale), *args, _lib.ptr(ws), ws_bytes,
+                          _lib.stream_handle(dev))
+    _lib.check("block_sparse_tree_fwd_kernel", st)
+    return o
+
+
+class _BlockSparseTreeFwdKernel:
+    """``block_sparse_tree_fwd_kernel[grid](...)`` with the reference's arguments.
+
+    Positional arguments follow tree_sparse_flashattn.py:164-199 (9 tensors,
+    16 strides, sm_scale, 10 ints); BLOCK_M/BLOCK_N/BLOCK_D are keywords as in
+    the reference.  ``grid`` and Triton launch options (num_warps,
+    num_stages) are accepted and ignored: the HIP forward chooses its own
+    split-KV decomposition.  The launch is asynchronous on the current stream
+    of q's device.
+    """
+
+    def __getitem__(self, grid):
+        def launch(q_ptr, k_ptr, v_ptr, o_ptr, row_ptr_ptr, col_idx_ptr, blk_type_ptr, mixed_mask_payload_ptr,
+                   mixed_mask_offset_ptr, stride_qb, stride_qh, stride_qm, stride_qd, stride_kb, stride_kh,
+                   stride_kn, stride_kd, stride_vb, stride_vh, stride_vn, stride_vd, stride_ob, stride_oh,
+                   stride_om, stride_od, sm_scale, batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
+                   n_q_blocks, n_tree_blocks, gqa_group_size, *, BLOCK_M, BLOCK_N, BLOCK_D, num_warps=None,
+                   num_stages=None, **_unused):
+            if BLOCK_D != q_ptr.shape[-1]:
+                raise ValueError(f"BLOCK_D ({BLOCK_D}) must equal head_dim ({q_ptr.shape[-1]})")
+            strides = (stride_qb, stride_qh, stride_qm, stride_qd, stride_kb, stride_kh, stride_kn, stride_kd,
+                       stride_vb, stride_vh, stride_vn, stride_vd, stride_ob, stride_oh, stride_om, stride_od)
+            return _launch_fwd(q_ptr, k_ptr, v_ptr, o_ptr, row_ptr_ptr, col_idx_ptr, blk_type_ptr,
+                               mixed_mask_payload_ptr, mixed_mask_offset_ptr, (0, 0, 0, 0, 0), strides, sm_scale,
+                               batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
+                               n_tree_blocks, gqa_group_size, BLOCK_M, BLOCK_N, BLOCK_D)
+
+        return launch
+
+    def __call__(self, *args, **kwargs):
+        raise TypeError("launch with block_sparse_tree_fwd_kernel[grid](...)")
+
+
+block_sparse_tree_fwd_kernel = _BlockSparseTreeFwdKernel()
+
+
+def _row_contig(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        return t.contiguous()
+    return t
+
+
+def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta, *,
+                              sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """O = tree-sparse attention of q [B,Hq,T,D] over k/v [B,Hkv,P+T,D].
+
+    ``meta`` is a TreeSparseMetadata (one tree for the whole batch) or a
+    BatchedTreeSparseMetadata (one tree per sequence), already on q's device.
+    """
+    q, k, v = _row_contig(q), _row_contig(k), _row_contig(v)
+    bsz, n_heads, q_len, head_dim = q.shape
+    _, n_kv_heads, kv_len, _ = k.shape
+    if out is None:
+        out = torch.empty_like(q)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if isinstance(meta, BatchedTreeSparseMetadata):
+        if meta.row_ptr.shape[0] != bsz:
+            raise ValueError("batched metadata must have one tree per sequence")
+        tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
+        meta_strides = tuple(t.stride(0) for t in tensors)
+    else:
+        tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
+        meta_strides = (0, 0, 0, 0, 0)
+    strides = (*q.stride(), *k.stride(), *v.stride(), *out.stride())
+    return _launch_fwd(q, k, v, out, *tensors, meta_strides, strides, sm_scale, bsz, n_heads, n_kv_heads, q_len,
+                       kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, n_heads // n_kv_heads,
+                       meta.block_m, meta.block_n, head_dim)

@@ -1,0 +1,135 @@
+"""ctypes binding of libtsfa.so (declarations: include/tsfa.h).
+
+The library is loaded after ``import torch`` so that it binds to the HIP
+runtime torch already loaded (one runtime per process; torch's stream handles
+are then valid for libtsfa).  There is no fallback: if the library is missing
+or a call fails, an exception is raised.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent.parent / "libtsfa.so"
+
+TSFA_OK = 0
+TSFA_ERR_INVALID_ARGUMENT = 1
+TSFA_ERR_UNSUPPORTED = 2
+TSFA_ERR_WORKSPACE = 3
+TSFA_ERR_LAUNCH = 4
+TSFA_ERR_DEVICE = 5
+
+TSFA_DTYPE_FP16 = 0
+TSFA_DTYPE_BF16 = 1
+
+EXPORTS = (
+    "tsfa_version",
+    "tsfa_status_string",
+    "tsfa_meta_check_args",
+    "tsfa_meta_workspace_bytes",
+    "tsfa_meta_build",
+    "tsfa_pack_bits",
+    "tsfa_fwd_check_args",
+    "tsfa_fwd_workspace_bytes",
+    "tsfa_fwd",
+    "tsfa_fwd_plan",
+    "tsfa_fwd_set_split_events",
+)
+
+_c_int, _c_i64, _c_size, _c_vp, _c_float = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
+
+_SIGNATURES = {
+    "tsfa_version": (_c_int, []),
+    "tsfa_status_string": (ctypes.c_char_p, [_c_int]),
+    "tsfa_meta_check_args": (_c_int, [_c_int] * 4),
+    "tsfa_meta_workspace_bytes": (_c_size, [_c_int] * 4),
+    "tsfa_meta_build": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                 _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "tsfa_pack_bits": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp]),
+    "tsfa_fwd_check_args": (_c_int, [_c_int] * 13),
+    "tsfa_fwd_workspace_bytes": (_c_size, [_c_int] * 7),
+    "tsfa_fwd": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                          ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
+                 + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
+    "tsfa_fwd_plan": (_c_int, [_c_int] * 7 + [ctypes.POINTER(ctypes.c_int32)]),
+    "tsfa_fwd_set_split_events": (_c_int, [_c_vp, _c_vp]),
+}
+
+_lib = None
+
+
+class TsfaError(RuntimeError):
+    def __init__(self, fn: str, status: int):
+        self.status = status
+        super().__init__(f"{fn} failed: {status_string(status)} (status {status})")
+
+
+def load() -> ctypes.CDLL:
+    """Load libtsfa.so (built by ``tsfa.build``); raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("TSFA_LIB", LIB_PATH))
+    if not path.exists():
+        raise RuntimeError(
+            f"libtsfa.so not found at {path}: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+            "(the HIP path has no CPU fallback)"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def status_string(status: int) -> str:
+    try:
+        return load().tsfa_status_string(status).decode()
+    except Exception:  # pragma: no cover
+        return f"status {status}"
+
+
+def check(fn: str, status: int) -> None:
+    """Map a tsfa status to the reference's exception types."""
+    if status == TSFA_OK:
+        return
+    if status == TSFA_ERR_INVALID_ARGUMENT:
+        raise ValueError(f"{fn}: {status_string(status)}")
+    if status == TSFA_ERR_UNSUPPORTED:
+        raise NotImplementedError(f"{fn}: {status_string(status)}")
+    raise TsfaError(fn, status)
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def i64_array(values):
+    arr = (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+    return arr
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return TSFA_DTYPE_FP16
+    if dtype == torch.bfloat16:
+        return TSFA_DTYPE_BF16
+    raise NotImplementedError(f"dtype {dtype} is not supported by the HIP kernels (fp16/bf16 only)")
+
+
+def fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim) -> dict:
+    out = (ctypes.c_int32 * 6)()
+    check("tsfa_fwd_plan", load().tsfa_fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
+                                                 head_dim, out))
+    keys = ("prefix_splits", "tiles_per_split", "tokens_per_chunk", "row_chunks", "workgroups", "ring_stages")
+    return dict(zip(keys, list(out)))

@@ -1,0 +1,140 @@
+/*
+ * tsfa.h -- C ABI of libtsfa.so, the MI355X (gfx950) tree-sparse attention
+ * library for EAGLE-style speculative-decoding verification.
+ *
+ * Every entry point is extern "C", stateless apart from a per-device cache of
+ * the compute-unit count, takes plain pointers and sizes, enqueues its work on
+ * the caller's stream and returns an int status (TSFA_OK == 0).  Device
+ * pointers must be device memory of the current HIP device.  No entry point
+ * allocates device memory: scratch comes in through `workspace`.
+ *
+ * Reference interfaces replaced (LUOseu/eagle3-tree-sparse-flashattn):
+ *   tsfa_meta_build   prepare_tree_sparse_metadata     tree_sparse_flashattn.py:67-160
+ *   tsfa_pack_bits    _pack_block_mask_to_int32         tree_sparse_flashattn.py:44-64
+ *   tsfa_fwd          block_sparse_tree_fwd_kernel[grid] tree_sparse_flashattn.py:163-339
+ *                     (argument list: tree_sparse_flashattn.py:164-203,
+ *                      call sites eagle_tree_sparse_bridge.py:119-158,
+ *                      benchmark.py:183-194)
+ */
+#ifndef TSFA_H_
+#define TSFA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* tsfa_stream_t; /* a hipStream_t; NULL = default stream */
+
+enum tsfa_status {
+  TSFA_OK = 0,
+  TSFA_ERR_INVALID_ARGUMENT = 1, /* shapes/values the reference rejects (ValueError / assert) */
+  TSFA_ERR_UNSUPPORTED = 2,      /* valid for the reference, outside this build's kernels */
+  TSFA_ERR_WORKSPACE = 3,        /* workspace missing or smaller than *_workspace_bytes() */
+  TSFA_ERR_LAUNCH = 4,           /* the HIP runtime refused a launch */
+  TSFA_ERR_DEVICE = 5            /* no usable HIP device / attribute query failed */
+};
+
+enum tsfa_dtype { TSFA_DTYPE_FP16 = 0, TSFA_DTYPE_BF16 = 1 };
+
+/* Block codes of blk_type (tree_sparse_flashattn.py:11-12). ZERO blocks are absent. */
+enum { TSFA_FULL_BLOCK = 0, TSFA_MIXED_BLOCK = 1 };
+
+int tsfa_version(void);
+const char* tsfa_status_string(int status);
+
+/* ---------------------------------------------------------------- metadata
+ * Builds the CSR + tri-state metadata of `n_seq` tree masks, bit-exact with
+ * prepare_tree_sparse_metadata (tree_sparse_flashattn.py:67-160) applied to
+ * each mask: mask[s][i][j] != 0 means visible (tree_sparse_flashattn.py:90).
+ *
+ * mask      uint8 [n_seq][q_len][q_len], element (s,i,j) at
+ *           s*mask_seq_stride + i*mask_row_stride + j
+ * Outputs use capacity strides so one launch serves every sequence
+ * (nqb = ceil(q_len/block_m), ntb = ceil(q_len/block_n),
+ *  W = ceil(block_m*block_n/32), cap = nqb*ntb):
+ *   row_ptr  int32 [n_seq][nqb+1]
+ *   col_idx  int32 [n_seq][cap]     first nnz[s] valid
+ *   blk_type int8  [n_seq][cap]     first nnz[s] valid
+ *   payload  int32 [n_seq][cap*W]   first n_mixed[s]*W valid
+ *   offset   int32 [n_seq][cap]     first nnz[s] valid; the reference returns
+ *                                   an EMPTY tensor when n_mixed[s] == 0
+ *                                   (tree_sparse_flashattn.py:145-147)
+ *   counts   int32 [n_seq][2]       {nnz, n_mixed}
+ * Errors (tree_sparse_flashattn.py:85-88): block sizes <= 0 or q_len < 0 ->
+ * TSFA_ERR_INVALID_ARGUMENT.
+ */
+int tsfa_meta_check_args(int n_seq, int q_len, int block_m, int block_n);
+size_t tsfa_meta_workspace_bytes(int n_seq, int q_len, int block_m, int block_n);
+int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int64_t mask_row_stride,
+                    int n_seq, int q_len, int block_m, int block_n,
+                    int32_t* row_ptr, int32_t* col_idx, int8_t* blk_type,
+                    int32_t* payload, int32_t* offset, int32_t* counts,
+                    void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
+
+/* Packs n_bits bools (uint8, nonzero = 1) row-major into ceil(n_bits/32)
+ * int32 words, bit i of word w = bits[32w+i] (tree_sparse_flashattn.py:44-64). */
+int tsfa_pack_bits(const uint8_t* bits, int64_t n_bits, int32_t* words, tsfa_stream_t stream);
+
+/* ----------------------------------------------------------------- forward
+ * Tree-sparse attention forward: for every (b, h, t) row,
+ *   O = softmax(Q K^T * sm_scale + mask) V
+ * over keys [0, prefix_len) (dense prefix) and the tree keys
+ * prefix_len + tb*block_n + c (< kv_len) that the CSR row of q-block
+ * t / block_m marks visible (FULL block, or MIXED bit set), with
+ * kv head h / gqa_group_size.  Same semantics as block_sparse_tree_fwd_kernel
+ * (tree_sparse_flashattn.py:163-339) including the -inf/NaN guards: a row
+ * with no visible key yields NaN (0/0), as the reference does.
+ *
+ * q, o      [B, Hq, q_len, D] of `dtype`, last-dim stride 1
+ * k, v      [B, Hkv, kv_len, D] of `dtype`, last-dim stride 1
+ * strides   int64[16]: q(b,h,n,d), k(b,h,n,d), v(b,h,n,d), o(b,h,n,d) in
+ *           elements, the reference's stride arguments in order
+ *           (tree_sparse_flashattn.py:174-189); every d stride must be 1
+ * metadata  row_ptr/col_idx/blk_type/payload/offset as produced by
+ *           prepare_tree_sparse_metadata; meta_seq_stride[5] gives the
+ *           per-batch-element stride (elements) of each of the five arrays:
+ *           all zero = one tree shared by the batch (the reference's protocol),
+ *           non-zero = one tree per sequence (tsfa_meta_build's layout)
+ * o is written in `dtype` (one rounding of the fp32 result; the reference
+ * stores through float16, tree_sparse_flashattn.py:339).
+ * Supported: dtype fp16/bf16, head_dim 64 or 128, block_n a positive
+ * multiple of 16, block_m >= 1, num_heads % num_kv_heads == 0 with
+ * gqa_group_size == num_heads / num_kv_heads <= 256, q_len >= 1,
+ * kv_len >= prefix_len >= 0, 16-byte aligned q/k/v/o rows.
+ */
+int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                        int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size,
+                        int block_m, int block_n, int head_dim, int dtype);
+size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                                int prefix_len, int head_dim);
+int tsfa_fwd(const void* q, const void* k, const void* v, void* o,
+             const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
+             const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+             const int64_t* meta_seq_stride, const int64_t* strides, float sm_scale,
+             int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
+             int n_q_blocks, int n_tree_blocks, int gqa_group_size,
+             int block_m, int block_n, int head_dim, int dtype,
+             void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
+
+/* Work decomposition tsfa_fwd would use (for reports and tests):
+ * out[0] = prefix splits per (batch, kv head, row chunk), out[1] = prefix
+ * tiles (64 keys) per split, out[2] = tokens per row chunk, out[3] = row
+ * chunks, out[4] = workgroups of the main kernel, out[5] = LDS ring stages. */
+int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
+                  int head_dim, int32_t* out6);
+
+/* Measurement hook (no reference counterpart; for benchmarks and profilers):
+ * while set, every tsfa_fwd call on this host thread records `begin`/`end`
+ * (hipEvent_t, created by the caller) on its stream immediately before and
+ * after the main split-KV kernel, so the caller can time that kernel alone.
+ * Pass NULL, NULL to stop. */
+int tsfa_fwd_set_split_events(void* begin, void* end);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSFA_H_ */

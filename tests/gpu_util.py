@@ -1,0 +1,51 @@
+"""Helpers shared by the GPU parity tests (oracle comparison, tolerances)."""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import meta_oracle as mo
+from oracle.attn_oracle import dense_mask_attention
+
+# max_abs_err bars against the fp32 oracle.
+TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3}
+
+
+def assert_meta_equal(meta, ref: mo.OracleMetadata):
+    """Bit-exact comparison of a TreeSparseMetadata with the oracle's record."""
+    for field, dtype in (("row_ptr", torch.int32), ("col_idx", torch.int32), ("blk_type", torch.int8),
+                         ("mixed_mask_payload", torch.int32), ("mixed_mask_offset", torch.int32)):
+        got = getattr(meta, field)
+        assert got.dtype == dtype, (field, got.dtype)
+        exp = getattr(ref, field)
+        np.testing.assert_array_equal(got.cpu().numpy(), exp, err_msg=field)
+        assert tuple(got.shape) == exp.shape, (field, tuple(got.shape), exp.shape)
+    for field in ("n_q_blocks", "n_tree_blocks", "block_m", "block_n", "prefix_len"):
+        assert getattr(meta, field) == getattr(ref, field), field
+
+
+def oracle_out(q, k, v, mask, prefix_len, heads=None, head_chunk=8):
+    """fp32 oracle output; `heads` restricts it to a subset of query heads."""
+    if heads is None:
+        return dense_mask_attention(q, k, v, mask, prefix_len, head_chunk=head_chunk)
+    group = q.shape[1] // k.shape[1]
+    outs = []
+    for h in heads:
+        kv = h // group
+        outs.append(dense_mask_attention(q[:, h:h + 1], k[:, kv:kv + 1], v[:, kv:kv + 1], mask, prefix_len))
+    return torch.cat(outs, dim=1)
+
+
+def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None):
+    got = out.float().cpu()
+    if heads is not None:
+        got = got[:, list(heads)]
+    tol = TOL[dtype] if atol is None else atol
+    nan_got, nan_ref = torch.isnan(got), torch.isnan(ref)
+    assert torch.equal(nan_got, nan_ref), f"NaN pattern differs: got {int(nan_got.sum())}, ref {int(nan_ref.sum())}"
+    diff = (got - ref).abs()
+    diff[nan_ref] = 0
+    err = float(diff.max()) if diff.numel() else 0.0
+    assert err <= tol, f"max_abs_err {err:.3e} > {tol:.1e}"
+    return err

@@ -1,0 +1,80 @@
+"""The C-ABI library loads, exports every declared symbol, and validates
+arguments on the host exactly as the reference rejects them (no GPU work)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from tsfa import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "tsfa.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tsfa_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared()
+    assert set(declared) == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.tsfa_version() >= 1
+    assert lib.tsfa_status_string(0) == b"ok"
+    assert b"invalid" in lib.tsfa_status_string(1)
+
+
+def test_meta_check_args():
+    lib = _lib.load()
+    assert lib.tsfa_meta_check_args(1, 64, 16, 64) == _lib.TSFA_OK
+    assert lib.tsfa_meta_check_args(1, 0, 16, 64) == _lib.TSFA_OK        # empty mask is valid
+    assert lib.tsfa_meta_check_args(1, 64, 0, 64) == _lib.TSFA_ERR_INVALID_ARGUMENT   # :87-88
+    assert lib.tsfa_meta_check_args(1, 64, 16, -2) == _lib.TSFA_ERR_INVALID_ARGUMENT
+    assert lib.tsfa_meta_workspace_bytes(2, 64, 16, 64) > 0
+
+
+FWD_OK = dict(batch=1, num_heads=32, num_kv_heads=8, q_len=64, kv_len=4160, prefix_len=4096, n_q_blocks=4,
+              n_tree_blocks=1, gqa_group_size=4, block_m=16, block_n=64, head_dim=128, dtype=_lib.TSFA_DTYPE_BF16)
+
+
+def _fwd_check(**kw):
+    args = dict(FWD_OK)
+    args.update(kw)
+    return _lib.load().tsfa_fwd_check_args(*args.values())
+
+
+def test_fwd_check_args_ok():
+    assert _fwd_check() == _lib.TSFA_OK
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(block_m=0), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(prefix_len=-1), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(kv_len=100, prefix_len=200), _lib.TSFA_ERR_INVALID_ARGUMENT),   # eagle_tree_sparse_bridge.py:91-93
+    (dict(gqa_group_size=3), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(n_q_blocks=5), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(head_dim=96), _lib.TSFA_ERR_UNSUPPORTED),
+    (dict(block_n=24, n_tree_blocks=3), _lib.TSFA_ERR_UNSUPPORTED),
+    (dict(dtype=7), _lib.TSFA_ERR_UNSUPPORTED),
+])
+def test_fwd_check_args_rejects(kw, status):
+    assert _fwd_check(**kw) == status
+
+
+def test_null_pointers_rejected_before_device_work():
+    lib = _lib.load()
+    strides = (ctypes.c_int64 * 16)(*([1] * 16))
+    ms = (ctypes.c_int64 * 5)()
+    st = lib.tsfa_fwd(None, None, None, None, None, None, None, None, None, ms, strides, ctypes.c_float(0.1),
+                      *list(FWD_OK.values()), None, 0, None)
+    assert st == _lib.TSFA_ERR_INVALID_ARGUMENT
+    assert lib.tsfa_pack_bits(None, -1, None, None) == _lib.TSFA_ERR_INVALID_ARGUMENT
