@@ -88,6 +88,8 @@ def main():
     ap.add_argument("--cold-mib", type=int, default=512, help="K/V bytes cycled through (defeats the MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--split-events", choices=("on", "off"), default="on",
+                    help="record HIP events around the split kernel inside the graph (roofline figure)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -141,8 +143,9 @@ def main():
         torch.cuda.synchronize()
         with torch.cuda.graph(graph, stream=s):
             for i in range(steps):
-                _lib.check("tsfa_fwd_set_split_events",
-                           lib.tsfa_fwd_set_split_events(ev[i][0].cuda_event, ev[i][1].cuda_event))
+                if args.split_events == "on":
+                    _lib.check("tsfa_fwd_set_split_events",
+                               lib.tsfa_fwd_set_split_events(ev[i][0].cuda_event, ev[i][1].cuda_event))
                 call(i)
         _lib.check("tsfa_fwd_set_split_events", lib.tsfa_fwd_set_split_events(None, None))
     torch.cuda.synchronize()
@@ -157,7 +160,7 @@ def main():
     t_end.record()
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_end)
-    split_ms = [b.elapsed_time(e) for b, e in ev]
+    split_ms = [b.elapsed_time(e) for b, e in ev] if args.split_events == "on" else [total_ms / steps]
     split_avg_s = sum(split_ms) / len(split_ms) / 1e3
     per_call_s = total_ms / 1e3 / steps
     _log(f"[bench] {steps} calls in {total_ms:.3f} ms: {per_call_s * 1e6:.2f} us/call, "

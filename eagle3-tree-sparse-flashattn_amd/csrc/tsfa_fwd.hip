@@ -40,12 +40,11 @@
 namespace tsfa {
 namespace fwd {
 
-constexpr int kThreads = 256;
-constexpr int kRowsPerWave = 64;
-constexpr int kRowsPerChunk = 256;
+constexpr int kRowsPerChunk = 256;  // rows of one workgroup (all waves)
 constexpr int kTileKeys = 64;
 constexpr int kMaskBytes = 16384;    // per-token tree visibility words
 constexpr int kMaxTreeTiles = 512;   // tree keys <= 32768
+constexpr int kMiscInts = 320;       // LDS scalars: visited count, row_ptr window of <= 258 q-blocks
 constexpr float kRescaleLog2 = 8.0f;
 
 struct SplitArgs {
@@ -64,8 +63,8 @@ struct SplitArgs {
   int tpc, n_chunks, tiles_per_split, n_ptiles, n_slots, n_items, items_per_xcd;
   int tree_key_limit;  // min(n_tree_blocks*BN, kv_len - prefix_len)
   int vt_max;          // tree tiles per mask batch
-  float* ws_acc;
-  float2* ws_ml;
+  void* ws_o;          // [B*Hkv][n_slots][q_len*G][D] partial O / l in the input dtype
+  float2* ws_ml;       // [B*Hkv][n_slots][q_len*G] (m, l) of each partial
 };
 
 struct CombineArgs {
@@ -73,7 +72,7 @@ struct CombineArgs {
   int64_t sob, soh, som;
   float scale_log2;
   int batch, num_heads, num_kv_heads, group, q_len, n_slots;
-  const float* ws_acc;
+  const void* ws_o;
   const float2* ws_ml;
 };
 
@@ -132,10 +131,31 @@ __device__ inline uint32_t lds_addr(const void* p) {
 
 template <typename V, typename U> __device__ inline V bit_cast(U u) { return __builtin_bit_cast(V, u); }
 
-template <typename T, int D, int NSTAGE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// Max / sum over lanes {l, l^16, l^32, l^48} with the gfx950 row-swap
+// permutes (two VALU ops each, no LDS round trip).
+__device__ inline float row_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float row_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// WAVES waves per workgroup, each owning RT row tiles (16 rows) of the 256-row
+// chunk: WAVES = 8 gives two waves per SIMD (one wave's softmax overlaps the
+// other's MFMAs) at <= 256 registers per lane.
+template <typename T, int D, int NSTAGE, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
+  constexpr int kThreads = WAVES * 64;
+  constexpr int RT = kRowsPerChunk / (WAVES * 16);
+  constexpr int kRowsPerWave = RT * 16;
   constexpr int ROWB = D * 2;
   constexpr int CPR = D / 8;
   constexpr int TILEB = kTileKeys * ROWB;
@@ -149,7 +169,7 @@ void split_kernel(const SplitArgs a) {
   unsigned char* ring = smem;
   uint16_t* masks = reinterpret_cast<uint16_t*>(smem + NSTAGE * STAGEB);
   int* vis = reinterpret_cast<int*>(smem + NSTAGE * STAGEB + kMaskBytes);
-  int* misc = vis + kMaxTreeTiles;
+  int* misc = vis + kMaxTreeTiles;  // kMiscInts ints
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -176,48 +196,10 @@ void split_kernel(const SplitArgs a) {
   const int rows = ntok * G;
   const bool active = wave * kRowsPerWave < rows;
   const float sl2 = a.scale_log2;
+  const float rescale_raw = kRescaleLog2 / sl2;  // re-base the running max past 2^8 growth
 
   const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
-
-  // Q^T fragments: row r = wave*64 + rt*16 + li, d = ks*32 + lg*8 + [0, 8).
-  i16x8 qf[4][KSTEPS];
-  int row_tok[4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    const int r = wave * kRowsPerWave + rt * 16 + li;
-    row_tok[rt] = 0;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[rt][ks] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < rows) {
-      const int tt = r / G;
-      const int g = r - tt * G;
-      row_tok[rt] = tt;
-      const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh +
-                    (int64_t)(t_lo + tt) * a.sqm + lg * 8;
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) qf[rt][ks] = *reinterpret_cast<const i16x8*>(qp + ks * 32);
-    }
-  }
-
-  // Consume the Q loads here: otherwise the compiler waits for them lazily at
-  // their first use inside the tile loop, where its vmcnt count would also
-  // cover (and stall on) the in-flight K/V prefetch it does not know about.
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) asm volatile("" : : "v"(qf[rt][ks]));
-
-  // Running state per lane: rows (rt, li); O^T element d = dt*16 + lg*4 + [0,4).
-  f32x4 o[DTILES][4];
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    m_run[rt] = -INFINITY;
-    l_run[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt) o[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
 
   // HBM -> LDS for tile j (keys key0 .. key0+63) into ring stage j % NSTAGE.
   auto issue = [&](int j, int key0) {
@@ -241,21 +223,69 @@ void split_kernel(const SplitArgs a) {
     }
   };
 
+  // The prefix split's first tile goes out before anything else so the Q
+  // loads below overlap its HBM latency.  The rest of the prologue is issued
+  // after Q is consumed: the compiler waits for Q with vmcnt(0), which would
+  // otherwise also wait for every tile issued before it.
+  const int prefix_tile0 = is_tree ? 0 : slot * a.tiles_per_split;
+  const int prefix_ntl = is_tree ? 0 : min(a.tiles_per_split, a.n_ptiles - prefix_tile0);
+  if (prefix_ntl > 0) issue(0, prefix_tile0 * kTileKeys);
+
+  // Q^T fragments: row r = wave*RT*16 + rt*16 + li, d = ks*32 + lg*8 + [0, 8).
+  i16x8 qf[RT][KSTEPS];
+  int row_tok[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = wave * kRowsPerWave + rt * 16 + li;
+    row_tok[rt] = 0;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) qf[rt][ks] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (r < rows) {
+      const int tt = r / G;
+      const int g = r - tt * G;
+      row_tok[rt] = tt;
+      const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh +
+                    (int64_t)(t_lo + tt) * a.sqm + lg * 8;
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) qf[rt][ks] = *reinterpret_cast<const i16x8*>(qp + ks * 32);
+    }
+  }
+
+  // Consume the Q loads here: otherwise the compiler waits for them lazily at
+  // their first use inside the tile loop, where its vmcnt count would also
+  // cover (and stall on) the in-flight K/V prefetch it does not know about.
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) asm volatile("" : : "v"(qf[rt][ks]));
+  for (int j = 1; j < NSTAGE - 1 && j < prefix_ntl; ++j) issue(j, (prefix_tile0 + j) * kTileKeys);
+
+  // Running state per lane: rows (rt, li); O^T element d = dt*16 + lg*4 + [0,4).
+  f32x4 o[DTILES][RT];
+  float m_run[RT], l_run[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    m_run[rt] = -INFINITY;
+    l_run[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DTILES; ++dt) o[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
   // One 64-key tile for this wave's 64 rows, as two 32-key halves (keeps the
   // live score/probability registers small).  mrow[rt] is the 64-bit key
   // visibility of row tile rt's lane row (read only when `masked`).
-  auto compute = [&](int stage, bool masked, const uint64_t (&mrow)[4]) {
+  auto compute = [&](int stage, bool masked, const uint64_t (&mrow)[RT]) {
     const unsigned char* sk = ring + stage * STAGEB;
     const unsigned char* sv = sk + TILEB;
 #pragma unroll
     for (int hk = 0; hk < 2; ++hk) {
       // S^T sub-tile h: MFMA row li holds key hk*32 + (li/4)*8 + h*4 + li%4, so
       // each lane's 8 scores of this half are 8 consecutive keys.
-      f32x4 s[2][4];
+      f32x4 s[2][RT];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) s[h][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int rt = 0; rt < RT; ++rt) s[h][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
 #pragma unroll
@@ -264,13 +294,13 @@ void split_kernel(const SplitArgs a) {
           const int chunk = ks * 4 + lg;
           const i16x8 kf = *reinterpret_cast<const i16x8*>(sk + key * ROWB + ((chunk ^ swz_k<D>(key)) << 4));
 #pragma unroll
-          for (int rt = 0; rt < 4; ++rt)
+          for (int rt = 0; rt < RT; ++rt)
             s[h][rt] = Mma<T>::run(bit_cast<V8>(kf), bit_cast<V8>(qf[rt][ks]), s[h][rt]);
         }
       }
       if (masked) {
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
           const uint32_t bb = (uint32_t)(mrow[rt] >> (hk * 32 + lg * 8)) & 0xffu;
 #pragma unroll
           for (int h = 0; h < 2; ++h)
@@ -279,21 +309,21 @@ void split_kernel(const SplitArgs a) {
               if (!((bb >> (h * 4 + i)) & 1u)) s[h][rt][i] = -INFINITY;
         }
       }
-      float m_new[4];
+      float m_new[RT];
       bool need = false;
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         float mx = fmaxf(s[0][rt][0], s[1][rt][0]);
 #pragma unroll
         for (int i = 1; i < 4; ++i) mx = fmaxf(mx, fmaxf(s[0][rt][i], s[1][rt][i]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // the row's 64 keys sit in lanes li, li+16, li+32, li+48
+        mx = row_max4(mx);
         m_new[rt] = fmaxf(m_run[rt], mx);
-        need |= (m_new[rt] - m_run[rt]) * sl2 > kRescaleLog2;  // false for -inf/-inf (NaN)
+        need |= m_new[rt] - m_run[rt] > rescale_raw;  // false for -inf/-inf (NaN)
       }
       if (__ballot(need) != 0) {
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
           // alpha = 1 when both are -inf (tree_sparse_flashattn.py:276, :324)
           const float alpha =
               (m_new[rt] == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_run[rt] - m_new[rt]) * sl2);
@@ -303,9 +333,9 @@ void split_kernel(const SplitArgs a) {
           for (int dt = 0; dt < DTILES; ++dt) o[dt][rt] *= alpha;
         }
       }
-      V8 pb[4];
+      V8 pb[RT];
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         // p = 0 where the score is -inf (tree_sparse_flashattn.py:274, :322): with a
         // finite reference point exp2(-inf) = 0; a row with no visible key yet keeps
         // m = -inf and uses reference 0, so every p there is exp2(-inf) = 0 too.
@@ -334,25 +364,24 @@ void split_kernel(const SplitArgs a) {
         const i16x8 vf = i16x8{half[0][0], half[0][1], half[0][2], half[0][3],
                                half[1][0], half[1][1], half[1][2], half[1][3]};
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) o[dt][rt] = Mma<T>::run(bit_cast<V8>(vf), pb[rt], o[dt][rt]);
+        for (int rt = 0; rt < RT; ++rt) o[dt][rt] = Mma<T>::run(bit_cast<V8>(vf), pb[rt], o[dt][rt]);
       }
     }
   };
 
   // Pipeline over ntl tiles: NSTAGE-1 tiles in flight ahead of the one in use.
-  auto run_tiles = [&](int ntl, auto key0_of, auto masked_of, auto mask_of_tile) {
-    for (int j = 0; j < NSTAGE - 1 && j < ntl; ++j) issue(j, key0_of(j));
+  auto run_tiles = [&](int ntl, bool prologue_issued, auto key0_of, auto masked_of, auto mask_of_tile) {
+    if (!prologue_issued)
+      for (int j = 0; j < NSTAGE - 1 && j < ntl; ++j) issue(j, key0_of(j));
     for (int j = 0; j < ntl; ++j) {
       // tile j landed for every wave; stage (j-1)%NSTAGE is free
       sync_tiles<LPT, NSTAGE>(min(ntl - 1 - j, NSTAGE - 2));
       if (j + NSTAGE - 1 < ntl) issue(j + NSTAGE - 1, key0_of(j + NSTAGE - 1));
       if (active) {
         const bool masked = masked_of(j);
-        uint64_t mrow[4] = {~0ull, ~0ull, ~0ull, ~0ull};
-        if (masked) {
+        uint64_t mrow[RT];
 #pragma unroll
-          for (int rt = 0; rt < 4; ++rt) mrow[rt] = mask_of_tile(j, rt);
-        }
+        for (int rt = 0; rt < RT; ++rt) mrow[rt] = masked ? mask_of_tile(j, rt) : ~0ull;
         compute(j % NSTAGE, masked, mrow);
       }
     }
@@ -361,10 +390,9 @@ void split_kernel(const SplitArgs a) {
 
   if (!is_tree) {
     const int P = a.prefix_len;
-    const int tile0 = slot * a.tiles_per_split;
-    const int ntl = min(a.tiles_per_split, a.n_ptiles - tile0);
+    const int tile0 = prefix_tile0;
     run_tiles(
-        ntl, [&](int j) { return (tile0 + j) * kTileKeys; },
+        prefix_ntl, true, [&](int j) { return (tile0 + j) * kTileKeys; },
         [&](int j) { return P - (tile0 + j) * kTileKeys < kTileKeys; },
         [&](int j, int) {
           const int valid = P - (tile0 + j) * kTileKeys;
@@ -379,15 +407,19 @@ void split_kernel(const SplitArgs a) {
     const int32_t* pl = a.payload + b * a.ms_payload;
     const int32_t* of = a.offset + b * a.ms_offset;
     int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
+    int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
+    // Two parallel round trips: the chunk's row_ptr window, then every CSR
+    // entry of those rows at once.
     auto build_state = [&]() {
       for (int i = tid; i < nqbc * ntb; i += kThreads) st[i] = 0;
+      if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
       sync_lds();
-      for (int qq = 0; qq < nqbc; ++qq) {
-        const int e0 = rp[qb_lo + qq], e1 = rp[qb_lo + qq + 1];
-        for (int e = e0 + tid; e < e1; e += kThreads) {
-          const int tb = ci[e];
-          if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
-        }
+      const int e_begin = rps[0], e_end = rps[nqbc];
+      for (int e = e_begin + tid; e < e_end; e += kThreads) {
+        int qq = 0;
+        while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
+        const int tb = ci[e];
+        if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
       }
       sync_lds();
     };
@@ -442,68 +474,111 @@ void split_kernel(const SplitArgs a) {
       }
       sync_lds();
       run_tiles(
-          nb, [&](int j) { return P + vis[vb0 + j] * kTileKeys; }, [&](int) { return true; },
+          nb, false, [&](int j) { return P + vis[vb0 + j] * kTileKeys; }, [&](int) { return true; },
           [&](int j, int rt) -> uint64_t {
-            const int tt = rt == 0 ? row_tok[0] : rt == 1 ? row_tok[1] : rt == 2 ? row_tok[2] : row_tok[3];
+            int tt = row_tok[0];
+#pragma unroll
+            for (int r2 = 1; r2 < RT; ++r2) tt = (rt == r2) ? row_tok[r2] : tt;
             return *reinterpret_cast<const uint64_t*>(masks + (tt * a.vt_max + j) * 4);
           });
     }
   }
 
+  // Epilogue.  Each wave stages its rows' O/l (input dtype) through its own
+  // 8 KB of the (now idle) ring, row-major with a 16-byte-chunk XOR swizzle,
+  // then stores whole rows: every store instruction writes 1 KB contiguous.
   if (!active) return;
   const int64_t TG = (int64_t)a.q_len * G;
   const int64_t base =
       ((int64_t)(b * a.num_kv_heads + kvh) * a.n_slots + slot) * TG + (int64_t)t_lo * G;
+  unsigned char* stage = ring + wave * (kRowsPerWave * ROWB);
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
-    float l = l_run[rt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+  for (int rt = 0; rt < RT; ++rt) {
+    const float l = row_sum4(l_run[rt]);
+    const float inv = l > 0.f ? 1.f / l : 0.f;  // empty partial: O = 0, weight 0 in the combine
     const int r = wave * kRowsPerWave + rt * 16 + li;
-    if (r < rows) {
-      if (lg == 0) a.ws_ml[base + r] = make_float2(m_run[rt], l);
-      float* dst = a.ws_acc + (base + r) * D + lg * 4;
+    if (lg == 0 && r < rows) a.ws_ml[base + r] = make_float2(m_run[rt], l);
+    const int rl = rt * 16 + li;
 #pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) *reinterpret_cast<f32x4*>(dst + dt * 16) = o[dt][rt];
+    for (int dt = 0; dt < DTILES; ++dt) {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      T4 v4;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v4[i] = (T)(o[dt][rt][i] * inv);
+      const int chunk = (dt * 2 + (lg >> 1)) ^ (rl & (CPR - 1));
+      *reinterpret_cast<T4*>(stage + rl * ROWB + chunk * 16 + (lg & 1) * 8) = v4;
     }
+  }
+  T* dst = static_cast<T*>(a.ws_o) + (base + wave * kRowsPerWave) * D;
+  const int wave_rows = min(kRowsPerWave, rows - wave * kRowsPerWave);
+#pragma unroll
+  for (int k = 0; k < kRowsPerWave * CPR / 64; ++k) {
+    const int idx = k * 64 + lane;
+    const int rl = idx / CPR, c = idx % CPR;
+    const i16x8 v = *reinterpret_cast<const i16x8*>(stage + rl * ROWB + ((c ^ (rl & (CPR - 1))) << 4));
+    if (rl < wave_rows) *reinterpret_cast<i16x8*>(dst + (int64_t)rl * D + c * 8) = v;
   }
 }
 
-// Merge the n_slots partials of every row and write O.  8 outputs per thread.
+// Merge the n_slots partials of every row and write O.  Threads walk the
+// workspace rows in order (coalesced 16-byte partial loads); 8 outputs per
+// thread; the slot loop is branch-free (an empty partial has weight 0) so the
+// loads of several slots are in flight together.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
   constexpr int TPR = D / 8;
   const int64_t gtid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gtid / TPR;
-  const int part = (int)(gtid % TPR);
-  const int64_t n_rows = (int64_t)a.batch * a.num_heads * a.q_len;
-  if (row >= n_rows) return;
-  const int t = (int)(row % a.q_len);
-  const int bh = (int)(row / a.q_len);
-  const int h = bh % a.num_heads, b = bh / a.num_heads;
-  const int kvh = h / a.group, g = h - kvh * a.group;
   const int64_t TG = (int64_t)a.q_len * a.group;
-  const int64_t r0 = (int64_t)(b * a.num_kv_heads + kvh) * a.n_slots * TG + (int64_t)t * a.group + g;
+  const int64_t row = gtid / TPR;  // over B*Hkv*TG
+  const int part = (int)(gtid % TPR);
+  if (row >= (int64_t)a.batch * a.num_kv_heads * TG) return;
+  const int64_t bk = row / TG;
+  const int R = (int)(row - bk * TG);
+  const int t = R / a.group, g = R - t * a.group;
+  const int kvh = (int)(bk % a.num_kv_heads), b = (int)(bk / a.num_kv_heads);
+  const int h = kvh * a.group + g;
+  const int64_t r0 = bk * a.n_slots * TG + R;
+  const float2* ml = a.ws_ml + r0;
+  const T* src = static_cast<const T*>(a.ws_o) + r0 * D + part * 8;
+  const int64_t slot_stride = TG * D;
+  typedef T T8 __attribute__((ext_vector_type(8)));
 
-  float mx = -INFINITY;
-  for (int s = 0; s < a.n_slots; ++s) mx = fmaxf(mx, a.ws_ml[r0 + s * TG].x);
-  float l = 0.f;
+  // Running merge in batches of 8 slots: the 8 (m, l) pairs and 8 partial
+  // vectors of a batch are loaded together, then folded into (M, L, acc)
+  // with the same re-basing as the online softmax.
+  float mx = -INFINITY, l = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < a.n_slots; ++s) {
-    const float2 ml = a.ws_ml[r0 + s * TG];
-    if (ml.x == -INFINITY) continue;  // empty partial: weight 0
-    const float w = __builtin_amdgcn_exp2f((ml.x - mx) * a.scale_log2);
-    l += w * ml.y;
-    const f32x4* src = reinterpret_cast<const f32x4*>(a.ws_acc + (r0 + s * TG) * D + part * 8);
-    const f32x4 x0 = src[0], x1 = src[1];
+  for (int s0 = 0; s0 < a.n_slots; s0 += 8) {
+    const int nb = min(8, a.n_slots - s0);
+    float2 v[8];
+    T8 x[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[i] += w * x0[i];
-      acc[4 + i] += w * x1[i];
+    for (int i = 0; i < 8; ++i) {
+      const int s = s0 + min(i, nb - 1);  // duplicates of the last slot get weight 0 below
+      v[i] = ml[s * TG];
+      x[i] = *reinterpret_cast<const T8*>(src + s * slot_stride);
+    }
+    float bm = mx;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bm = (i < nb) ? fmaxf(bm, v[i].x) : bm;
+    if (bm != -INFINITY && bm != mx) {  // re-base the running sums on the new max
+      const float alpha = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mx - bm) * a.scale_log2);
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+      mx = bm;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // weight of partial s: l_s * 2^((m_s - M) * scale); 0 for an empty partial
+      const float w = (i >= nb || v[i].x == -INFINITY) ? 0.f
+                                                      : v[i].y * __builtin_amdgcn_exp2f((v[i].x - mx) * a.scale_log2);
+      l += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += w * (float)x[i][e];
     }
   }
   // l == 0 (no visible key anywhere) gives 0/0 = NaN, as acc / l_i does in the reference.
-  typedef T T8 __attribute__((ext_vector_type(8)));
   T8 out;
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = (T)(acc[i] / l);
@@ -521,7 +596,7 @@ struct Plan {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 size_t lds_bytes_for(int head_dim, int nstage) {
-  return (size_t)nstage * 2 * kTileKeys * head_dim * 2 + kMaskBytes + (kMaxTreeTiles + 16) * 4;
+  return (size_t)nstage * 2 * kTileKeys * head_dim * 2 + kMaskBytes + (kMaxTreeTiles + kMiscInts) * 4;
 }
 
 int env_int(const char* name, int dflt) {
@@ -581,21 +656,23 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   p->vt_max = kMaskBytes / (p->tpc * 8);
   p->tree_key_limit = kv_len - prefix_len;  // refined by the caller with n_tree_blocks*BN
   const size_t rows = (size_t)batch * num_heads * q_len;
-  p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 4);
+  p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 2);
   p->ws_ml_bytes = align256(rows * p->n_slots * 8);
   return TSFA_OK;
 }
 
 template <typename T, int D, int NSTAGE>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
+  constexpr int WAVES = 8;
   static bool attr_set = false;  // benign race: idempotent attribute write
   if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, NSTAGE>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, NSTAGE, WAVES>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set = true;
   }
-  hipLaunchKernelGGL((split_kernel<T, D, NSTAGE>), dim3(p.grid), dim3(kThreads), p.lds_bytes, stream, args);
+  hipLaunchKernelGGL((split_kernel<T, D, NSTAGE, WAVES>), dim3(p.grid), dim3(WAVES * 64), p.lds_bytes, stream,
+                     args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -609,7 +686,7 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   int st = (p.nstage == 4) ? launch_split<T, D, 4>(sa, p, stream) : launch_split<T, D, 2>(sa, p, stream);
   if (st != TSFA_OK) return st;
   if (g_split_end != nullptr && hipEventRecord(g_split_end, stream) != hipSuccess) return TSFA_ERR_LAUNCH;
-  const int64_t threads = (int64_t)ca.batch * ca.num_heads * ca.q_len * (D / 8);
+  const int64_t threads = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group * (D / 8);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, ca);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
@@ -740,7 +817,7 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   sa.items_per_xcd = p.items_per_xcd;
   sa.tree_key_limit = p.tree_key_limit;
   sa.vt_max = p.vt_max;
-  sa.ws_acc = static_cast<float*>(workspace);
+  sa.ws_o = workspace;
   sa.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
 
   CombineArgs ca;
@@ -755,7 +832,7 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   ca.group = gqa_group_size;
   ca.q_len = q_len;
   ca.n_slots = p.n_slots;
-  ca.ws_acc = sa.ws_acc;
+  ca.ws_o = sa.ws_o;
   ca.ws_ml = sa.ws_ml;
 
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);

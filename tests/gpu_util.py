@@ -8,8 +8,14 @@ import torch
 from oracle import meta_oracle as mo
 from oracle.attn_oracle import dense_mask_attention
 
-# max_abs_err bars against the fp32 oracle.
+# max_abs_err bars against the fp32 oracle (the named workloads use these alone).
 TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3}
+# Edge cases with few visible keys have |O| up to ~4, where rounding O once to
+# the output dtype already costs up to 2^-9*|O| (bf16) -- 7.8e-3 at |O| = 3.3,
+# and the reference's own numerics (P rounded to the input dtype before PV,
+# tree_sparse_flashattn.py:278) add as much again.  Those tests allow
+# TOL + REL * |ref| with REL = 4 ulp of the output dtype.
+REL = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -9}
 
 
 def assert_meta_equal(meta, ref: mo.OracleMetadata):
@@ -37,7 +43,8 @@ def oracle_out(q, k, v, mask, prefix_len, heads=None, head_chunk=8):
     return torch.cat(outs, dim=1)
 
 
-def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None):
+def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None, relative=False):
+    """max |out - ref| <= TOL[dtype] (+ REL[dtype]*|ref| when `relative`); NaN where ref is NaN."""
     got = out.float().cpu()
     if heads is not None:
         got = got[:, list(heads)]
@@ -47,5 +54,10 @@ def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None):
     diff = (got - ref).abs()
     diff[nan_ref] = 0
     err = float(diff.max()) if diff.numel() else 0.0
-    assert err <= tol, f"max_abs_err {err:.3e} > {tol:.1e}"
+    if relative:
+        bound = tol + REL[dtype] * ref.abs().nan_to_num(0.0)
+        excess = float((diff - bound).max()) if diff.numel() else 0.0
+        assert excess <= 0, f"max_abs_err {err:.3e} exceeds {tol:.1e} + {REL[dtype]:.1e}*|ref|"
+    else:
+        assert err <= tol, f"max_abs_err {err:.3e} > {tol:.1e}"
     return err

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from tsfa import configs, trees
-from tests.gpu_util import TOL, assert_close_to_oracle, oracle_out
+from tests.gpu_util import REL, TOL, assert_close_to_oracle, oracle_out
 
 pytestmark = pytest.mark.gpu
 
@@ -91,7 +91,8 @@ def test_cases(case):
     q, k, v = _qkv(b, hq, hkv, t, p, d, dtype, seed=t + p)
     out = _run(q, k, v, mask, bm, bn)
     torch.cuda.synchronize()
-    assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype)
+    # short prefixes leave rows with few keys and |O| ~ 1-4: relative bar (gpu_util.REL)
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -102,7 +103,7 @@ def test_per_sequence_trees(dtype):
     q, k, v = _qkv(b, hq, hkv, t, p, d, dtype)
     out = _run(q, k, v, masks, 16, 32)
     torch.cuda.synchronize()
-    assert_close_to_oracle(out, oracle_out(q, k, v, masks, p), dtype)
+    assert_close_to_oracle(out, oracle_out(q, k, v, masks, p), dtype, relative=True)
 
 
 def test_all_full_blocks_no_offsets():
@@ -180,3 +181,4 @@ def test_unsupported_dtype_raises(dtype):
 
 def test_tolerances_declared():
     assert TOL[torch.bfloat16] == 8e-3 and TOL[torch.float16] == 2e-3
+    assert REL[torch.bfloat16] == 2.0 ** -7 and REL[torch.float16] == 2.0 ** -9
