@@ -10,25 +10,31 @@
 // Work decomposition (the MI355X design, not the reference's grid):
 //   * rows of one (batch, kv head) are packed token-major, r = t*G + g, so the
 //     G query heads that share a K/V head share every K/V byte staged in LDS;
-//     a workgroup owns a chunk of <= 256 rows (tokens_per_chunk * G);
-//   * the prefix is split into runs of 64-key tiles; each (b, kvh, chunk,
-//     split) is one workgroup, so a small tree still spreads the prefix over
-//     all 256 CUs (split-KV);
-//   * one more workgroup per (b, kvh, chunk) runs the tree part: it expands
-//     the CSR rows of the chunk's q-blocks into per-token 64-bit visibility
-//     words for every 64-key tree tile that holds a visible key, and skips
-//     the rest (ZERO blocks are never loaded);
-//   * every workgroup writes an fp32 partial (m, l, acc) per row; a second
-//     kernel merges the partials (log-sum-exp) and writes O in the input
-//     dtype.
-// Inside a workgroup: 4 waves x 64 rows; K/V tiles of 64 keys go HBM -> LDS
-// with global_load_lds (16 B per lane, no VGPR staging) into a ring of
-// NSTAGE stages; S^T = K Q^T and O^T += V^T P^T run on
-// v_mfma_f32_16x16x32_{bf16,f16}; V^T operands come from ds_read_b64_tr_b16,
-// so V is never transposed in memory.  Scores stay in registers; exp2 with
-// sm_scale*log2(e) folded into one FMA.  The running max is only re-based
-// when it grows by more than 2^8 (rescaling is exact for any consistent
-// reference point), which skips the O rescale on almost every tile.
+//     a workgroup owns a chunk of 128 consecutive rows;
+//   * keys move in units of 32.  The prefix units are cut into runs (split-KV:
+//     a small tree still spreads the prefix over all 256 CUs) and one more
+//     workgroup per chunk runs the tree units: it expands the CSR rows of the
+//     chunk's q-blocks into per-token 32-bit visibility words for every tree
+//     unit that holds a visible key, and skips the rest (ZERO blocks are never
+//     loaded);
+//   * a workgroup is 8 waves, two per SIMD: two key streams x four row groups
+//     of 32 rows.  Stream s takes every other unit of the workgroup's run
+//     through its own LDS ring, filled by global_load_lds (HBM -> LDS, 16 B
+//     per lane, no VGPR staging) with the stream's four waves moving a
+//     quarter each; one barrier per step.  The two waves sharing a SIMD
+//     belong to different streams, so one's softmax overlaps the other's
+//     MFMAs;
+//   * S^T = K Q^T and O^T += V^T P^T run on v_mfma_f32_32x32x16_{bf16,f16}:
+//     a lane holds one query row in both, so the softmax statistics and the
+//     rescale of O never leave the lane; V^T operands come from
+//     ds_read_b64_tr_b16, so V is never transposed in memory.  exp2 with
+//     sm_scale*log2(e) folded into one FMA; the running max is only re-based
+//     when a score exceeds it by more than 2^8 (rescaling is exact for any
+//     consistent reference point), which skips the O rescale on almost every
+//     unit;
+//   * at the end the two streams' (m, l, O) merge in LDS and the workgroup writes
+//     one partial per row (O/l in the input dtype, fp32 (m, l)); a second
+//     kernel merges the partials (log-sum-exp) and writes O.
 
 #include <math.h>
 #include <stdlib.h>
@@ -40,11 +46,15 @@
 namespace tsfa {
 namespace fwd {
 
-constexpr int kRowsPerChunk = 256;  // rows of one workgroup (all waves)
-constexpr int kTileKeys = 64;
-constexpr int kMaskBytes = 16384;    // per-token tree visibility words
-constexpr int kMaxTreeTiles = 512;   // tree keys <= 32768
-constexpr int kMiscInts = 320;       // LDS scalars: visited count, row_ptr window of <= 258 q-blocks
+constexpr int kWaves = 8;
+constexpr int kStreams = 2;
+constexpr int kRowGroups = kWaves / kStreams;  // 32 rows each
+constexpr int kUnitKeys = 32;
+constexpr int kRows = 32 * kRowGroups;  // rows per chunk (workgroup)
+constexpr int kRingBytes = 131072;   // K/V rings of the streams; the merge buffer at the end
+constexpr int kMaskWords = 4096;     // per-token 32-bit visibility words of tree units
+constexpr int kMaxTreeUnits = 1024;  // tree keys <= 32768
+constexpr int kMiscInts = 320;       // LDS scalars: visible-unit count, row_ptr window
 constexpr float kRescaleLog2 = 8.0f;
 
 struct SplitArgs {
@@ -58,11 +68,12 @@ struct SplitArgs {
   const int32_t* offset;
   int64_t ms_row_ptr, ms_col_idx, ms_blk_type, ms_payload, ms_offset;
   int64_t sqb, sqh, sqm, skb, skh, skn, svb, svh, svn;
-  float scale_log2;  // sm_scale * log2(e)
+  float scale_log2;  // |sm_scale| * log2(e), never 0
+  int neg_q;         // sm_scale < 0: Q enters negated (scores keep their sign)
   int num_kv_heads, group, q_len, kv_len, prefix_len, block_m, block_n, n_tree_blocks;
-  int tpc, n_chunks, tiles_per_split, n_ptiles, n_slots, n_items, items_per_xcd;
+  int n_chunks, units_per_split, n_pu, n_slots, n_items, items_per_xcd;
   int tree_key_limit;  // min(n_tree_blocks*BN, kv_len - prefix_len)
-  int vt_max;          // tree tiles per mask batch
+  int vt_max;          // tree units per mask batch
   void* ws_o;          // [B*Hkv][n_slots][q_len*G][D] partial O / l in the input dtype
   float2* ws_ml;       // [B*Hkv][n_slots][q_len*G] (m, l) of each partial
 };
@@ -76,22 +87,19 @@ struct CombineArgs {
   const float2* ws_ml;
 };
 
-// 16-byte-chunk XOR swizzles of the K and V LDS tiles (row = key in tile).
-// K: the 16 keys one MFMA A-operand read touches land on 16 distinct bank
-// groups.  V: the 4 keys x 32 bytes of a ds_read_b64_tr_b16 group, and the
-// neighbouring group, land on distinct bank groups.
-template <int D> __device__ inline int swz_k(int key);
-template <> __device__ inline int swz_k<128>(int key) { return (key & 3) | ((key >> 1) & 12); }
-template <> __device__ inline int swz_k<64>(int key) { return ((key >> 1) & 1) | ((key >> 2) & 6); }
-template <int D> __device__ inline int swz_v(int key);
-template <> __device__ inline int swz_v<128>(int key) { return ((key & 3) << 1) | (((key >> 3) & 1) << 3); }
-template <> __device__ inline int swz_v<64>(int key) { return (((key >> 1) & 1) << 1) | (((key >> 3) & 1) << 2); }
+// 16-byte-chunk XOR swizzles of the K and V LDS tiles (row = key in unit).
+// K: the 16 keys of one quarter-wave of an MFMA A-operand read land on 16
+// distinct bank groups.  V: the 4 keys x 64 bytes a half-wave of
+// ds_read_b64_tr_b16 touches land on 4 distinct 64-byte bank windows.
+template <int D> __device__ inline int swz_k(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
+template <int D> __device__ inline int swz_v(int key) { return D == 128 ? ((key & 3) << 2) : (((key >> 1) & 1) << 2); }
 
 // 16 bytes per lane HBM -> LDS (global_load_lds_dwordx4): lane i's bytes land
 // at LDS address lds_base + 16*i.  Issued as inline asm so the compiler does
 // not treat every later LDS read as aliasing the in-flight copy (it would
 // insert vmcnt(0) before them and serialise the prefetch); completion is
-// ordered explicitly by sync_tiles().
+// ordered explicitly by wait_units().  dma16_s takes a scalar base and a
+// 32-bit lane offset (no per-lane 64-bit address arithmetic).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; the clobber documents the write
 __device__ inline void dma16(const void* src, uint32_t lds_base) {
@@ -100,307 +108,354 @@ __device__ inline void dma16(const void* src, uint32_t lds_base) {
                : "v"(src), "s"(lds_base)
                : "memory", "m0");
 }
+__device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
-// Wait until at most N of this wave's vector-memory loads are in flight, then
-// workgroup barrier (LDS writes of every wave complete and visible).
-template <int N> __device__ inline void sync_vm() {
+template <int N> __device__ inline void vm_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
-// sync_vm with at most `tiles` ring tiles (LPT loads each) still in flight.
-template <int LPT, int NSTAGE> __device__ inline void sync_tiles(int tiles) {
-  if constexpr (NSTAGE >= 4) {
-    if (tiles >= 2) { sync_vm<2 * LPT>(); return; }
+// Wait until at most k units (LPU loads each) of this wave are in flight.
+template <int LPU, int K> __device__ inline void wait_units(int k) {
+  if constexpr (K == 0) {
+    vm_wait<0>();
+  } else {
+    if (k >= K) {
+      vm_wait<K * LPU>();
+      return;
+    }
+    wait_units<LPU, K - 1>(k);
   }
-  if constexpr (NSTAGE >= 3) {
-    if (tiles >= 1) { sync_vm<LPT>(); return; }
-  }
-  sync_vm<0>();
 }
 
+__device__ inline void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // Workgroup barrier that also orders LDS accesses (compiler and hardware).
-__device__ inline void sync_lds() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
+__device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ inline void sync_all() { asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__device__ inline uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const TSFA_LDS void*)p;
-}
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const TSFA_LDS void*)p; }
 
 template <typename V, typename U> __device__ inline V bit_cast(U u) { return __builtin_bit_cast(V, u); }
 
-// Max / sum over lanes {l, l^16, l^32, l^48} with the gfx950 row-swap
-// permutes (two VALU ops each, no LDS round trip).
-__device__ inline float row_max4(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+// Max / sum over lanes {l, l^32} (one gfx950 row-swap permute, no LDS).
+__device__ inline float pair_max(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
-__device__ inline float row_sum4(float x) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+__device__ inline float pair_sum(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
-// WAVES waves per workgroup, each owning RT row tiles (16 rows) of the 256-row
-// chunk: WAVES = 8 gives two waves per SIMD (one wave's softmax overlaps the
-// other's MFMAs) at <= 256 registers per lane.
-template <typename T, int D, int NSTAGE, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(WAVES / 4, WAVES / 4)))
+// Loads [u_lo, u_lo + NL) of one half (K or V) of a 32-key unit, HBM -> LDS.
+// Load u covers 1 KB of the row-major tile (RPL key rows); 16-byte chunk pos
+// of key row `row` comes from chunk pos ^ swz(row) of the source row (the
+// reader applies the same XOR).
+// Fast path: the lane offset depends on u only through the swizzle, which
+// repeats every NOFF loads, so NOFF precomputed lane offsets and a scalar row
+// base per load address everything.  Slow path (a unit reaching past kv_len):
+// per-lane clamped rows; those keys are masked.
+template <typename T, int D, bool IS_V, int NL>
+__device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst, int key0, int kv_len, int lane,
+                                int u_lo, const uint32_t* loff) {
+  constexpr int CPR = D / 8;
+  constexpr int RPL = 64 / CPR;
+  constexpr int NOFF = IS_V ? 1 : (D == 128 ? 4 : 2);
+  if (key0 + kUnitKeys <= kv_len) {
+    const char* rowp = reinterpret_cast<const char*>(base + (int64_t)(key0 + u_lo * RPL) * stride);
+    const int64_t step = (int64_t)RPL * stride * 2;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int u = u_lo + i;
+      dma16_s(rowp, loff[u % NOFF], lds_dst + u * 1024);
+      rowp += step;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int u = u_lo + i;
+      const int row = u * RPL + lane / CPR, pos = lane % CPR;
+      const int key = min(key0 + row, kv_len - 1);
+      const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
+      dma16(base + (int64_t)key * stride + ((pos ^ sw) << 3), lds_dst + u * 1024);
+    }
+  }
+}
+
+// Lane offsets (bytes from the load's first key row) of dma_half's fast path.
+template <int D, bool IS_V> __device__ inline uint32_t dma_lane_off(int u, int64_t stride, int lane) {
+  constexpr int CPR = D / 8;
+  constexpr int RPL = 64 / CPR;
+  const int lr = lane / CPR, pos = lane % CPR;
+  const int sw = IS_V ? swz_v<D>(u * RPL + lr) : swz_k<D>(u * RPL + lr);
+  return (uint32_t)(lr * stride * 2 + ((pos ^ sw) << 4));
+}
+
+template <int D> constexpr size_t lds_bytes_for() {
+  return (size_t)kRingBytes + kMaskWords * 4 + (kMaxTreeUnits + kMiscInts) * 4;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
-  constexpr int kThreads = WAVES * 64;
-  constexpr int RT = kRowsPerChunk / (WAVES * 16);
-  constexpr int kRowsPerWave = RT * 16;
-  constexpr int ROWB = D * 2;
-  constexpr int CPR = D / 8;
-  constexpr int TILEB = kTileKeys * ROWB;
-  constexpr int STAGEB = 2 * TILEB;
-  constexpr int KLOADS = TILEB / (kThreads * 16);
-  constexpr int LPT = 2 * KLOADS;
-  constexpr int KSTEPS = D / 32;
-  constexpr int DTILES = D / 16;
+  constexpr int ROWB = D * 2;                // bytes of one key row
+  constexpr int HALF = kUnitKeys * ROWB;     // K (or V) bytes of one unit
+  constexpr int SB = 2 * HALF;               // ring stage
+  constexpr int RB = kRingBytes / kStreams;  // ring of one stream
+  constexpr int NS = RB / SB;                // stages per stream
+  constexpr int LPH = HALF / 1024;           // 1 KB loads per half
+  constexpr int LPU = 2 * LPH / kRowGroups;  // loads per unit per wave
+  constexpr int KSTEPS = D / 16;
+  constexpr int DT = D / 32;
+  static_assert(NS >= 2 && (NS & (NS - 1)) == 0 && LPU * (NS - 2) < 64 && LPH % 2 == 0, "ring geometry");
+  static_assert(kWaves * DT * 64 * 64 <= kRingBytes, "merge buffer");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   unsigned char* ring = smem;
-  uint16_t* masks = reinterpret_cast<uint16_t*>(smem + NSTAGE * STAGEB);
-  int* vis = reinterpret_cast<int*>(smem + NSTAGE * STAGEB + kMaskBytes);
-  int* misc = vis + kMaxTreeTiles;  // kMiscInts ints
+  uint32_t* masks = reinterpret_cast<uint32_t*>(smem + kRingBytes);
+  int* vis = reinterpret_cast<int*>(masks + kMaskWords);
+  int* misc = vis + kMaxTreeUnits;  // kMiscInts ints
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int li = lane & 15, lg = lane >> 4;
+  const int rg = wave & (kRowGroups - 1), ks = wave / kRowGroups;  // SIMD rg holds both streams
+  const int ln = lane & 31, lh = lane >> 5;
 
-  // XCD-aware item order: consecutive block ids go to different XCDs, so map
-  // each XCD to a contiguous range of items (items sharing K/V stay together).
-  const int bid = blockIdx.x;
-  const int item = (bid & 7) * a.items_per_xcd + (bid >> 3);
+  // XCD-aware item order: consecutive block ids go to different XCDs, so each
+  // XCD gets a contiguous range of items; items are ordered chunk-fastest, so
+  // the chunks that read the same K/V units share an XCD's L2.
+  const int item = (blockIdx.x & 7) * a.items_per_xcd + (blockIdx.x >> 3);
   if (item >= a.n_items) return;
-  const int slot = item % a.n_slots;
-  int rest = item / a.n_slots;
-  const int chunk = rest % a.n_chunks;
-  rest /= a.n_chunks;
-  const int kvh = rest % a.num_kv_heads;
-  const int b = rest / a.num_kv_heads;
+  const int chunk = item % a.n_chunks;
+  int rest = item / a.n_chunks;
+  const int slot = rest % a.n_slots;
+  const int bk = rest / a.n_slots;
+  const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
   const bool is_tree = slot == a.n_slots - 1;
 
   const int G = a.group;
-  const int t_lo = chunk * a.tpc;
-  const int t_hi = min(t_lo + a.tpc, a.q_len);
-  const int ntok = t_hi - t_lo;
-  const int rows = ntok * G;
-  const bool active = wave * kRowsPerWave < rows;
+  const int TG = a.q_len * G;
+  const int row0 = chunk * kRows;
+  const int rows_chunk = min(kRows, TG - row0);
+  const bool active = rg * 32 < rows_chunk;
+  const int tok_lo = row0 / G;
   const float sl2 = a.scale_log2;
-  const float rescale_raw = kRescaleLog2 / sl2;  // re-base the running max past 2^8 growth
+  const float thr_raw = kRescaleLog2 / sl2;  // re-base the running max past 2^8 growth
 
   const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  unsigned char* sring = ring + ks * RB;
+  const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
 
-  // HBM -> LDS for tile j (keys key0 .. key0+63) into ring stage j % NSTAGE.
-  auto issue = [&](int j, int key0) {
-    unsigned char* sk = ring + (j % NSTAGE) * STAGEB;
-    unsigned char* sv = sk + TILEB;
+  // The stream's four waves move a quarter of each unit: row groups 0-1 the
+  // two halves of K, 2-3 the two halves of V.
+  const bool dma_v = rg >= 2;
+  const int dma_u0 = (rg & 1) * (LPH / 2);
+  uint32_t loff[D == 128 ? 4 : 2];
 #pragma unroll
-    for (int u = 0; u < KLOADS; ++u) {
-      const int sidx = (wave * KLOADS + u) * 64 + lane;
-      const int row = sidx / CPR, pos = sidx % CPR;
-      const int key = min(key0 + row, a.kv_len - 1);
-      const T* src = kbase + (int64_t)key * a.skn + ((pos ^ swz_k<D>(row)) * 8);
-      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(sk + (wave * KLOADS + u) * 1024)));
-    }
-#pragma unroll
-    for (int u = 0; u < KLOADS; ++u) {
-      const int sidx = (wave * KLOADS + u) * 64 + lane;
-      const int row = sidx / CPR, pos = sidx % CPR;
-      const int key = min(key0 + row, a.kv_len - 1);
-      const T* src = vbase + (int64_t)key * a.svn + ((pos ^ swz_v<D>(row)) * 8);
-      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(sv + (wave * KLOADS + u) * 1024)));
-    }
+  for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
+    loff[u] = dma_v ? dma_lane_off<D, true>(u, a.svn, lane) : dma_lane_off<D, false>(u, a.skn, lane);
+
+  // HBM -> LDS: this wave's quarter of one unit (keys key0 .. key0+31) into
+  // stage st of its stream's ring.
+  auto issue = [&](int st, int key0) {
+    const uint32_t sb = sring_lds + st * SB;
+    if (dma_v)
+      dma_half<T, D, true, LPU>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
+    else
+      dma_half<T, D, false, LPU>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
   };
 
-  // The prefix split's first tile goes out before anything else so the Q
-  // loads below overlap its HBM latency.  The rest of the prologue is issued
-  // after Q is consumed: the compiler waits for Q with vmcnt(0), which would
-  // otherwise also wait for every tile issued before it.
-  const int prefix_tile0 = is_tree ? 0 : slot * a.tiles_per_split;
-  const int prefix_ntl = is_tree ? 0 : min(a.tiles_per_split, a.n_ptiles - prefix_tile0);
-  if (prefix_ntl > 0) issue(0, prefix_tile0 * kTileKeys);
-
-  // Q^T fragments: row r = wave*RT*16 + rt*16 + li, d = ks*32 + lg*8 + [0, 8).
-  i16x8 qf[RT][KSTEPS];
-  int row_tok[RT];
+  // Q^T operand fragments of the wave's row tile: row r = row0 + rg*32 + ln,
+  // d = kk*16 + lh*8 + [0, 8); Q is negated for a negative scale.
+  i16x8 qf[KSTEPS];
+  const int qrow = row0 + rg * 32 + ln;
+  const int row_tt = qrow < TG ? qrow / G - tok_lo : 0;  // token of the lane's row, chunk-relative
+  const short qsgn = a.neg_q ? (short)0x8000 : (short)0;
+  // Q straight into registers (rows past the end load zeros).
+  auto load_q = [&]() {
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int r = wave * kRowsPerWave + rt * 16 + li;
-    row_tok[rt] = 0;
+    for (int kk = 0; kk < KSTEPS; ++kk) qf[kk] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+    if (qrow < TG) {
+      const int t = qrow / G;
+      const int g = qrow - t * G;
+      const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
+                    lh * 8;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) qf[rt][ks] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-    if (r < rows) {
-      const int tt = r / G;
-      const int g = r - tt * G;
-      row_tok[rt] = tt;
-      const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh +
-                    (int64_t)(t_lo + tt) * a.sqm + lg * 8;
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) qf[rt][ks] = *reinterpret_cast<const i16x8*>(qp + ks * 32);
+      for (int kk = 0; kk < KSTEPS; ++kk) qf[kk] = *reinterpret_cast<const i16x8*>(qp + kk * 16) ^ qsgn;
     }
+    // Consume the Q loads here: otherwise the compiler waits for them lazily
+    // at their first use inside the unit loop, where its vmcnt count would
+    // also cover (and stall on) the in-flight K/V prefetch it does not know of.
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(qf[kk]));
+  };
+  // Q through LDS instead: the chunk's rows go HBM -> LDS into the last ring
+  // stage of the stream whose row groups use them (rows 64*s .. 64*s+63 of
+  // the chunk in stream s), as global_load_lds issued ahead of the first K/V
+  // units, so the prologue need not wait for Q before filling the ring.
+  // Rows past the end repeat the last row (their outputs are never stored).
+  auto issue_q = [&]() {
+    constexpr int RPL = 1024 / ROWB, CPR = D / 8;
+    constexpr int QL = kRows / RPL / kWaves;  // 1 KB loads per wave
+#pragma unroll
+    for (int i = 0; i < QL; ++i) {
+      const int l0 = (wave * QL + i) * RPL;  // first chunk row of the load
+      const int row = l0 + lane / CPR, pos = lane % CPR, tr = row & 63;
+      const int R = min(row0 + row, TG - 1);
+      const int t = R / G;
+      const int g = R - t * G;
+      const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
+                     ((pos ^ swz_k<D>(tr)) << 3);
+      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(ring + (l0 >> 6) * RB + (NS - 1) * SB + (l0 & 63) * ROWB)));
+    }
+  };
+  auto read_q = [&]() {
+    const unsigned char* qs = ring + (rg >> 1) * RB + (NS - 1) * SB + ((rg & 1) * 32) * ROWB;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk)
+      qf[kk] = *reinterpret_cast<const i16x8*>(qs + ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4)) ^ qsgn;
+  };
+
+  // Running state per lane (query row ln of the row tile): O^T element i of
+  // d-tile dt is d = dt*32 + 8*(i/4) + 4*lh + i%4.  l_run is this lane's half
+  // of the row sum (keys 4*lh + [0,4) of every 8).
+  f32x16 o[DT];
+  float m_run = -INFINITY, m_lim = -INFINITY, mb = 0.f, l_run = 0.f;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+
+  // LDS byte offsets of this lane's operand reads (the chunk XOR does not
+  // commute with the d offset, so one per d-tile / k-step; loop invariant).
+  // V^T: 16-lane group x = (h, d-half); lane i of the group reads 8 bytes of
+  // key row 4*h + i/4 (+16*s2 + 8*jj, which keeps the swizzle) at d = dt*32 +
+  // 16*(x&1) + 4*(i%4); the transpose read hands lane i keys +[0,4) of d = i.
+  // K: lane (ln, lh) reads 16 bytes of key row ln at d = kk*16 + 8*lh.
+  const int vx = lane >> 4, vi = lane & 15;
+  const int vkey = 4 * (vx >> 1) + (vi >> 2);
+  int v_off[DT], k_off[KSTEPS];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
+    v_off[dt] = vkey * ROWB + (((d >> 3) ^ swz_v<D>(vkey)) << 4) + ((d & 7) << 1);
   }
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) k_off[kk] = ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4);
 
-  // Consume the Q loads here: otherwise the compiler waits for them lazily at
-  // their first use inside the tile loop, where its vmcnt count would also
-  // cover (and stall on) the in-flight K/V prefetch it does not know about.
+  // One 32-key unit for the wave's 32 rows.  S^T row (MFMA m) = key, column =
+  // query row: lane (ln, lh) holds keys 8*(i/4) + 4*lh + i%4 of row ln.  mw is
+  // the 32-bit key visibility of the lane's row (read only when `masked`).
+  auto compute = [&](const unsigned char* sk, bool masked, uint32_t mw) {
+    const unsigned char* sv = sk + HALF;
+    f32x16 s;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) asm volatile("" : : "v"(qf[rt][ks]));
-  for (int j = 1; j < NSTAGE - 1 && j < prefix_ntl; ++j) issue(j, (prefix_tile0 + j) * kTileKeys);
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const i16x8 kf = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
+      s = Mma<T>::run(bit_cast<V8>(kf), bit_cast<V8>(qf[kk]), s);
+    }
+    if (masked) {
+      const uint32_t w = mw >> (4 * lh);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (!((w >> (8 * (i >> 2) + (i & 3))) & 1u)) s[i] = -INFINITY;
+    }
+    float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    if (__ballot(mx > m_lim) != 0) {  // false while both are -inf
+      const float m_new = fmaxf(m_run, pair_max(mx));
+      // alpha = 1 when both are -inf (tree_sparse_flashattn.py:276, :324)
+      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sl2);
+      m_run = m_new;
+      mb = (m_new == -INFINITY) ? 0.f : m_new * sl2;
+      m_lim = m_new + thr_raw;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+    // p = 0 where the score is -inf (tree_sparse_flashattn.py:274, :322): with a
+    // finite reference point exp2(-inf) = 0; a row with no visible key yet keeps
+    // m = -inf and reference 0, so every p there is exp2(-inf) = 0 too.
+    V8 pb[2];
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -mb));
+      ls += p;
+      pb[i >> 3][i & 7] = (T)p;  // P rounded to the input dtype (:278)
+    }
+    l_run += ls;
+    // O^T += V^T P^T; k-step s2 covers keys 16*s2 + 8*jj + 4*lh + [0,4), the
+    // order P^T's lane holds them in (elements 8*s2 .. 8*s2+7 of S^T).
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const unsigned char* vp = sv + v_off[dt] + (16 * s2) * ROWB;
+        const i16x4 h0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(vp));
+        const i16x4 h1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(vp + 8 * ROWB));
+        const i16x8 vf = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+        o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
+      }
+  };
 
-  // Running state per lane: rows (rt, li); O^T element d = dt*16 + lg*4 + [0,4).
-  f32x4 o[DTILES][RT];
-  float m_run[RT], l_run[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    m_run[rt] = -INFINITY;
-    l_run[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt) o[dt][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  // One 64-key tile for this wave's 64 rows, as two 32-key halves (keeps the
-  // live score/probability registers small).  mrow[rt] is the 64-bit key
-  // visibility of row tile rt's lane row (read only when `masked`).
-  auto compute = [&](int stage, bool masked, const uint64_t (&mrow)[RT]) {
-    const unsigned char* sk = ring + stage * STAGEB;
-    const unsigned char* sv = sk + TILEB;
-#pragma unroll
-    for (int hk = 0; hk < 2; ++hk) {
-      // S^T sub-tile h: MFMA row li holds key hk*32 + (li/4)*8 + h*4 + li%4, so
-      // each lane's 8 scores of this half are 8 consecutive keys.
-      f32x4 s[2][RT];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) s[h][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int key = hk * 32 + (li >> 2) * 8 + h * 4 + (li & 3);
-          const int chunk = ks * 4 + lg;
-          const i16x8 kf = *reinterpret_cast<const i16x8*>(sk + key * ROWB + ((chunk ^ swz_k<D>(key)) << 4));
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt)
-            s[h][rt] = Mma<T>::run(bit_cast<V8>(kf), bit_cast<V8>(qf[rt][ks]), s[h][rt]);
-        }
-      }
-      if (masked) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const uint32_t bb = (uint32_t)(mrow[rt] >> (hk * 32 + lg * 8)) & 0xffu;
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              if (!((bb >> (h * 4 + i)) & 1u)) s[h][rt][i] = -INFINITY;
-        }
-      }
-      float m_new[RT];
-      bool need = false;
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        float mx = fmaxf(s[0][rt][0], s[1][rt][0]);
-#pragma unroll
-        for (int i = 1; i < 4; ++i) mx = fmaxf(mx, fmaxf(s[0][rt][i], s[1][rt][i]));
-        // the row's 64 keys sit in lanes li, li+16, li+32, li+48
-        mx = row_max4(mx);
-        m_new[rt] = fmaxf(m_run[rt], mx);
-        need |= m_new[rt] - m_run[rt] > rescale_raw;  // false for -inf/-inf (NaN)
-      }
-      if (__ballot(need) != 0) {
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          // alpha = 1 when both are -inf (tree_sparse_flashattn.py:276, :324)
-          const float alpha =
-              (m_new[rt] == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_run[rt] - m_new[rt]) * sl2);
-          m_run[rt] = m_new[rt];
-          l_run[rt] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < DTILES; ++dt) o[dt][rt] *= alpha;
-        }
-      }
-      V8 pb[RT];
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        // p = 0 where the score is -inf (tree_sparse_flashattn.py:274, :322): with a
-        // finite reference point exp2(-inf) = 0; a row with no visible key yet keeps
-        // m = -inf and uses reference 0, so every p there is exp2(-inf) = 0 too.
-        const float mb = (m_run[rt] == -INFINITY) ? 0.f : m_run[rt] * sl2;
-        float lsum = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[h][rt][i], sl2, -mb));
-            lsum += p;
-            pb[rt][h * 4 + i] = (T)p;  // P rounded to the input dtype (:278)
-          }
-        l_run[rt] += lsum;
-      }
-#pragma unroll
-      for (int dt = 0; dt < DTILES; ++dt) {
-        i16x4 half[2];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int key = hk * 32 + lg * 8 + hh * 4 + (li >> 2);
-          const int d = dt * 16 + 4 * (li & 3);
-          const int off = key * ROWB + (((d >> 3) ^ swz_v<D>(key)) << 4) + ((d & 7) << 1);
-          half[hh] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(sv + off));
-        }
-        const i16x8 vf = i16x8{half[0][0], half[0][1], half[0][2], half[0][3],
-                               half[1][0], half[1][1], half[1][2], half[1][3]};
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) o[dt][rt] = Mma<T>::run(bit_cast<V8>(vf), pb[rt], o[dt][rt]);
+  // The streams' shares of a run of n units (unit i of the run: key0_of(i),
+  // masked_of(i), mask_of(i)): stream s takes units s, s+2, ...  NS-1 units
+  // are in flight ahead of the one in use (the first `pre` already issued);
+  // one workgroup barrier per step.
+  auto run_units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
+    const int mine = n > ks ? (n - ks + kStreams - 1) / kStreams : 0;
+    const int steps = (n + kStreams - 1) / kStreams;
+    for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + kStreams * j));
+    for (int j = 0; j < steps; ++j) {
+      // unit j landed for every wave of the stream; stage (j-1)%NS is free
+      if (j < mine) wait_units<LPU, NS - 2>(min(mine - 1 - j, NS - 2));
+      sync_lds();
+      if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + kStreams * (j + NS - 1)));
+      if (j < mine && active) {
+        const int i = ks + kStreams * j;
+        const bool masked = masked_of(i);
+        compute(sring + (j % NS) * SB, masked, masked ? mask_of(i) : ~0u);
       }
     }
   };
-
-  // Pipeline over ntl tiles: NSTAGE-1 tiles in flight ahead of the one in use.
-  auto run_tiles = [&](int ntl, bool prologue_issued, auto key0_of, auto masked_of, auto mask_of_tile) {
-    if (!prologue_issued)
-      for (int j = 0; j < NSTAGE - 1 && j < ntl; ++j) issue(j, key0_of(j));
-    for (int j = 0; j < ntl; ++j) {
-      // tile j landed for every wave; stage (j-1)%NSTAGE is free
-      sync_tiles<LPT, NSTAGE>(min(ntl - 1 - j, NSTAGE - 2));
-      if (j + NSTAGE - 1 < ntl) issue(j + NSTAGE - 1, key0_of(j + NSTAGE - 1));
-      if (active) {
-        const bool masked = masked_of(j);
-        uint64_t mrow[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) mrow[rt] = masked ? mask_of_tile(j, rt) : ~0ull;
-        compute(j % NSTAGE, masked, mrow);
-      }
-    }
-    sync_lds();  // ring free again
-  };
-
   if (!is_tree) {
+    // Prefix run: units [u_lo, u_lo + n) of keys [0, prefix_len); the last
+    // unit of the prefix may be partial.
     const int P = a.prefix_len;
-    const int tile0 = prefix_tile0;
-    run_tiles(
-        prefix_ntl, true, [&](int j) { return (tile0 + j) * kTileKeys; },
-        [&](int j) { return P - (tile0 + j) * kTileKeys < kTileKeys; },
-        [&](int j, int) {
-          const int valid = P - (tile0 + j) * kTileKeys;
-          return valid >= 64 ? ~0ull : ((1ull << valid) - 1ull);
-        });
+    const int u_lo = slot * a.units_per_split;
+    const int n = min(a.units_per_split, a.n_pu - u_lo);
+    auto key0_of = [&](int i) { return (u_lo + i) * kUnitKeys; };
+    // Q and the first NS-1 units of each stream leave together; wait for Q
+    // only (loads complete in order), then every wave reads its fragments.
+    const int mine = n > ks ? (n - ks + kStreams - 1) / kStreams : 0;
+    const int pre = min(mine, NS - 1);
+    issue_q();
+    for (int j = 0; j < pre; ++j) issue(j, key0_of(ks + kStreams * j));
+    wait_units<LPU, NS - 1>(pre);
+    sync_lds();
+    read_q();
+    run_units(
+        n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
+        [&](int i) { return (1u << (P - key0_of(i))) - 1u; });
   } else {
+    load_q();
     const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-    const int qb_lo = t_lo / BM, qb_hi = (t_hi - 1) / BM, nqbc = qb_hi - qb_lo + 1;
+    const int tok_hi = (row0 + rows_chunk - 1) / G;  // tokens tok_lo .. tok_hi
+    const int ntok = tok_hi - tok_lo + 1;
+    const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
     const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
     const int32_t* ci = a.col_idx + b * a.ms_col_idx;
     const int8_t* bt = a.blk_type + b * a.ms_blk_type;
@@ -408,14 +463,14 @@ void split_kernel(const SplitArgs a) {
     const int32_t* of = a.offset + b * a.ms_offset;
     int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
     int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
-    // Two parallel round trips: the chunk's row_ptr window, then every CSR
-    // entry of those rows at once.
+    // Block states of the chunk's q-blocks in two parallel round trips: the
+    // row_ptr window, then every CSR entry of those rows at once.
     auto build_state = [&]() {
-      for (int i = tid; i < nqbc * ntb; i += kThreads) st[i] = 0;
+      for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
       if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
       sync_lds();
       const int e_begin = rps[0], e_end = rps[nqbc];
-      for (int e = e_begin + tid; e < e_end; e += kThreads) {
+      for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
         int qq = 0;
         while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
         const int tb = ci[e];
@@ -424,39 +479,42 @@ void split_kernel(const SplitArgs a) {
       sync_lds();
     };
     build_state();
-    const int n_tt = (a.tree_key_limit + kTileKeys - 1) / kTileKeys;
-    for (int i = tid; i < n_tt; i += kThreads) vis[i] = 0;
+    // Tree units holding a key some row of the chunk can see, compacted.
+    const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
+    for (int i = tid; i < n_tu; i += kWaves * 64) vis[i] = 0;
     sync_lds();
-    for (int i = tid; i < nqbc * ntb; i += kThreads) {
+    for (int i = tid; i < nqbc * ntb; i += kWaves * 64) {
       if (st[i] != 0) {
         const int tb = i % ntb;
         const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
-        for (int v = c_first / kTileKeys; v <= c_last / kTileKeys; ++v) vis[v] = 1;
+        for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
       }
     }
     sync_lds();
     if (wave == 0) {
-      int n = 0;
-      for (int base = 0; base < n_tt; base += 64) {
+      int nv = 0;
+      for (int base = 0; base < n_tu; base += 64) {
         const int idx = base + lane;
-        const bool f = idx < n_tt && vis[idx] != 0;
+        const bool f = idx < n_tu && vis[idx] != 0;
         const uint64_t bal = __ballot(f);
         const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-        if (f) vis[n + pre] = idx;
-        n += __popcll(bal);
+        if (f) vis[nv + pre] = idx;
+        nv += __popcll(bal);
       }
-      if (lane == 0) misc[0] = n;
+      if (lane == 0) misc[0] = nv;
     }
     sync_lds();
     const int n_vis = misc[0];
     for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
       const int nb = min(a.vt_max, n_vis - vb0);
       if (vb0 > 0) build_state();
-      for (int it = tid; it < ntok * nb * 4; it += kThreads) {
-        const int q4 = it & 3, jt = it >> 2;
+      // Per-token visibility word of each unit of the batch, from two 16-key
+      // groups (BN is a multiple of 16, so a group never straddles blocks).
+      for (int it = tid; it < ntok * nb * 2; it += kWaves * 64) {
+        const int q2 = it & 1, jt = it >> 1;
         const int j = jt % nb, tt = jt / nb;
-        const int t = t_lo + tt, qb = t / BM, tl = t - qb * BM;
-        const int c0 = vis[vb0 + j] * kTileKeys + q4 * 16;
+        const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
+        const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
         uint32_t bits = 0;
         if (c0 < a.tree_key_limit) {
           const int tb = c0 / BN;
@@ -470,53 +528,65 @@ void split_kernel(const SplitArgs a) {
           const int valid = a.tree_key_limit - c0;
           if (valid < 16) bits &= (1u << valid) - 1u;
         }
-        masks[(tt * a.vt_max + j) * 4 + q4] = (uint16_t)bits;
+        // two 16-bit halves assembled through LDS: the q2 = 1 half lands in the high bits
+        reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
       }
       sync_lds();
-      run_tiles(
-          nb, false, [&](int j) { return P + vis[vb0 + j] * kTileKeys; }, [&](int) { return true; },
-          [&](int j, int rt) -> uint64_t {
-            int tt = row_tok[0];
-#pragma unroll
-            for (int r2 = 1; r2 < RT; ++r2) tt = (rt == r2) ? row_tok[r2] : tt;
-            return *reinterpret_cast<const uint64_t*>(masks + (tt * a.vt_max + j) * 4);
-          });
+      run_units(
+          nb, 0, [&](int i) { return P + vis[vb0 + i] * kUnitKeys; }, [&](int) { return true; },
+          [&](int i) { return masks[row_tt * a.vt_max + i]; });
+      sync_all();  // ring and masks free for the next batch
     }
   }
 
-  // Epilogue.  Each wave stages its rows' O/l (input dtype) through its own
-  // 8 KB of the (now idle) ring, row-major with a 16-byte-chunk XOR swizzle,
-  // then stores whole rows: every store instruction writes 1 KB contiguous.
-  if (!active) return;
-  const int64_t TG = (int64_t)a.q_len * G;
-  const int64_t base =
-      ((int64_t)(b * a.num_kv_heads + kvh) * a.n_slots + slot) * TG + (int64_t)t_lo * G;
-  unsigned char* stage = ring + wave * (kRowsPerWave * ROWB);
+  // Epilogue.  Stream 1 leaves (m, l) and O^T of its rows in LDS; stream 0
+  // merges them into its own (log-sum-exp), normalises, and stages the rows in
+  // the input dtype; then all waves store whole rows (1 KB per instruction).
+  sync_all();
+  float2* mls = reinterpret_cast<float2*>(masks);  // [row group][32]
+  unsigned char* stg = ring + kRingBytes / 2;      // [kRows][D], 16-byte chunks swizzled
+  if (ks == 1) {
+    const float lt = pair_sum(l_run);
+    if (lh == 0) mls[rg * 32 + ln] = make_float2(m_run, lt);
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float l = row_sum4(l_run[rt]);
-    const float inv = l > 0.f ? 1.f / l : 0.f;  // empty partial: O = 0, weight 0 in the combine
-    const int r = wave * kRowsPerWave + rt * 16 + li;
-    if (lg == 0 && r < rows) a.ws_ml[base + r] = make_float2(m_run[rt], l);
-    const int rl = rt * 16 + li;
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < DTILES; ++dt) {
-      typedef T T4 __attribute__((ext_vector_type(4)));
-      T4 v4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v4[i] = (T)(o[dt][rt][i] * inv);
-      const int chunk = (dt * 2 + (lg >> 1)) ^ (rl & (CPR - 1));
-      *reinterpret_cast<T4*>(stage + rl * ROWB + chunk * 16 + (lg & 1) * 8) = v4;
-    }
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16) =
+            f32x4{o[dt][4 * q], o[dt][4 * q + 1], o[dt][4 * q + 2], o[dt][4 * q + 3]};
   }
-  T* dst = static_cast<T*>(a.ws_o) + (base + wave * kRowsPerWave) * D;
-  const int wave_rows = min(kRowsPerWave, rows - wave * kRowsPerWave);
+  sync_lds();
+  const int64_t part_row0 = ((int64_t)bk * a.n_slots + slot) * TG + row0;
+  if (ks == 0) {
+    const float2 other = mls[rg * 32 + ln];
+    const float lt = pair_sum(l_run);
+    const float M = fmaxf(m_run, other.x);
+    // weights 2^((m_s - M) * scale); 0 for a stream that saw no key
+    const float w0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - M) * sl2);
+    const float w1 = (other.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((other.x - M) * sl2);
+    const float L = w0 * lt + w1 * other.y;
+    const float inv = L > 0.f ? 1.f / L : 0.f;  // empty partial: O = 0, weight 0 in the combine
+    const int r = rg * 32 + ln;
+    typedef T T4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int k = 0; k < kRowsPerWave * CPR / 64; ++k) {
-    const int idx = k * 64 + lane;
-    const int rl = idx / CPR, c = idx % CPR;
-    const i16x8 v = *reinterpret_cast<const i16x8*>(stage + rl * ROWB + ((c ^ (rl & (CPR - 1))) << 4));
-    if (rl < wave_rows) *reinterpret_cast<i16x8*>(dst + (int64_t)rl * D + c * 8) = v;
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16);
+        T4 v4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = (T)((w0 * o[dt][4 * q + i] + w1 * x[i]) * inv);
+        *reinterpret_cast<T4*>(stg + r * ROWB + (((4 * dt + q) ^ swz_k<D>(r)) << 4) + 8 * lh) = v4;
+      }
+    if (lh == 0 && r < rows_chunk) a.ws_ml[part_row0 + r] = make_float2(M, L);
+  }
+  sync_lds();
+  constexpr int CPR = D / 8;
+  T* dst = static_cast<T*>(a.ws_o) + part_row0 * D;
+  for (int idx = tid; idx < rows_chunk * CPR; idx += kWaves * 64) {
+    const int r = idx / CPR, c = idx % CPR;
+    *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) =
+        *reinterpret_cast<const i16x8*>(stg + r * ROWB + ((c ^ swz_k<D>(r)) << 4));
   }
 }
 
@@ -588,16 +658,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
 
 // ------------------------------------------------------------------- plan
 struct Plan {
-  int tpc, n_chunks, n_ptiles, tiles_per_split, n_splits, n_slots, n_items, items_per_xcd, grid;
-  int nstage, vt_max, tree_key_limit;
+  int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages;
+  int vt_max, tree_key_limit;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-size_t lds_bytes_for(int head_dim, int nstage) {
-  return (size_t)nstage * 2 * kTileKeys * head_dim * 2 + kMaskBytes + (kMaxTreeTiles + kMiscInts) * 4;
-}
 
 int env_int(const char* name, int dflt) {
   const char* s = getenv(name);
@@ -605,40 +671,48 @@ int env_int(const char* name, int dflt) {
   return atoi(s);
 }
 
-// Decide tokens per chunk, prefix split size and LDS ring depth.
+// Tokens a chunk of kRows consecutive rows can touch, and q-blocks those span.
+int64_t chunk_tokens(int group) { return (int64_t)(kRows - 1) / group + 2; }
+int64_t chunk_qblocks(int group, int block_m) { return (chunk_tokens(group) - 1) / block_m + 2; }
+
+// Prefix run length (units per split) and the grid.
 int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
               Plan* p) {
   const int G = num_heads / num_kv_heads;
-  p->tpc = std::max(1, std::min(q_len, kRowsPerChunk / G));
-  p->n_chunks = ceil_div(q_len, p->tpc);
-  p->n_ptiles = ceil_div(prefix_len, kTileKeys);
+  const int64_t TG = (int64_t)q_len * G;
+  if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
+  p->n_chunks = (int)((TG + kRows - 1) / kRows);
+  p->n_pu = ceil_div(prefix_len, kUnitKeys);
   int cus = 256;
   if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
   const int64_t groups = (int64_t)batch * num_kv_heads * p->n_chunks;
-  int tps = 0;
-  if (p->n_ptiles > 0) {
-    tps = env_int("TSFA_PREFIX_TILES_PER_SPLIT", 0);
-    if (tps <= 0) {
-      // Makespan model: workgroups run one per CU; a split of tps tiles costs
-      // tps + 1 tile-times (tile + prologue/epilogue) and every extra slot of
-      // partials costs a little combine traffic.
-      double best = 1e30;
-      for (int cand = 1; cand <= p->n_ptiles; ++cand) {
-        const int64_t splits = ceil_div(p->n_ptiles, cand);
-        if (cand > 1 && ceil_div(p->n_ptiles, cand - 1) == splits) continue;
+  int ups = 0;
+  if (p->n_pu > 0) {
+    ups = env_int("TSFA_PREFIX_UNITS_PER_SPLIT", 0);
+    if (ups <= 0) {
+      // Makespan model (microseconds): one workgroup per CU; a workgroup
+      // costs a fixed start/finish plus its longest stream; every slot of
+      // partials is written once and read once by the combine.
+      const double t_unit = 0.5 * head_dim / 128.0, t_fixed = 1.5;
+      const double part_bytes = (double)batch * num_heads * q_len * (2.0 * head_dim + 8.0);
+      double best = 1e300;
+      for (int cand = 1; cand <= p->n_pu; ++cand) {
+        const int64_t splits = ceil_div(p->n_pu, cand);
+        if (cand > 1 && ceil_div(p->n_pu, cand - 1) == splits) continue;
         const int64_t items = groups * (splits + 1);
         const int64_t rounds = (items + cus - 1) / cus;
-        const double cost = (double)rounds * (cand + 1) + 0.15 * (double)(splits + 1);
-        if (cost < best - 1e-9) {
+        const double cost = (double)rounds * (t_fixed + ceil_div(cand, kStreams) * t_unit) +
+                            part_bytes * (double)(splits + 1) * 2.0 / 5.0e6;
+        if (cost < best * (1.0 - 1e-9)) {
           best = cost;
-          tps = cand;
+          ups = cand;
         }
       }
     }
-    tps = std::min(std::max(tps, 1), p->n_ptiles);
+    ups = std::min(std::max(ups, 1), p->n_pu);
   }
-  p->tiles_per_split = tps;
-  p->n_splits = tps > 0 ? ceil_div(p->n_ptiles, tps) : 0;
+  p->units_per_split = ups;
+  p->n_splits = ups > 0 ? ceil_div(p->n_pu, ups) : 0;
   p->n_slots = p->n_splits + 1;
   const int64_t items = groups * p->n_slots;
   if (items > (int64_t)INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
@@ -647,13 +721,10 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   p->grid = p->items_per_xcd * 8;
   int max_lds = 65536;
   if (device_max_lds_per_block(&max_lds) != TSFA_OK) return TSFA_ERR_DEVICE;
-  int nstage = env_int("TSFA_RING_STAGES", 4);
-  if (nstage != 2 && nstage != 4) nstage = 4;
-  if (lds_bytes_for(head_dim, nstage) > (size_t)max_lds) nstage = 2;
-  if (lds_bytes_for(head_dim, nstage) > (size_t)max_lds) return TSFA_ERR_UNSUPPORTED;
-  p->nstage = nstage;
-  p->lds_bytes = lds_bytes_for(head_dim, nstage);
-  p->vt_max = kMaskBytes / (p->tpc * 8);
+  p->lds_bytes = head_dim == 128 ? lds_bytes_for<128>() : lds_bytes_for<64>();
+  if (p->lds_bytes > (size_t)max_lds) return TSFA_ERR_UNSUPPORTED;
+  p->ring_stages = kRingBytes / kStreams / (2 * kUnitKeys * head_dim * 2);
+  p->vt_max = (int)(kMaskWords / chunk_tokens(G));
   p->tree_key_limit = kv_len - prefix_len;  // refined by the caller with n_tree_blocks*BN
   const size_t rows = (size_t)batch * num_heads * q_len;
   p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 2);
@@ -661,18 +732,13 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   return TSFA_OK;
 }
 
-template <typename T, int D, int NSTAGE>
+template <typename T, int D>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
-  constexpr int WAVES = 8;
-  static bool attr_set = false;  // benign race: idempotent attribute write
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, NSTAGE, WAVES>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
-      return TSFA_ERR_LAUNCH;
-    attr_set = true;
-  }
-  hipLaunchKernelGGL((split_kernel<T, D, NSTAGE, WAVES>), dim3(p.grid), dim3(WAVES * 64), p.lds_bytes, stream,
-                     args);
+  // per launch: the attribute is per device and costs a host call only
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
+    return TSFA_ERR_LAUNCH;
+  hipLaunchKernelGGL((split_kernel<T, D>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -683,7 +749,7 @@ thread_local hipEvent_t g_split_end = nullptr;
 template <typename T, int D>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_split_begin != nullptr && hipEventRecord(g_split_begin, stream) != hipSuccess) return TSFA_ERR_LAUNCH;
-  int st = (p.nstage == 4) ? launch_split<T, D, 4>(sa, p, stream) : launch_split<T, D, 2>(sa, p, stream);
+  int st = launch_split<T, D>(sa, p, stream);
   if (st != TSFA_OK) return st;
   if (g_split_end != nullptr && hipEventRecord(g_split_end, stream) != hipSuccess) return TSFA_ERR_LAUNCH;
   const int64_t threads = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group * (D / 8);
@@ -710,13 +776,12 @@ extern "C" int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, i
   if (dtype != TSFA_DTYPE_FP16 && dtype != TSFA_DTYPE_BF16) return TSFA_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return TSFA_ERR_UNSUPPORTED;
   if (block_n % 16 != 0) return TSFA_ERR_UNSUPPORTED;
-  if (gqa_group_size > kRowsPerChunk) return TSFA_ERR_UNSUPPORTED;
   const int64_t tree_limit = std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
-  if (tree_limit > (int64_t)kMaxTreeTiles * kTileKeys) return TSFA_ERR_UNSUPPORTED;
-  // tree state table [q-blocks per chunk][n_tree_blocks] must fit the smallest LDS ring
-  const int tpc = std::max(1, std::min(q_len, kRowsPerChunk / gqa_group_size));
-  const int64_t nqbc = (int64_t)(tpc > 0 ? (tpc - 1) / block_m : 0) + 2;
-  if (nqbc * n_tree_blocks * 4 > (int64_t)2 * 2 * kTileKeys * head_dim * 2) return TSFA_ERR_UNSUPPORTED;
+  if (tree_limit > (int64_t)kMaxTreeUnits * kUnitKeys) return TSFA_ERR_UNSUPPORTED;
+  // the tree block-state table [q-blocks of a chunk][n_tree_blocks] lives in
+  // the LDS ring and the chunk's row_ptr window in the LDS scalars
+  const int64_t nqbc = chunk_qblocks(gqa_group_size, block_m);
+  if (nqbc * n_tree_blocks * 4 > (int64_t)kRingBytes || nqbc + 1 > kMiscInts - 8) return TSFA_ERR_UNSUPPORTED;
   return TSFA_OK;
 }
 
@@ -736,11 +801,11 @@ extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_l
   const int st = make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p);
   if (st != TSFA_OK) return st;
   out6[0] = p.n_splits;
-  out6[1] = p.tiles_per_split;
-  out6[2] = p.tpc;
+  out6[1] = p.units_per_split;
+  out6[2] = kRows;
   out6[3] = p.n_chunks;
   out6[4] = p.grid;
-  out6[5] = p.nstage;
+  out6[5] = p.ring_stages;
   return TSFA_OK;
 }
 
@@ -763,6 +828,8 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
     for (int j = 0; j < 3; ++j)
       if (strides[4 * i + j] % 8 != 0) return TSFA_ERR_UNSUPPORTED;  // 16-byte aligned rows
   }
+  // K/V row strides must keep a 32-bit lane offset of 8 rows
+  if (strides[6] >= ((int64_t)1 << 26) || strides[10] >= ((int64_t)1 << 26)) return TSFA_ERR_UNSUPPORTED;
   const void* ptrs[4] = {q, k, v, o};
   for (const void* ptr : ptrs)
     if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0) return TSFA_ERR_UNSUPPORTED;
@@ -799,7 +866,13 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   sa.svb = strides[8];
   sa.svh = strides[9];
   sa.svn = strides[10];
-  sa.scale_log2 = sm_scale * 1.4426950408889634f;
+  // Scores enter the exponent as s * |sm_scale| * log2(e) with Q negated for a
+  // negative scale; a zero scale becomes a vanishing one (every visible p = 1
+  // and masked keys still get p = 0).
+  float sl2 = fabsf(sm_scale) * 1.4426950408889634f;
+  if (sl2 == 0.f) sl2 = 1e-30f;
+  sa.scale_log2 = sl2;
+  sa.neg_q = sm_scale < 0.f ? 1 : 0;
   sa.num_kv_heads = num_kv_heads;
   sa.group = gqa_group_size;
   sa.q_len = q_len;
@@ -808,10 +881,9 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   sa.block_m = block_m;
   sa.block_n = block_n;
   sa.n_tree_blocks = n_tree_blocks;
-  sa.tpc = p.tpc;
   sa.n_chunks = p.n_chunks;
-  sa.tiles_per_split = p.tiles_per_split;
-  sa.n_ptiles = p.n_ptiles;
+  sa.units_per_split = p.units_per_split;
+  sa.n_pu = p.n_pu;
   sa.n_slots = p.n_slots;
   sa.n_items = p.n_items;
   sa.items_per_xcd = p.items_per_xcd;

@@ -131,5 +131,5 @@ def fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim
     out = (ctypes.c_int32 * 6)()
     check("tsfa_fwd_plan", load().tsfa_fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
                                                  head_dim, out))
-    keys = ("prefix_splits", "tiles_per_split", "tokens_per_chunk", "row_chunks", "workgroups", "ring_stages")
+    keys = ("prefix_splits", "units_per_split", "rows_per_chunk", "row_chunks", "workgroups", "ring_stages")
     return dict(zip(keys, list(out)))

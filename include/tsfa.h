@@ -121,8 +121,9 @@ int tsfa_fwd(const void* q, const void* k, const void* v, void* o,
 
 /* Work decomposition tsfa_fwd would use (for reports and tests):
  * out[0] = prefix splits per (batch, kv head, row chunk), out[1] = prefix
- * tiles (64 keys) per split, out[2] = tokens per row chunk, out[3] = row
- * chunks, out[4] = workgroups of the main kernel, out[5] = LDS ring stages. */
+ * units (32 keys) per split, out[2] = query rows (token x head of a GQA
+ * group) per row chunk, out[3] = row chunks per (batch, kv head),
+ * out[4] = workgroups of the main kernel, out[5] = LDS ring stages per wave. */
 int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
                   int head_dim, int32_t* out6);
 
