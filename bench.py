@@ -7,17 +7,26 @@ top-8), BLOCK_M=16, BLOCK_N=64.  Synthetic N(0,1) inputs (seed 42).
 
 A step is one forward call (split-KV kernel + combine kernel) over the whole
 batch with the metadata already on the device, as benchmark.py:228-237 times
-the reference kernel.  The K steps run inside one captured HIP graph so host
-launch overhead cannot starve the GPU, and they cycle through enough
-independent K/V copies (>= 512 MiB) that every call reads its K/V from HBM
-rather than from the 256 MB Infinity Cache.
+the reference kernel.  The calls cycle through enough independent K/V copies
+(>= 512 MiB) that every call reads its K/V from HBM rather than from the
+256 MB Infinity Cache.
 
-value      = K/V bytes per call * K / timed seconds  (TB/s, whole call)
-roofline   = the split-KV kernel alone: K/V bytes / its average duration,
-             measured with HIP events recorded around it inside the graph,
-             against 8 TB/s HBM
+Timing: three regions, each K steps captured in one HIP graph (no host
+launch gaps) and bracketed by HIP events on the stream the graph replays on
+(tsfa_fwd_set_kernel_mask selects the kernels a call launches):
+  * full calls (split-KV + combine)  -> value;
+  * the combine alone                -> its duration; full - combine = the
+                                        split-KV kernel's duration inside real
+                                        calls (the roofline figure);
+  * the split-KV kernel alone        -> reported beside it (back to back it
+                                        runs faster than after a combine).
+
+value        = K/V bytes per call * K / full-region seconds  (TB/s, whole call)
+roofline     = K/V bytes / split-KV kernel duration in real calls, against
+               8 TB/s HBM; traffic = HBM bytes per launch from the committed
+               rocprofv3 PMC summary
 cpu_baseline = the fp32 dense+mask oracle (benchmark.py:8-35 restated) on the
-             host cores, over a bounded sample of calls
+               host cores, over a bounded sample of calls
 """
 
 from __future__ import annotations
@@ -79,6 +88,18 @@ def cpu_baseline(w, q, k, v, mask, seconds: float):
     }
 
 
+def calibrate_copy(mib: int, reps: int):
+    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    src = torch.ones(mib * 2 ** 18, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": mib * 2 ** 20, "reps": reps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -88,8 +109,8 @@ def main():
     ap.add_argument("--cold-mib", type=int, default=512, help="K/V bytes cycled through (defeats the MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--split-events", choices=("on", "off"), default="on",
-                    help="record HIP events around the split kernel inside the graph (roofline figure)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain MIB-MiB device copy (rocprofv3 PMC calibration) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -99,6 +120,10 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.calibrate_copy > 0:
+        calibrate_copy(args.calibrate_copy, max(1, args.steps))
+        return
 
     from tsfa import _lib, configs
     import tree_sparse_flashattn as tsf
@@ -130,41 +155,41 @@ def main():
     torch.cuda.synchronize()
 
     steps = args.steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for b, e in ev:  # materialise the underlying hipEvent_t handles
-        b.record()
-        e.record()
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        call(0)  # allocator warm-up on the capture stream
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(steps):
-                if args.split_events == "on":
-                    _lib.check("tsfa_fwd_set_split_events",
-                               lib.tsfa_fwd_set_split_events(ev[i][0].cuda_event, ev[i][1].cuda_event))
-                call(i)
-        _lib.check("tsfa_fwd_set_split_events", lib.tsfa_fwd_set_split_events(None, None))
-    torch.cuda.synchronize()
-    graph.replay()  # warm replay (graph upload)
-    torch.cuda.synchronize()
 
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start.record()
-    graph.replay()
-    t_end.record()
-    torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    split_ms = [b.elapsed_time(e) for b, e in ev] if args.split_events == "on" else [total_ms / steps]
-    split_avg_s = sum(split_ms) / len(split_ms) / 1e3
-    per_call_s = total_ms / 1e3 / steps
-    _log(f"[bench] {steps} calls in {total_ms:.3f} ms: {per_call_s * 1e6:.2f} us/call, "
-         f"split kernel avg {split_avg_s * 1e6:.2f} us (min {min(split_ms) * 1e3:.2f} us)")
+    def capture(kernel_mask: int):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        _lib.check("tsfa_fwd_set_kernel_mask", lib.tsfa_fwd_set_kernel_mask(kernel_mask))
+        try:
+            with torch.cuda.stream(s):
+                call(0)  # allocator warm-up on the capture stream
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    for i in range(steps):
+                        call(i)
+        finally:
+            _lib.check("tsfa_fwd_set_kernel_mask", lib.tsfa_fwd_set_kernel_mask(3))
+        torch.cuda.synchronize()
+        return g, s
+
+    def timed(g, s):
+        g.replay()  # upload / warm
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            a.record()
+            g.replay()
+            b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / 1e3
+
+    regions = {name: capture(mask) for name, mask in (("full", 3), ("combine", 2), ("split", 1))}
+    secs = {name: timed(*gs) / steps for name, gs in regions.items()}
+    per_call_s = secs["full"]
+    split_avg_s = secs["full"] - secs["combine"]
+    _log(f"[bench] {steps} calls: {per_call_s * 1e6:.2f} us/call = split-KV {split_avg_s * 1e6:.2f} + combine "
+         f"{secs['combine'] * 1e6:.2f} us; split-KV back to back {secs['split'] * 1e6:.2f} us/launch")
 
     achieved_gbps = kvb / split_avg_s / 1e9
     traffic = _traffic(w.name)
@@ -187,7 +212,8 @@ def main():
             "workload": w.name,
             "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
             "prefix_len": w.prefix_len, "tree_len": w.tree_len, "block_m": w.block_m, "block_n": w.block_n,
-            "kv_bytes_per_call": kvb, "kv_copies_cycled": copies, "plan": plan, "timing": "hip graph of all steps",
+            "kv_bytes_per_call": kvb, "kv_copies_cycled": copies, "plan": plan,
+            "timing": "hip graph of all steps; HIP events on the replay stream",
         },
         "roofline": {
             "bound": "hbm",
@@ -198,6 +224,8 @@ def main():
             "frac": round(achieved_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "split_kernel_us": round(split_avg_s * 1e6, 3),
+            "split_kernel_back_to_back_us": round(secs["split"] * 1e6, 3),
+            "combine_kernel_us": round(secs["combine"] * 1e6, 3),
         },
         "cpu_baseline": None,
     }

@@ -40,6 +40,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "tsfa_internal.h"
 
@@ -734,24 +735,33 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
 
 template <typename T, int D>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
-  // per launch: the attribute is per device and costs a host call only
-  if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
-    return TSFA_ERR_LAUNCH;
+  // The LDS limit attribute is set once per device (the first call on a
+  // device, before any graph capture that replays it).
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
+  const uint64_t bit = 1ull << (dev & 63);
+  if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
+      return TSFA_ERR_LAUNCH;
+    attr_set.fetch_or(bit, std::memory_order_acq_rel);
+  }
   hipLaunchKernelGGL((split_kernel<T, D>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
-// Measurement hook: events recorded around the split kernel (per thread).
-thread_local hipEvent_t g_split_begin = nullptr;
-thread_local hipEvent_t g_split_end = nullptr;
+// Measurement hook (per host thread): which of the two kernels a call
+// launches (bit 0 split-KV, bit 1 combine).
+thread_local int g_kernel_mask = 3;
 
 template <typename T, int D>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
-  if (g_split_begin != nullptr && hipEventRecord(g_split_begin, stream) != hipSuccess) return TSFA_ERR_LAUNCH;
-  int st = launch_split<T, D>(sa, p, stream);
-  if (st != TSFA_OK) return st;
-  if (g_split_end != nullptr && hipEventRecord(g_split_end, stream) != hipSuccess) return TSFA_ERR_LAUNCH;
+  if (g_kernel_mask & 1) {
+    const int st = launch_split<T, D>(sa, p, stream);
+    if (st != TSFA_OK) return st;
+  }
+  if ((g_kernel_mask & 2) == 0) return TSFA_OK;
   const int64_t threads = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group * (D / 8);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, ca);
@@ -913,9 +923,8 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   return head_dim == 128 ? launch_all<_Float16, 128>(sa, ca, p, stream) : launch_all<_Float16, 64>(sa, ca, p, stream);
 }
 
-extern "C" int tsfa_fwd_set_split_events(void* begin, void* end) {
-  if ((begin == nullptr) != (end == nullptr)) return TSFA_ERR_INVALID_ARGUMENT;
-  g_split_begin = static_cast<hipEvent_t>(begin);
-  g_split_end = static_cast<hipEvent_t>(end);
+extern "C" int tsfa_fwd_set_kernel_mask(int mask) {
+  if (mask < 1 || mask > 3) return TSFA_ERR_INVALID_ARGUMENT;
+  g_kernel_mask = mask;
   return TSFA_OK;
 }

@@ -37,7 +37,7 @@ EXPORTS = (
     "tsfa_fwd_workspace_bytes",
     "tsfa_fwd",
     "tsfa_fwd_plan",
-    "tsfa_fwd_set_split_events",
+    "tsfa_fwd_set_kernel_mask",
 )
 
 _c_int, _c_i64, _c_size, _c_vp, _c_float = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
@@ -56,7 +56,7 @@ _SIGNATURES = {
                           ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
     "tsfa_fwd_plan": (_c_int, [_c_int] * 7 + [ctypes.POINTER(ctypes.c_int32)]),
-    "tsfa_fwd_set_split_events": (_c_int, [_c_vp, _c_vp]),
+    "tsfa_fwd_set_kernel_mask": (_c_int, [_c_int]),
 }
 
 _lib = None

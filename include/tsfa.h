@@ -128,11 +128,12 @@ int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_
                   int head_dim, int32_t* out6);
 
 /* Measurement hook (no reference counterpart; for benchmarks and profilers):
- * while set, every tsfa_fwd call on this host thread records `begin`/`end`
- * (hipEvent_t, created by the caller) on its stream immediately before and
- * after the main split-KV kernel, so the caller can time that kernel alone.
- * Pass NULL, NULL to stop. */
-int tsfa_fwd_set_split_events(void* begin, void* end);
+ * which kernels tsfa_fwd launches on this host thread -- bit 0 the split-KV
+ * kernel, bit 1 the combine (3 = both, the default and the only setting that
+ * computes O).  A benchmark times each kernel alone this way; any other mask
+ * leaves O unwritten or computed from stale partials.  Invalid: mask outside
+ * 1..3. */
+int tsfa_fwd_set_kernel_mask(int mask);
 
 #ifdef __cplusplus
 }

@@ -78,3 +78,23 @@ def test_null_pointers_rejected_before_device_work():
                       *list(FWD_OK.values()), None, 0, None)
     assert st == _lib.TSFA_ERR_INVALID_ARGUMENT
     assert lib.tsfa_pack_bits(None, -1, None, None) == _lib.TSFA_ERR_INVALID_ARGUMENT
+
+
+def test_kernel_mask_hook_validates_and_restores():
+    lib = _lib.load()
+    for bad in (0, 4, -1):
+        assert lib.tsfa_fwd_set_kernel_mask(bad) == _lib.TSFA_ERR_INVALID_ARGUMENT
+    for ok in (1, 2, 3):
+        assert lib.tsfa_fwd_set_kernel_mask(ok) == _lib.TSFA_OK
+    assert lib.tsfa_fwd_set_kernel_mask(3) == _lib.TSFA_OK  # back to computing O
+
+
+def test_tree_limits_reported_unsupported():
+    # tree keys beyond 32768 (1024 units of 32) and block-state tables larger
+    # than the LDS ring are refused, not silently mis-computed
+    assert _fwd_check(q_len=40000, kv_len=44096, n_q_blocks=2500, n_tree_blocks=625) == _lib.TSFA_ERR_UNSUPPORTED
+    # 34 q-blocks x 2048 tree blocks x 4 B > 128 KiB
+    assert _fwd_check(q_len=32768, kv_len=36864, block_m=1, n_q_blocks=32768, block_n=16,
+                      n_tree_blocks=2048) == _lib.TSFA_ERR_UNSUPPORTED
+    assert _fwd_check(q_len=8192, kv_len=12288, block_m=1, n_q_blocks=8192, block_n=16,
+                      n_tree_blocks=512) == _lib.TSFA_OK
