@@ -47,11 +47,9 @@
 namespace tsfa {
 namespace fwd {
 
-constexpr int kWaves = 8;
-constexpr int kStreams = 2;
-constexpr int kRowGroups = kWaves / kStreams;  // 32 rows each
+constexpr int kWaves = 8;                  // 32 query rows each
+constexpr int kMaxRows = 32 * kWaves;      // rows per chunk with one key stream
 constexpr int kUnitKeys = 32;
-constexpr int kRows = 32 * kRowGroups;  // rows per chunk (workgroup)
 constexpr int kRingBytes = 131072;   // K/V rings of the streams; the merge buffer at the end
 constexpr int kMaskWords = 4096;     // per-token 32-bit visibility words of tree units
 constexpr int kMaxTreeUnits = 1024;  // tree keys <= 32768
@@ -202,21 +200,29 @@ template <int D> constexpr size_t lds_bytes_for() {
   return (size_t)kRingBytes + kMaskWords * 4 + (kMaxTreeUnits + kMiscInts) * 4;
 }
 
-template <typename T, int D>
+// S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.
+template <typename T, int D, int S>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
+  constexpr int RG = kWaves / S;             // row groups (waves per stream)
+  constexpr int ROWS = 32 * RG;              // rows per chunk
   constexpr int ROWB = D * 2;                // bytes of one key row
   constexpr int HALF = kUnitKeys * ROWB;     // K (or V) bytes of one unit
   constexpr int SB = 2 * HALF;               // ring stage
-  constexpr int RB = kRingBytes / kStreams;  // ring of one stream
+  constexpr int RB = kRingBytes / S;         // ring of one stream
   constexpr int NS = RB / SB;                // stages per stream
   constexpr int LPH = HALF / 1024;           // 1 KB loads per half
-  constexpr int LPU = 2 * LPH / kRowGroups;  // loads per unit per wave
+  constexpr int LPU = 2 * LPH / RG;          // loads per unit per wave
+  constexpr int QROWS = ROWS / S;            // Q rows staged in each stream's ring
+  constexpr int QS = QROWS * ROWB / SB;      // ring stages they occupy at start
   constexpr int KSTEPS = D / 16;
   constexpr int DT = D / 32;
-  static_assert(NS >= 2 && (NS & (NS - 1)) == 0 && LPU * (NS - 2) < 64 && LPH % 2 == 0, "ring geometry");
-  static_assert(kWaves * DT * 64 * 64 <= kRingBytes, "merge buffer");
+  static_assert(S == 1 || S == 2, "streams");
+  static_assert(NS >= 4 && (NS & (NS - 1)) == 0 && LPU >= 1 && LPU * (NS - 2) < 64 && LPH % (RG / 2) == 0,
+                "ring geometry");
+  static_assert(QS >= 1 && QS < NS && QROWS * ROWB == QS * SB, "Q staging");
+  static_assert(S == 1 || kWaves * DT * 64 * 64 / 2 + ROWS * ROWB <= kRingBytes, "merge buffer");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   unsigned char* ring = smem;
@@ -227,7 +233,7 @@ void split_kernel(const SplitArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rg = wave & (kRowGroups - 1), ks = wave / kRowGroups;  // SIMD rg holds both streams
+  const int rg = wave % RG, ks = wave / RG;  // with S = 2, SIMD rg%4 holds one wave of each stream
   const int ln = lane & 31, lh = lane >> 5;
 
   // XCD-aware item order: consecutive block ids go to different XCDs, so each
@@ -244,8 +250,8 @@ void split_kernel(const SplitArgs a) {
 
   const int G = a.group;
   const int TG = a.q_len * G;
-  const int row0 = chunk * kRows;
-  const int rows_chunk = min(kRows, TG - row0);
+  const int row0 = chunk * ROWS;
+  const int rows_chunk = min(ROWS, TG - row0);
   const bool active = rg * 32 < rows_chunk;
   const int tok_lo = row0 / G;
   const float sl2 = a.scale_log2;
@@ -256,16 +262,16 @@ void split_kernel(const SplitArgs a) {
   unsigned char* sring = ring + ks * RB;
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
 
-  // The stream's four waves move a quarter of each unit: row groups 0-1 the
-  // two halves of K, 2-3 the two halves of V.
-  const bool dma_v = rg >= 2;
-  const int dma_u0 = (rg & 1) * (LPH / 2);
+  // The stream's RG waves move equal shares of each unit: the first half of
+  // them K, the second half V.
+  const bool dma_v = rg >= RG / 2;
+  const int dma_u0 = (rg % (RG / 2)) * LPU;
   uint32_t loff[D == 128 ? 4 : 2];
 #pragma unroll
   for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
     loff[u] = dma_v ? dma_lane_off<D, true>(u, a.svn, lane) : dma_lane_off<D, false>(u, a.skn, lane);
 
-  // HBM -> LDS: this wave's quarter of one unit (keys key0 .. key0+31) into
+  // HBM -> LDS: this wave's share of one unit (keys key0 .. key0+31) into
   // stage st of its stream's ring.
   auto issue = [&](int st, int key0) {
     const uint32_t sb = sring_lds + st * SB;
@@ -299,28 +305,29 @@ void split_kernel(const SplitArgs a) {
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(qf[kk]));
   };
-  // Q through LDS instead: the chunk's rows go HBM -> LDS into the last ring
-  // stage of the stream whose row groups use them (rows 64*s .. 64*s+63 of
-  // the chunk in stream s), as global_load_lds issued ahead of the first K/V
-  // units, so the prologue need not wait for Q before filling the ring.
-  // Rows past the end repeat the last row (their outputs are never stored).
+  // Q through LDS instead: the chunk's rows go HBM -> LDS into the last QS
+  // ring stages of the stream whose row groups use them (QROWS rows per
+  // stream), as global_load_lds issued ahead of the first K/V units, so the
+  // prologue need not wait for Q before filling the ring.  Rows past the end
+  // repeat the last row (their outputs are never stored).
   auto issue_q = [&]() {
     constexpr int RPL = 1024 / ROWB, CPR = D / 8;
-    constexpr int QL = kRows / RPL / kWaves;  // 1 KB loads per wave
+    constexpr int QL = ROWS / RPL / kWaves;  // 1 KB loads per wave
 #pragma unroll
     for (int i = 0; i < QL; ++i) {
       const int l0 = (wave * QL + i) * RPL;  // first chunk row of the load
-      const int row = l0 + lane / CPR, pos = lane % CPR, tr = row & 63;
+      const int row = l0 + lane / CPR, pos = lane % CPR, tr = row % QROWS;
       const int R = min(row0 + row, TG - 1);
       const int t = R / G;
       const int g = R - t * G;
       const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
                      ((pos ^ swz_k<D>(tr)) << 3);
-      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(ring + (l0 >> 6) * RB + (NS - 1) * SB + (l0 & 63) * ROWB)));
+      dma16(src, __builtin_amdgcn_readfirstlane(
+                     lds_addr(ring + (l0 / QROWS) * RB + (NS - QS) * SB + (l0 % QROWS) * ROWB)));
     }
   };
   auto read_q = [&]() {
-    const unsigned char* qs = ring + (rg >> 1) * RB + (NS - 1) * SB + ((rg & 1) * 32) * ROWB;
+    const unsigned char* qs = ring + (rg * 32 / QROWS) * RB + (NS - QS) * SB + ((rg * 32) % QROWS) * ROWB;
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
       qf[kk] = *reinterpret_cast<const i16x8*>(qs + ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4)) ^ qsgn;
@@ -358,15 +365,31 @@ void split_kernel(const SplitArgs a) {
   // the 32-bit key visibility of the lane's row (read only when `masked`).
   auto compute = [&](const unsigned char* sk, bool masked, uint32_t mw) {
     const unsigned char* sv = sk + HALF;
+    // Every LDS operand read of the unit goes out first (K for S^T, then the
+    // V^T halves for O^T, which land during the softmax), so no MFMA waits on
+    // a read issued just before it.
+    i16x8 kf[KSTEPS];
+    i16x4 vh[DT][2][2];
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) kf[kk] = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          vh[dt][s2][jj] =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(sv + v_off[dt] + (16 * s2 + 8 * jj) * ROWB));
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      const i16x8 kf = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
-      s = Mma<T>::run(bit_cast<V8>(kf), bit_cast<V8>(qf[kk]), s);
-    }
+    for (int kk = 0; kk < KSTEPS; ++kk) s = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[kk]), s);
     if (masked) {
+      // a real (wave-uniform) branch: the empty asm keeps the compiler from
+      // speculating the mask into selects that every unmasked unit would pay
+      asm volatile("" ::: "memory");
       const uint32_t w = mw >> (4 * lh);
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -404,29 +427,26 @@ void split_kernel(const SplitArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const unsigned char* vp = sv + v_off[dt] + (16 * s2) * ROWB;
-        const i16x4 h0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(vp));
-        const i16x4 h1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(vp + 8 * ROWB));
-        const i16x8 vf = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
         o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
       }
   };
 
   // The streams' shares of a run of n units (unit i of the run: key0_of(i),
-  // masked_of(i), mask_of(i)): stream s takes units s, s+2, ...  NS-1 units
+  // masked_of(i), mask_of(i)): stream s takes units s, s+S, ...  NS-1 units
   // are in flight ahead of the one in use (the first `pre` already issued);
   // one workgroup barrier per step.
   auto run_units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
-    const int mine = n > ks ? (n - ks + kStreams - 1) / kStreams : 0;
-    const int steps = (n + kStreams - 1) / kStreams;
-    for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + kStreams * j));
+    const int mine = n > ks ? (n - ks + S - 1) / S : 0;
+    const int steps = (n + S - 1) / S;
+    for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + S * j));
     for (int j = 0; j < steps; ++j) {
       // unit j landed for every wave of the stream; stage (j-1)%NS is free
       if (j < mine) wait_units<LPU, NS - 2>(min(mine - 1 - j, NS - 2));
       sync_lds();
-      if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + kStreams * (j + NS - 1)));
+      if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
       if (j < mine && active) {
-        const int i = ks + kStreams * j;
+        const int i = ks + S * j;
         const bool masked = masked_of(i);
         compute(sring + (j % NS) * SB, masked, masked ? mask_of(i) : ~0u);
       }
@@ -439,15 +459,17 @@ void split_kernel(const SplitArgs a) {
     const int u_lo = slot * a.units_per_split;
     const int n = min(a.units_per_split, a.n_pu - u_lo);
     auto key0_of = [&](int i) { return (u_lo + i) * kUnitKeys; };
-    // Q and the first NS-1 units of each stream leave together; wait for Q
+    // Q and the first NS-QS units of each stream leave together; wait for Q
     // only (loads complete in order), then every wave reads its fragments.
-    const int mine = n > ks ? (n - ks + kStreams - 1) / kStreams : 0;
-    const int pre = min(mine, NS - 1);
+    // With QS > 1 the ring prologue reuses Q stages: one more barrier first.
+    const int mine = n > ks ? (n - ks + S - 1) / S : 0;
+    const int pre = min(mine, NS - QS);
     issue_q();
-    for (int j = 0; j < pre; ++j) issue(j, key0_of(ks + kStreams * j));
-    wait_units<LPU, NS - 1>(pre);
+    for (int j = 0; j < pre; ++j) issue(j, key0_of(ks + S * j));
+    wait_units<LPU, NS - QS>(pre);
     sync_lds();
     read_q();
+    if (QS > 1) sync_lds();
     run_units(
         n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; });
@@ -540,13 +562,14 @@ void split_kernel(const SplitArgs a) {
     }
   }
 
-  // Epilogue.  Stream 1 leaves (m, l) and O^T of its rows in LDS; stream 0
-  // merges them into its own (log-sum-exp), normalises, and stages the rows in
-  // the input dtype; then all waves store whole rows (1 KB per instruction).
+  // Epilogue.  With two streams, stream 1 leaves (m, l) and O^T of its rows in
+  // LDS and stream 0 merges them into its own (log-sum-exp).  Each row's
+  // owner normalises and stages the row in the input dtype; then all waves
+  // store whole rows (1 KB per instruction).
   sync_all();
-  float2* mls = reinterpret_cast<float2*>(masks);  // [row group][32]
-  unsigned char* stg = ring + kRingBytes / 2;      // [kRows][D], 16-byte chunks swizzled
-  if (ks == 1) {
+  float2* mls = reinterpret_cast<float2*>(masks);                   // [row group][32]
+  unsigned char* stg = ring + (S == 2 ? kRingBytes - ROWS * ROWB : 0);  // [ROWS][D], chunks swizzled
+  if (S == 2 && ks == 1) {
     const float lt = pair_sum(l_run);
     if (lh == 0) mls[rg * 32 + ln] = make_float2(m_run, lt);
 #pragma unroll
@@ -556,16 +579,19 @@ void split_kernel(const SplitArgs a) {
         *reinterpret_cast<f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16) =
             f32x4{o[dt][4 * q], o[dt][4 * q + 1], o[dt][4 * q + 2], o[dt][4 * q + 3]};
   }
-  sync_lds();
+  if (S == 2) sync_lds();
   const int64_t part_row0 = ((int64_t)bk * a.n_slots + slot) * TG + row0;
   if (ks == 0) {
-    const float2 other = mls[rg * 32 + ln];
     const float lt = pair_sum(l_run);
-    const float M = fmaxf(m_run, other.x);
-    // weights 2^((m_s - M) * scale); 0 for a stream that saw no key
-    const float w0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - M) * sl2);
-    const float w1 = (other.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((other.x - M) * sl2);
-    const float L = w0 * lt + w1 * other.y;
+    float M = m_run, L = lt, w0 = 1.f, w1 = 0.f;
+    if (S == 2) {
+      const float2 other = mls[rg * 32 + ln];
+      M = fmaxf(m_run, other.x);
+      // weights 2^((m_s - M) * scale); 0 for a stream that saw no key
+      w0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - M) * sl2);
+      w1 = (other.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((other.x - M) * sl2);
+      L = w0 * lt + w1 * other.y;
+    }
     const float inv = L > 0.f ? 1.f / L : 0.f;  // empty partial: O = 0, weight 0 in the combine
     const int r = rg * 32 + ln;
     typedef T T4 __attribute__((ext_vector_type(4)));
@@ -573,10 +599,15 @@ void split_kernel(const SplitArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const f32x4 x = *reinterpret_cast<const f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16);
         T4 v4;
+        if (S == 2) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = (T)((w0 * o[dt][4 * q + i] + w1 * x[i]) * inv);
+          for (int i = 0; i < 4; ++i) v4[i] = (T)((w0 * o[dt][4 * q + i] + w1 * x[i]) * inv);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v4[i] = (T)(o[dt][4 * q + i] * inv);
+        }
         *reinterpret_cast<T4*>(stg + r * ROWB + (((4 * dt + q) ^ swz_k<D>(r)) << 4) + 8 * lh) = v4;
       }
     if (lh == 0 && r < rows_chunk) a.ws_ml[part_row0 + r] = make_float2(M, L);
@@ -592,12 +623,15 @@ void split_kernel(const SplitArgs a) {
 }
 
 // Merge the n_slots partials of every row and write O.  Threads walk the
-// workspace rows in order (coalesced 16-byte partial loads); 8 outputs per
-// thread; the slot loop is branch-free (an empty partial has weight 0) so the
-// loads of several slots are in flight together.
+// workspace rows in order (coalesced partial loads), kEpt outputs per thread;
+// up to kBatch slots are loaded together (one memory round trip for the
+// usual slot counts) and folded in branch-free (an empty partial has weight 0).
+constexpr int kEpt = 4;
+constexpr int kBatch = 16;
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
-  constexpr int TPR = D / 8;
+  constexpr int TPR = D / kEpt;
   const int64_t gtid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t TG = (int64_t)a.q_len * a.group;
   const int64_t row = gtid / TPR;  // over B*Hkv*TG
@@ -610,55 +644,58 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
   const int h = kvh * a.group + g;
   const int64_t r0 = bk * a.n_slots * TG + R;
   const float2* ml = a.ws_ml + r0;
-  const T* src = static_cast<const T*>(a.ws_o) + r0 * D + part * 8;
+  const T* src = static_cast<const T*>(a.ws_o) + r0 * D + part * kEpt;
   const int64_t slot_stride = TG * D;
-  typedef T T8 __attribute__((ext_vector_type(8)));
+  typedef T TV __attribute__((ext_vector_type(kEpt)));
 
-  // Running merge in batches of 8 slots: the 8 (m, l) pairs and 8 partial
-  // vectors of a batch are loaded together, then folded into (M, L, acc)
-  // with the same re-basing as the online softmax.
+  // Running merge over batches of slots: a batch's (m, l) pairs and partial
+  // vectors are loaded together, then folded into (M, L, acc) with the same
+  // re-basing as the online softmax.
   float mx = -INFINITY, l = 0.f;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < a.n_slots; s0 += 8) {
-    const int nb = min(8, a.n_slots - s0);
-    float2 v[8];
-    T8 x[8];
+  float acc[kEpt];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+  for (int e = 0; e < kEpt; ++e) acc[e] = 0.f;
+  for (int s0 = 0; s0 < a.n_slots; s0 += kBatch) {
+    const int nb = min(kBatch, a.n_slots - s0);
+    float2 v[kBatch];
+    TV x[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
       const int s = s0 + min(i, nb - 1);  // duplicates of the last slot get weight 0 below
       v[i] = ml[s * TG];
-      x[i] = *reinterpret_cast<const T8*>(src + s * slot_stride);
+      x[i] = *reinterpret_cast<const TV*>(src + s * slot_stride);
     }
     float bm = mx;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) bm = (i < nb) ? fmaxf(bm, v[i].x) : bm;
+    for (int i = 0; i < kBatch; ++i) bm = (i < nb) ? fmaxf(bm, v[i].x) : bm;
     if (bm != -INFINITY && bm != mx) {  // re-base the running sums on the new max
       const float alpha = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mx - bm) * a.scale_log2);
       l *= alpha;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+      for (int e = 0; e < kEpt; ++e) acc[e] *= alpha;
       mx = bm;
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < kBatch; ++i) {
       // weight of partial s: l_s * 2^((m_s - M) * scale); 0 for an empty partial
       const float w = (i >= nb || v[i].x == -INFINITY) ? 0.f
                                                       : v[i].y * __builtin_amdgcn_exp2f((v[i].x - mx) * a.scale_log2);
       l += w;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += w * (float)x[i][e];
+      for (int e = 0; e < kEpt; ++e) acc[e] += w * (float)x[i][e];
     }
   }
   // l == 0 (no visible key anywhere) gives 0/0 = NaN, as acc / l_i does in the reference.
-  T8 out;
+  TV out;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = (T)(acc[i] / l);
-  T* dst = static_cast<T*>(a.o) + b * a.sob + (int64_t)h * a.soh + (int64_t)t * a.som + part * 8;
-  *reinterpret_cast<T8*>(dst) = out;
+  for (int i = 0; i < kEpt; ++i) out[i] = (T)(acc[i] / l);
+  T* dst = static_cast<T*>(a.o) + b * a.sob + (int64_t)h * a.soh + (int64_t)t * a.som + part * kEpt;
+  *reinterpret_cast<TV*>(dst) = out;
 }
 
 // ------------------------------------------------------------------- plan
 struct Plan {
+  int streams, rows_per_chunk;
   int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages;
   int vt_max, tree_key_limit;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
@@ -672,17 +709,22 @@ int env_int(const char* name, int dflt) {
   return atoi(s);
 }
 
-// Tokens a chunk of kRows consecutive rows can touch, and q-blocks those span.
-int64_t chunk_tokens(int group) { return (int64_t)(kRows - 1) / group + 2; }
-int64_t chunk_qblocks(int group, int block_m) { return (chunk_tokens(group) - 1) / block_m + 2; }
+// Tokens a chunk of `rows` consecutive rows can touch, and q-blocks those span.
+int64_t chunk_tokens(int rows, int group) { return (int64_t)(rows - 1) / group + 2; }
+int64_t chunk_qblocks(int rows, int group, int block_m) { return (chunk_tokens(rows, group) - 1) / block_m + 2; }
 
-// Prefix run length (units per split) and the grid.
+// Key streams per workgroup, prefix run length (units per split) and the grid.
+// Two streams (128-row chunks) by default: measured faster than one stream
+// (256-row chunks, each K/V byte reaching one workgroup) on the 8B decode
+// shape, where one stream doubles the Q and partial bytes per row.
 int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
               Plan* p) {
   const int G = num_heads / num_kv_heads;
   const int64_t TG = (int64_t)q_len * G;
   if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
-  p->n_chunks = (int)((TG + kRows - 1) / kRows);
+  p->streams = env_int("TSFA_STREAMS", 2) == 1 ? 1 : 2;
+  p->rows_per_chunk = kMaxRows / p->streams;
+  p->n_chunks = (int)((TG + p->rows_per_chunk - 1) / p->rows_per_chunk);
   p->n_pu = ceil_div(prefix_len, kUnitKeys);
   int cus = 256;
   if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
@@ -702,7 +744,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
         if (cand > 1 && ceil_div(p->n_pu, cand - 1) == splits) continue;
         const int64_t items = groups * (splits + 1);
         const int64_t rounds = (items + cus - 1) / cus;
-        const double cost = (double)rounds * (t_fixed + ceil_div(cand, kStreams) * t_unit) +
+        const double cost = (double)rounds * (t_fixed + ceil_div(cand, p->streams) * t_unit) +
                             part_bytes * (double)(splits + 1) * 2.0 / 5.0e6;
         if (cost < best * (1.0 - 1e-9)) {
           best = cost;
@@ -724,8 +766,8 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   if (device_max_lds_per_block(&max_lds) != TSFA_OK) return TSFA_ERR_DEVICE;
   p->lds_bytes = head_dim == 128 ? lds_bytes_for<128>() : lds_bytes_for<64>();
   if (p->lds_bytes > (size_t)max_lds) return TSFA_ERR_UNSUPPORTED;
-  p->ring_stages = kRingBytes / kStreams / (2 * kUnitKeys * head_dim * 2);
-  p->vt_max = (int)(kMaskWords / chunk_tokens(G));
+  p->ring_stages = kRingBytes / p->streams / (2 * kUnitKeys * head_dim * 2);
+  p->vt_max = (int)(kMaskWords / chunk_tokens(p->rows_per_chunk, G));
   p->tree_key_limit = kv_len - prefix_len;  // refined by the caller with n_tree_blocks*BN
   const size_t rows = (size_t)batch * num_heads * q_len;
   p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 2);
@@ -733,7 +775,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   return TSFA_OK;
 }
 
-template <typename T, int D>
+template <typename T, int D, int S>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -742,12 +784,12 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((split_kernel<T, D>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
+  hipLaunchKernelGGL((split_kernel<T, D, S>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -758,11 +800,11 @@ thread_local int g_kernel_mask = 3;
 template <typename T, int D>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
-    const int st = launch_split<T, D>(sa, p, stream);
+    const int st = p.streams == 2 ? launch_split<T, D, 2>(sa, p, stream) : launch_split<T, D, 1>(sa, p, stream);
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;
-  const int64_t threads = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group * (D / 8);
+  const int64_t threads = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group * (D / kEpt);
   const unsigned blocks = (unsigned)((threads + 255) / 256);
   hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, ca);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
@@ -790,7 +832,7 @@ extern "C" int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, i
   if (tree_limit > (int64_t)kMaxTreeUnits * kUnitKeys) return TSFA_ERR_UNSUPPORTED;
   // the tree block-state table [q-blocks of a chunk][n_tree_blocks] lives in
   // the LDS ring and the chunk's row_ptr window in the LDS scalars
-  const int64_t nqbc = chunk_qblocks(gqa_group_size, block_m);
+  const int64_t nqbc = chunk_qblocks(kMaxRows, gqa_group_size, block_m);
   if (nqbc * n_tree_blocks * 4 > (int64_t)kRingBytes || nqbc + 1 > kMiscInts - 8) return TSFA_ERR_UNSUPPORTED;
   return TSFA_OK;
 }
@@ -812,7 +854,7 @@ extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_l
   if (st != TSFA_OK) return st;
   out6[0] = p.n_splits;
   out6[1] = p.units_per_split;
-  out6[2] = kRows;
+  out6[2] = p.rows_per_chunk;
   out6[3] = p.n_chunks;
   out6[4] = p.grid;
   out6[5] = p.ring_stages;

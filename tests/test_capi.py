@@ -93,8 +93,8 @@ def test_tree_limits_reported_unsupported():
     # tree keys beyond 32768 (1024 units of 32) and block-state tables larger
     # than the LDS ring are refused, not silently mis-computed
     assert _fwd_check(q_len=40000, kv_len=44096, n_q_blocks=2500, n_tree_blocks=625) == _lib.TSFA_ERR_UNSUPPORTED
-    # 34 q-blocks x 2048 tree blocks x 4 B > 128 KiB
-    assert _fwd_check(q_len=32768, kv_len=36864, block_m=1, n_q_blocks=32768, block_n=16,
-                      n_tree_blocks=2048) == _lib.TSFA_ERR_UNSUPPORTED
+    # a 256-row chunk of G = 4 spans 66 q-blocks of BM = 1: 66 x 512 tree blocks x 4 B > 128 KiB
     assert _fwd_check(q_len=8192, kv_len=12288, block_m=1, n_q_blocks=8192, block_n=16,
-                      n_tree_blocks=512) == _lib.TSFA_OK
+                      n_tree_blocks=512) == _lib.TSFA_ERR_UNSUPPORTED
+    assert _fwd_check(q_len=8192, kv_len=12288, block_m=1, n_q_blocks=8192, block_n=32,
+                      n_tree_blocks=256) == _lib.TSFA_OK
