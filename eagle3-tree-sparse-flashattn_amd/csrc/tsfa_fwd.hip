@@ -142,6 +142,15 @@ __device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t
 
 template <typename V, typename U> __device__ inline V bit_cast(U u) { return __builtin_bit_cast(V, u); }
 
+// max(a, b, c) in one v_max3_f32.  fmaxf would first quiet each operand the
+// compiler cannot prove canonical (an MFMA result), one extra VALU op apiece;
+// scores are never signaling NaNs.
+__device__ inline float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Max / sum over lanes {l, l^32} (one gfx950 row-swap permute, no LDS).
 __device__ inline float pair_max(float x) {
   const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -219,6 +228,7 @@ void split_kernel(const SplitArgs a) {
   constexpr int KSTEPS = D / 16;
   constexpr int DT = D / 32;
   static_assert(S == 1 || S == 2, "streams");
+  static_assert(kWaves == 8, "two waves per SIMD: w and w + 4");
   static_assert(NS >= 4 && (NS & (NS - 1)) == 0 && LPU >= 1 && LPU * (NS - 2) < 64 && LPH % (RG / 2) == 0,
                 "ring geometry");
   static_assert(QS >= 1 && QS < NS && QROWS * ROWB == QS * SB, "Q staging");
@@ -360,18 +370,24 @@ void split_kernel(const SplitArgs a) {
 #pragma unroll
   for (int kk = 0; kk < KSTEPS; ++kk) k_off[kk] = ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4);
 
-  // One 32-key unit for the wave's 32 rows.  S^T row (MFMA m) = key, column =
-  // query row: lane (ln, lh) holds keys 8*(i/4) + 4*lh + i%4 of row ln.  mw is
-  // the 32-bit key visibility of the lane's row (read only when `masked`).
-  auto compute = [&](const unsigned char* sk, bool masked, uint32_t mw) {
-    const unsigned char* sv = sk + HALF;
-    // Every LDS operand read of the unit goes out first (K for S^T, then the
-    // V^T halves for O^T, which land during the softmax), so no MFMA waits on
-    // a read issued just before it.
-    i16x8 kf[KSTEPS];
-    i16x4 vh[DT][2][2];
+  // S^T of one 32-key unit for the wave's 32 rows: MFMA row m = key, column =
+  // query row; lane (ln, lh) holds keys 8*(i/4) + 4*lh + i%4 of row ln.
+  auto read_k = [&](const unsigned char* sk, i16x8 (&kf)[KSTEPS]) {
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) kf[kk] = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
+  };
+  auto qk = [&](const i16x8 (&kf)[KSTEPS]) {
+    f32x16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) s = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[kk]), s);
+    return s;
+  };
+
+  // V^T fragments of one unit (stage base sv): lane i of 16-lane group x gets
+  // keys 16*s2 + 8*jj + 4*(x>>1) + [0,4) of d = dt*32 + 16*(x&1) + i.
+  auto read_v = [&](const unsigned char* sv, i16x4 (&vh)[DT][2][2]) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -380,24 +396,25 @@ void split_kernel(const SplitArgs a) {
         for (int jj = 0; jj < 2; ++jj)
           vh[dt][s2][jj] =
               __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(sv + v_off[dt] + (16 * s2 + 8 * jj) * ROWB));
-    __builtin_amdgcn_sched_barrier(0);
-    f32x16 s;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) s = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[kk]), s);
+  };
+  // Online softmax of one unit's S^T (VALU only): masks the unit's invisible
+  // keys, re-bases (m, l, O) when the running max grows past the lazy
+  // threshold, and leaves P = exp2(s*scale - m) rounded to T in pb.
+  // One wave runs this while the other wave of its SIMD issues MFMAs, so its
+  // dependency chains are exposed: the max and the row sum are trees (depth
+  // 3 and 4), not chains.
+  auto softmax = [&](f32x16& s, bool masked, uint32_t mask, V8 (&pb)[2]) {
     if (masked) {
       // a real (wave-uniform) branch: the empty asm keeps the compiler from
       // speculating the mask into selects that every unmasked unit would pay
       asm volatile("" ::: "memory");
-      const uint32_t w = mw >> (4 * lh);
+      const uint32_t w = mask >> (4 * lh);
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         if (!((w >> (8 * (i >> 2) + (i & 3))) & 1u)) s[i] = -INFINITY;
     }
-    float mx = fmaxf(s[0], s[1]);
-#pragma unroll
-    for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    const float mx = max3f(max3f(max3f(s[0], s[1], s[2]), max3f(s[3], s[4], s[5]), max3f(s[6], s[7], s[8])),
+                           max3f(max3f(s[9], s[10], s[11]), max3f(s[12], s[13], s[14]), s[15]), -INFINITY);
     if (__ballot(mx > m_lim) != 0) {  // false while both are -inf
       const float m_new = fmaxf(m_run, pair_max(mx));
       // alpha = 1 when both are -inf (tree_sparse_flashattn.py:276, :324)
@@ -409,20 +426,24 @@ void split_kernel(const SplitArgs a) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
-    // p = 0 where the score is -inf (tree_sparse_flashattn.py:274, :322): with a
-    // finite reference point exp2(-inf) = 0; a row with no visible key yet keeps
-    // m = -inf and reference 0, so every p there is exp2(-inf) = 0 too.
-    V8 pb[2];
-    float ls = 0.f;
+    // p = 0 where the score is -inf (tree_sparse_flashattn.py:274, :322):
+    // with a finite reference point exp2(-inf) = 0; a row with no visible key
+    // yet keeps m = -inf and reference 0, so p = exp2(-inf) = 0.
+    float p[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -mb));
-      ls += p;
-      pb[i >> 3][i & 7] = (T)p;  // P rounded to the input dtype (:278)
+      p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -mb));
+      pb[i >> 3][i & 7] = (T)p[i];  // P rounded to the input dtype (:278)
     }
-    l_run += ls;
-    // O^T += V^T P^T; k-step s2 covers keys 16*s2 + 8*jj + 4*lh + [0,4), the
-    // order P^T's lane holds them in (elements 8*s2 .. 8*s2+7 of S^T).
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
+    l_run += p[0];
+  };
+  // O^T += V^T P^T; k-step s2 covers keys 16*s2 + 8*jj + 4*lh + [0,4), the
+  // order P^T's lane holds them in (elements 8*s2 .. 8*s2+7 of S^T).
+  auto pv = [&](const i16x4 (&vh)[DT][2][2], const V8 (&pb)[2]) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -433,22 +454,61 @@ void split_kernel(const SplitArgs a) {
   };
 
   // The streams' shares of a run of n units (unit i of the run: key0_of(i),
-  // masked_of(i), mask_of(i)): stream s takes units s, s+S, ...  NS-1 units
-  // are in flight ahead of the one in use (the first `pre` already issued);
-  // one workgroup barrier per step.
+  // masked_of(i), mask_of(i)): stream s takes units s, s+S, ...  One
+  // workgroup barrier per step; units j and j+1 occupy two ring stages, NS-2
+  // more are in flight.  A step of a wave is a VALU phase (the softmax of
+  // unit j) and an MFMA phase (O^T += V^T P^T of unit j, then S^T of unit
+  // j+1).  The two waves of a SIMD (w and w+4) run half a step apart: waves
+  // 4..7 take their VALU phase before the step's barrier, waves 0..3 after
+  // it, so each SIMD has one wave issuing MFMAs while the other issues the
+  // softmax (the MFMA phase runs at raised wave priority).  Both read K of
+  // unit j+1 only after barrier j, and both finish reading unit j-1 before
+  // it, so the barrier still orders the ring.
   auto run_units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + S * j));
+    f32x16 s_cur;
+    if (mine > 0) wait_units<LPU, NS - 2>(min(mine - 1, NS - 2));  // unit 0 landed
+    sync_lds();
+    if (mine > 0 && active) {
+      i16x8 kf[KSTEPS];
+      read_k(sring, kf);
+      s_cur = qk(kf);
+    }
+    const bool late = wave >= 4;  // barrier after the softmax (wave-uniform)
     for (int j = 0; j < steps; ++j) {
-      // unit j landed for every wave of the stream; stage (j-1)%NS is free
-      if (j < mine) wait_units<LPU, NS - 2>(min(mine - 1 - j, NS - 2));
-      sync_lds();
-      if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
-      if (j < mine && active) {
-        const int i = ks + S * j;
-        const bool masked = masked_of(i);
-        compute(sring + (j % NS) * SB, masked, masked ? mask_of(i) : ~0u);
+      const bool work = j < mine && active;
+      const int ui = ks + S * j;
+      // unit j+1 landed for every wave of the stream; stage (j-1)%NS is free
+      auto ring_step = [&]() {
+        if (j + 1 < mine) wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
+        __builtin_amdgcn_sched_barrier(0);
+        sync_lds();
+        __builtin_amdgcn_sched_barrier(0);
+        if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+      };
+      if (!late) ring_step();
+      V8 pb[2];
+      i16x4 vh[DT][2][2];
+      if (work) {
+        read_v(sring + (j % NS) * SB + HALF, vh);
+        softmax(s_cur, masked_of(ui), mask_of(ui), pb);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (late) ring_step();
+      if (work) {
+        // K of unit j+1 after the softmax (its registers are not live there);
+        // the O^T MFMAs cover the read.  On the last step this reads a stale
+        // stage that no load targets; that S^T is never used.
+        i16x8 kf[KSTEPS];
+        read_k(sring + ((j + 1) % NS) * SB, kf);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        pv(vh, pb);
+        s_cur = qk(kf);
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
