@@ -35,12 +35,15 @@
 //   * at the end the two streams' (m, l, O) merge in LDS and the workgroup writes
 //     one partial per row (O/l in the input dtype, fp32 (m, l)); a second
 //     kernel merges the partials (log-sum-exp) and writes O.
+//   * wide_kernel (opt-in) runs the same work items with one wave per SIMD and
+//     64 rows per wave (AGPR accumulators), halving LDS operand bytes per MFMA.
 
 #include <math.h>
 #include <stdlib.h>
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "tsfa_internal.h"
 
@@ -168,8 +171,11 @@ __device__ inline float pair_sum(float x) {
 // Fast path: the lane offset depends on u only through the swizzle, which
 // repeats every NOFF loads, so NOFF precomputed lane offsets and a scalar row
 // base per load address everything.  Slow path (a unit reaching past kv_len):
-// per-lane clamped rows; those keys are masked.
-template <typename T, int D, bool IS_V, int NL>
+// per-lane clamped rows; those keys are masked.  OFF32 addresses the slow
+// path like the fast one (scalar base, 32-bit lane offsets: fewer live VGPRs
+// for the wide kernel); otherwise per-lane 64-bit addresses (the 8-wave
+// kernel measured faster with them).
+template <typename T, int D, bool IS_V, int NL, bool OFF32 = false>
 __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst, int key0, int kv_len, int lane,
                                 int u_lo, const uint32_t* loff) {
   constexpr int CPR = D / 8;
@@ -183,6 +189,18 @@ __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst,
       const int u = u_lo + i;
       dma16_s(rowp, loff[u % NOFF], lds_dst + u * 1024);
       rowp += step;
+    }
+  } else if (OFF32) {
+    // scalar base at row key0; a lane's row is at most 31 rows further and
+    // row strides stay below 2^26 elements, so its byte offset fits 32 bits
+    const char* rowp = reinterpret_cast<const char*>(base + (int64_t)key0 * stride);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int u = u_lo + i;
+      const int row = u * RPL + lane / CPR, pos = lane % CPR;
+      const uint32_t rel = (uint32_t)(min(key0 + row, kv_len - 1) - key0);
+      const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
+      dma16_s(rowp, rel * (uint32_t)stride * 2u + (uint32_t)((pos ^ sw) << 4), lds_dst + u * 1024);
     }
   } else {
 #pragma unroll
@@ -682,6 +700,521 @@ void split_kernel(const SplitArgs a) {
   }
 }
 
+// ------------------------------------------------------------- wide kernel
+// The same work item (a chunk's prefix run or tree units, one partial per row)
+// with one wave per SIMD and 64 query rows per wave (two 32-row tiles):
+//   * each K / V^T fragment read from LDS feeds two MFMAs, half the LDS bytes
+//     per MFMA of 32-row waves; the 128 O^T accumulators per lane fit beside
+//     the operands because a lone wave owns all 512 registers (AGPRs hold O);
+//   * a chunk is 256 rows and one key stream: every K/V unit is staged once
+//     per workgroup, 8 ring stages of 32 keys (D=128);
+//   * iteration j issues O^T += V^T P^T of unit j-1 and S^T of unit j+1 (32
+//     MFMAs) and, between them, the softmax of unit j: the lone wave keeps the
+//     matrix core busy while its VALU works.  The running max moves row by row
+//     without a branch; the rare O rescale waits for the end of the iteration
+//     (after O^T of unit j-1, before that of unit j).
+constexpr int kWideWaves = 4;
+
+template <typename T, int D>
+__global__ __launch_bounds__(kWideWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void wide_kernel(const SplitArgs a) {
+  typedef typename Mma<T>::vec8 V8;
+  constexpr int NW = kWideWaves;
+  constexpr int NT = NW * 64;
+  constexpr int ROWS = 64 * NW;        // rows per chunk
+  constexpr int ROWB = D * 2;          // bytes of one key row
+  constexpr int HALF = kUnitKeys * ROWB;
+  constexpr int SB = 2 * HALF;         // ring stage: K then V of one unit
+  constexpr int NS = kRingBytes / SB;  // stages
+  constexpr int LPH = HALF / 1024;     // 1 KB loads per half
+  constexpr int LPU = 2 * LPH / NW;    // loads per unit per wave
+  constexpr int QS = ROWS * ROWB / SB; // stages the chunk's Q occupies at start
+  constexpr int KSTEPS = D / 16;
+  constexpr int DT = D / 32;
+  static_assert(ROWS == kMaxRows, "chunk rows");
+  static_assert(NS >= 4 && QS < NS && QS * SB == ROWS * ROWB && LPU >= 1 && LPU * (NS - 2) < 64 &&
+                    LPH % (NW / 2) == 0,
+                "ring geometry");
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* ring = smem;
+  uint32_t* masks = reinterpret_cast<uint32_t*>(smem + kRingBytes);
+  int* vis = reinterpret_cast<int*>(masks + kMaskWords);
+  int* misc = vis + kMaxTreeUnits;  // kMiscInts ints
+
+  // An AGPR in use: the MFMAs keep their accumulators in AGPRs (O^T needs
+  // them: 128 per lane beside the VGPR operands).
+  asm volatile("" ::: "a0");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, lh = lane >> 5;
+
+  const int item = (blockIdx.x & 7) * a.items_per_xcd + (blockIdx.x >> 3);
+  if (item >= a.n_items) return;
+  const int chunk = item % a.n_chunks;
+  int rest = item / a.n_chunks;
+  const int slot = rest % a.n_slots;
+  const int bk = rest / a.n_slots;
+  const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
+  const bool is_tree = slot == a.n_slots - 1;
+
+  const int G = a.group;
+  const int TG = a.q_len * G;
+  const int row0 = chunk * ROWS;
+  const int rows_chunk = min(ROWS, TG - row0);
+  const int tok_lo = row0 / G;
+  const float sl2 = a.scale_log2;
+  const float thr_raw = kRescaleLog2 / sl2;
+
+  const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+
+  // Waves 0 .. NW/2-1 move the K half of each unit, the others the V half.
+  const bool dma_v = wave >= NW / 2;
+  const int dma_u0 = (wave % (NW / 2)) * LPU;
+  uint32_t loff[D == 128 ? 4 : 2];
+#pragma unroll
+  for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
+    loff[u] = dma_v ? dma_lane_off<D, true>(u, a.svn, lane) : dma_lane_off<D, false>(u, a.skn, lane);
+  auto issue = [&](int st, int key0) {
+    const uint32_t sb = ring_lds + st * SB;
+    if (dma_v)
+      dma_half<T, D, true, LPU, true>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
+    else
+      dma_half<T, D, false, LPU, true>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
+  };
+
+  // Q^T fragments of the wave's two row tiles: tile t holds row
+  // row0 + wave*64 + t*32 + ln, d = kk*16 + lh*8 + [0, 8).
+  i16x8 qf[2][KSTEPS];
+  const short qsgn = a.neg_q ? (short)0x8000 : (short)0;
+  int row_tt[2];  // token of the lane's row in each tile, chunk-relative
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int qrow = row0 + wave * 64 + t * 32 + ln;
+    row_tt[t] = qrow < TG ? qrow / G - tok_lo : 0;
+  }
+  auto load_q = [&]() {  // straight into registers (rows past the end load zeros)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) qf[t][kk] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
+      const int qrow = row0 + wave * 64 + t * 32 + ln;
+      if (qrow < TG) {
+        const int tq = qrow / G;
+        const int g = qrow - tq * G;
+        const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh +
+                      (int64_t)tq * a.sqm + lh * 8;
+#pragma unroll
+        for (int kk = 0; kk < KSTEPS; ++kk) qf[t][kk] = *reinterpret_cast<const i16x8*>(qp + kk * 16) ^ qsgn;
+      }
+    }
+    // consume the loads here, before any K/V prefetch joins the vmcnt queue
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(qf[t][kk]));
+  };
+  // Q through LDS: the chunk's rows go HBM -> LDS into the last QS stages,
+  // issued ahead of the first K/V units; rows past the end repeat the last
+  // row (their outputs are never stored).
+  auto issue_q = [&]() {
+    constexpr int RPL = 1024 / ROWB, CPR = D / 8;
+    constexpr int QL = ROWS / RPL / NW;  // 1 KB loads per wave
+#pragma unroll
+    for (int i = 0; i < QL; ++i) {
+      const int l0 = (wave * QL + i) * RPL;
+      const int row = l0 + lane / CPR, pos = lane % CPR;
+      const int R = min(row0 + row, TG - 1);
+      const int tq = R / G;
+      const int g = R - tq * G;
+      const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)tq * a.sqm +
+                     ((pos ^ swz_k<D>(row)) << 3);
+      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(ring + (NS - QS) * SB + l0 * ROWB)));
+    }
+  };
+  auto read_q = [&]() {
+    const unsigned char* qs = ring + (NS - QS) * SB;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int r = wave * 64 + t * 32 + ln;
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk)
+        qf[t][kk] = *reinterpret_cast<const i16x8*>(qs + r * ROWB + (((2 * kk + lh) ^ swz_k<D>(r)) << 4)) ^ qsgn;
+    }
+  };
+
+  // Running state per lane and tile (query row ln of the tile): O^T element
+  // i of d-tile dt is d = dt*32 + 8*(i/4) + 4*lh + i%4; l_run is this lane's
+  // half of the row sum.
+  f32x16 o[2][DT];
+  float m_run[2], m_lim[2], mb[2], l_run[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    m_run[t] = -INFINITY;
+    m_lim[t] = -INFINITY;
+    mb[t] = 0.f;
+    l_run[t] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[t][dt][i] = 0.f;
+  }
+
+  const int vx = lane >> 4, vi = lane & 15;
+  const int vkey = 4 * (vx >> 1) + (vi >> 2);
+  int v_off[DT], k_off[KSTEPS];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
+    v_off[dt] = vkey * ROWB + (((d >> 3) ^ swz_v<D>(vkey)) << 4) + ((d & 7) << 1);
+  }
+#pragma unroll
+  for (int kk = 0; kk < KSTEPS; ++kk) k_off[kk] = ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4);
+
+  auto read_k = [&](const unsigned char* sk, i16x8 (&kf)[KSTEPS]) {
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) kf[kk] = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
+  };
+  auto read_v = [&](const unsigned char* sv, i16x4 (&vh)[DT][2][2]) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+          vh[dt][s2][jj] =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(sv + v_off[dt] + (16 * s2 + 8 * jj) * ROWB));
+  };
+  // S^T of one unit for both tiles, tile 0 first: its MFMAs only need tile
+  // 0's scores consumed, so they can run while tile 1's softmax does.
+  auto qk1 = [&](const i16x8 (&kf)[KSTEPS], f32x16& st, int t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) st[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) st = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[t][kk]), st);
+  };
+  auto qk2 = [&](const i16x8 (&kf)[KSTEPS], f32x16 (&s)[2]) {
+    qk1(kf, s[0], 0);
+    qk1(kf, s[1], 1);
+  };
+  // O^T += V^T P^T for both tiles (k-step s2 covers keys 16*s2 + 8*jj + 4*lh
+  // + [0,4), the order P^T's lane holds them in).
+  auto pv1 = [&](const i16x4 (&vh)[DT][2][2], const V8 (&pbt)[2], int t) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
+        o[t][dt] = Mma<T>::run(bit_cast<V8>(vf), pbt[s2], o[t][dt]);
+      }
+  };
+  auto pv2 = [&](const i16x4 (&vh)[DT][2][2], const V8 (&pb)[2][2]) {
+    pv1(vh, pb[0], 0);
+    pv1(vh, pb[1], 1);
+  };
+  auto apply_mask = [&](f32x16& s, uint32_t mask) {
+    const uint32_t w = mask >> (4 * lh);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!((w >> (8 * (i >> 2) + (i & 3))) & 1u)) s[i] = -INFINITY;
+  };
+  // Row statistics of one tile (VALU, no branch): the row max over both lane
+  // halves; when it passes the lazy threshold the row re-bases on it and
+  // alpha scales l now and O at the end of the iteration.
+  auto stats = [&](const f32x16& s, int t, float& alpha) {
+    const float mx = max3f(max3f(max3f(s[0], s[1], s[2]), max3f(s[3], s[4], s[5]), max3f(s[6], s[7], s[8])),
+                           max3f(max3f(s[9], s[10], s[11]), max3f(s[12], s[13], s[14]), s[15]), -INFINITY);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    const float rmax = max3f(__uint_as_float(sw[0]), __uint_as_float(sw[1]), -INFINITY);
+    // rmax > m_lim >= m_run, so a re-based row takes rmax; false while both are -inf
+    const bool need = rmax > m_lim[t];
+    const float m_new = need ? rmax : m_run[t];
+    // m_run = -inf gives alpha = 0 (O and l are still 0) (tree_sparse_flashattn.py:276, :324)
+    alpha = need ? __builtin_amdgcn_exp2f((m_run[t] - m_new) * sl2) : 1.f;
+    m_run[t] = m_new;
+    mb[t] = (m_new == -INFINITY) ? 0.f : m_new * sl2;
+    m_lim[t] = m_new + thr_raw;
+    l_run[t] *= alpha;
+    return need;
+  };
+  // P = exp2(s*scale - m) rounded to T (tree_sparse_flashattn.py:274-278,
+  // :322): masked scores give exp2(-inf) = 0, and so does a row with no
+  // visible key yet (m = -inf, reference 0).
+  auto expo = [&](const f32x16& s, int t, float (&p)[16], int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -mb[t]));
+  };
+  auto sum_cvt = [&](float (&p)[16], int t, V8 (&pbt)[2]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pbt[i >> 3][i & 7] = (T)p[i];
+#pragma unroll
+    for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+      for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
+    l_run[t] += p[0];
+  };
+  // Empty asm that "writes" its operands: the values must exist at this point
+  // (keeps IR passes from sinking a phase's VALU work, whose results are only
+  // read in the next iteration, out of the phase it overlaps).
+  auto pin_f = [&](float (&p)[16], int i0, int i1) {
+#pragma unroll
+    for (int i = i0; i < i1; ++i) asm volatile("" : "+v"(p[i]));
+  };
+  auto pin_pb = [&](V8 (&pbt)[2]) {
+    asm volatile("" : "+v"(pbt[0]));
+    asm volatile("" : "+v"(pbt[1]));
+  };
+  auto pin_v = [&](i16x4 (&vh)[DT][2][2]) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) asm volatile("" : "+v"(vh[dt][s2][jj]));
+  };
+  // One phase of an iteration: NM MFMAs, each followed by up to NV VALU ops.
+  auto interleave = [&](auto nm, auto nv) {
+#pragma unroll
+    for (int g = 0; g < decltype(nm)::value; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, decltype(nv)::value, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // A run of n units (unit i: keys key0_of(i); masked_of(i) / mask_of(i, t)
+  // the visibility of its keys for tile t).  Units pre .. NS-2 are issued
+  // here, the first pre by the caller.
+  auto run_units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
+    for (int j = pre; j < NS - 1 && j < n; ++j) issue(j, key0_of(j));
+    if (n > 0) wait_units<LPU, NS - 2>(min(n - 1, NS - 2));  // unit 0 landed
+    sync_lds();
+    f32x16 s[2];
+    i16x4 vh[DT][2][2];
+    V8 pb[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) pb[t][s2] = bit_cast<V8>(i16x8{0, 0, 0, 0, 0, 0, 0, 0});
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) vh[dt][s2][jj] = i16x4{0, 0, 0, 0};
+    if (n > 0) {
+      i16x8 kf[KSTEPS];
+      read_k(ring, kf);
+      qk2(kf, s);
+      if (masked_of(0)) {
+        asm volatile("" ::: "memory");
+        apply_mask(s[0], mask_of(0, 0));
+        apply_mask(s[1], mask_of(0, 1));
+      }
+    }
+    for (int j = 0; j < n; ++j) {
+      // unit j+1 landed for every wave; stage (j-1)%NS is free
+      if (j + 1 < n) wait_units<LPU, NS - 3>(min(n - 2 - j, NS - 3));
+      __builtin_amdgcn_sched_barrier(0);
+      sync_lds();
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + NS - 1 < n) issue((j + NS - 1) % NS, key0_of(j + NS - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        // K of unit j+1 (on the last step a stale stage that no load targets;
+        // that S^T is never used).  O^T += V^T P^T of unit j-1 (zeros before
+        // the first unit) with the statistics and exponentials of unit j,
+        // then V^T of unit j and S^T of unit j+1 with the rest.
+        // Four phases of 8 MFMAs; every register an MFMA overwrites was
+        // consumed in an earlier phase (P^T of a tile by its O^T MFMAs, the
+        // scores of a tile by its exponentials).
+        constexpr int NM = 2 * DT;
+        i16x8 kf[KSTEPS];
+        float alpha[2], p0[16], p1[16];
+        read_k(ring + ((j + 1) % NS) * SB, kf);
+        pv1(vh, pb[0], 0);
+        const bool need0 = stats(s[0], 0, alpha[0]);
+        const bool need1 = stats(s[1], 1, alpha[1]);
+        expo(s[0], 0, p0, 0, 8);
+        pin_f(p0, 0, 8);
+        interleave(std::integral_constant<int, NM>{}, std::integral_constant<int, 6>{});
+        pv1(vh, pb[1], 1);
+        expo(s[0], 0, p0, 8, 16);
+        sum_cvt(p0, 0, pb[0]);
+        pin_pb(pb[0]);
+        interleave(std::integral_constant<int, NM>{}, std::integral_constant<int, 5>{});
+        qk1(kf, s[0], 0);
+        read_v(ring + (j % NS) * SB + HALF, vh);
+        expo(s[1], 1, p1, 0, 16);
+        pin_f(p1, 0, 16);
+        interleave(std::integral_constant<int, KSTEPS>{}, std::integral_constant<int, 5>{});
+        qk1(kf, s[1], 1);
+        sum_cvt(p1, 1, pb[1]);
+        pin_pb(pb[1]);
+        interleave(std::integral_constant<int, KSTEPS>{}, std::integral_constant<int, 4>{});
+        pin_v(vh);
+        if (__ballot(need0 || need1) != 0) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              f32x16 x = o[t][dt];
+              asm volatile("" : "+v"(x));
+              x *= alpha[t];
+              asm volatile("" : "+v"(x));
+              o[t][dt] = x;
+            }
+        }
+        if (j + 1 < n && masked_of(j + 1)) {
+          asm volatile("" ::: "memory");
+          apply_mask(s[0], mask_of(j + 1, 0));
+          apply_mask(s[1], mask_of(j + 1, 1));
+        }
+      }
+    }
+    if (n > 0) pv2(vh, pb);  // O^T += V^T P^T of the last unit
+  };
+
+  if (!is_tree) {
+    const int P = a.prefix_len;
+    const int u_lo = slot * a.units_per_split;
+    const int n = min(a.units_per_split, a.n_pu - u_lo);
+    auto key0_of = [&](int i) { return (u_lo + i) * kUnitKeys; };
+    // Q and the first NS-QS units leave together; wait for Q only (loads
+    // complete in order), read the fragments, then free Q's stages.
+    const int pre = min(n, NS - QS);
+    issue_q();
+    for (int j = 0; j < pre; ++j) issue(j, key0_of(j));
+    wait_units<LPU, NS - QS>(pre);
+    sync_lds();
+    read_q();
+    sync_lds();
+    run_units(
+        n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
+        [&](int i, int) { return (1u << (P - key0_of(i))) - 1u; });
+  } else {
+    load_q();
+    const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
+    const int tok_hi = (row0 + rows_chunk - 1) / G;
+    const int ntok = tok_hi - tok_lo + 1;
+    const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
+    const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
+    const int32_t* ci = a.col_idx + b * a.ms_col_idx;
+    const int8_t* bt = a.blk_type + b * a.ms_blk_type;
+    const int32_t* pl = a.payload + b * a.ms_payload;
+    const int32_t* of = a.offset + b * a.ms_offset;
+    int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
+    int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
+    auto build_state = [&]() {
+      for (int i = tid; i < nqbc * ntb; i += NT) st[i] = 0;
+      if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
+      sync_lds();
+      const int e_begin = rps[0], e_end = rps[nqbc];
+      for (int e = e_begin + tid; e < e_end; e += NT) {
+        int qq = 0;
+        while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
+        const int tb = ci[e];
+        if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
+      }
+      sync_lds();
+    };
+    build_state();
+    const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
+    for (int i = tid; i < n_tu; i += NT) vis[i] = 0;
+    sync_lds();
+    for (int i = tid; i < nqbc * ntb; i += NT) {
+      if (st[i] != 0) {
+        const int tb = i % ntb;
+        const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
+        for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
+      }
+    }
+    sync_lds();
+    if (wave == 0) {
+      int nv = 0;
+      for (int base = 0; base < n_tu; base += 64) {
+        const int idx = base + lane;
+        const bool f = idx < n_tu && vis[idx] != 0;
+        const uint64_t bal = __ballot(f);
+        const int pre = __popcll(bal & ((1ull << lane) - 1ull));
+        if (f) vis[nv + pre] = idx;
+        nv += __popcll(bal);
+      }
+      if (lane == 0) misc[0] = nv;
+    }
+    sync_lds();
+    const int n_vis = misc[0];
+    for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
+      const int nb = min(a.vt_max, n_vis - vb0);
+      if (vb0 > 0) build_state();
+      for (int it = tid; it < ntok * nb * 2; it += NT) {
+        const int q2 = it & 1, jt = it >> 1;
+        const int j = jt % nb, tt = jt / nb;
+        const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
+        const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
+        uint32_t bits = 0;
+        if (c0 < a.tree_key_limit) {
+          const int tb = c0 / BN;
+          const int e = st[(qb - qb_lo) * ntb + tb];
+          if (e < 0) {
+            bits = 0xffffu;
+          } else if (e > 0) {
+            const int flat = tl * BN + (c0 - tb * BN);
+            bits = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 0xffffu;
+          }
+          const int valid = a.tree_key_limit - c0;
+          if (valid < 16) bits &= (1u << valid) - 1u;
+        }
+        reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
+      }
+      sync_lds();
+      run_units(
+          nb, 0, [&](int i) { return P + vis[vb0 + i] * kUnitKeys; }, [&](int) { return true; },
+          [&](int i, int t) { return masks[row_tt[t] * a.vt_max + i]; });
+      sync_all();  // ring and masks free for the next batch
+    }
+  }
+
+  // Epilogue: each tile's rows normalised and staged in LDS in the input
+  // dtype, then whole rows stored (1 KB per instruction).
+  sync_all();
+  unsigned char* stg = ring;  // [ROWS][D], chunks swizzled
+  const int64_t part_row0 = ((int64_t)bk * a.n_slots + slot) * TG + row0;
+  typedef T T4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float lt = pair_sum(l_run[t]);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;  // empty partial: O = 0, weight 0 in the combine
+    const int r = wave * 64 + t * 32 + ln;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      // one d-tile at a time into VGPRs (keeps the allocator from giving the
+      // accumulators a VGPR home for the whole kernel)
+      f32x16 x = o[t][dt];
+      asm volatile("" : "+v"(x));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        T4 v4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = (T)(x[4 * q + i] * inv);
+        *reinterpret_cast<T4*>(stg + r * ROWB + (((4 * dt + q) ^ swz_k<D>(r)) << 4) + 8 * lh) = v4;
+      }
+    }
+    if (lh == 0 && r < rows_chunk) a.ws_ml[part_row0 + r] = make_float2(m_run[t], lt);
+  }
+  sync_lds();
+  constexpr int CPR = D / 8;
+  T* dst = static_cast<T*>(a.ws_o) + part_row0 * D;
+  for (int idx = tid; idx < rows_chunk * CPR; idx += NT) {
+    const int r = idx / CPR, c = idx % CPR;
+    *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) =
+        *reinterpret_cast<const i16x8*>(stg + r * ROWB + ((c ^ swz_k<D>(r)) << 4));
+  }
+}
+
 // Merge the n_slots partials of every row and write O.  Threads walk the
 // workspace rows in order (coalesced partial loads), kEpt outputs per thread;
 // up to kBatch slots are loaded together (one memory round trip for the
@@ -755,7 +1288,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
 
 // ------------------------------------------------------------------- plan
 struct Plan {
-  int streams, rows_per_chunk;
+  int wide, streams, rows_per_chunk;
   int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages;
   int vt_max, tree_key_limit;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
@@ -773,16 +1306,21 @@ int env_int(const char* name, int dflt) {
 int64_t chunk_tokens(int rows, int group) { return (int64_t)(rows - 1) / group + 2; }
 int64_t chunk_qblocks(int rows, int group, int block_m) { return (chunk_tokens(rows, group) - 1) / block_m + 2; }
 
-// Key streams per workgroup, prefix run length (units per split) and the grid.
-// Two streams (128-row chunks) by default: measured faster than one stream
-// (256-row chunks, each K/V byte reaching one workgroup) on the 8B decode
-// shape, where one stream doubles the Q and partial bytes per row.
+// Kernel, key streams per workgroup, prefix run length (units per split) and
+// the grid.  The 8-wave kernel with two streams of 128-row chunks by default
+// (TSFA_STREAMS=1: one stream, 256-row chunks).  TSFA_WIDE=2 selects the wide
+// kernel (256-row chunks, one wave per SIMD), TSFA_WIDE=1 selects it above
+// 128 rows per (batch, kv head).  On the 8B decode shape the 8-wave kernel
+// measured faster: the short per-workgroup runs (4-8 units of 32 keys) leave
+// the wide kernel's longer Q staging and deeper pipeline unamortised.
 int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
               Plan* p) {
   const int G = num_heads / num_kv_heads;
   const int64_t TG = (int64_t)q_len * G;
   if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
-  p->streams = env_int("TSFA_STREAMS", 2) == 1 ? 1 : 2;
+  const int wide = env_int("TSFA_WIDE", 0);
+  p->wide = wide == 2 || (wide == 1 && TG > kMaxRows / 2);
+  p->streams = p->wide ? 1 : (env_int("TSFA_STREAMS", 2) == 1 ? 1 : 2);
   p->rows_per_chunk = kMaxRows / p->streams;
   p->n_chunks = (int)((TG + p->rows_per_chunk - 1) / p->rows_per_chunk);
   p->n_pu = ceil_div(prefix_len, kUnitKeys);
@@ -796,7 +1334,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
       // Makespan model (microseconds): one workgroup per CU; a workgroup
       // costs a fixed start/finish plus its longest stream; every slot of
       // partials is written once and read once by the combine.
-      const double t_unit = 0.5 * head_dim / 128.0, t_fixed = 1.5;
+      const double t_unit = (p->wide ? 0.6 : 0.5) * head_dim / 128.0, t_fixed = 1.5;
       const double part_bytes = (double)batch * num_heads * q_len * (2.0 * head_dim + 8.0);
       double best = 1e300;
       for (int cand = 1; cand <= p->n_pu; ++cand) {
@@ -853,6 +1391,22 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
+template <typename T, int D>
+int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
+  const uint64_t bit = 1ull << (dev & 63);
+  if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
+      return TSFA_ERR_LAUNCH;
+    attr_set.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  hipLaunchKernelGGL((wide_kernel<T, D>), dim3(p.grid), dim3(kWideWaves * 64), p.lds_bytes, stream, args);
+  return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+}
+
 // Measurement hook (per host thread): which of the two kernels a call
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
@@ -860,7 +1414,9 @@ thread_local int g_kernel_mask = 3;
 template <typename T, int D>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
-    const int st = p.streams == 2 ? launch_split<T, D, 2>(sa, p, stream) : launch_split<T, D, 1>(sa, p, stream);
+    const int st = p.wide           ? launch_wide<T, D>(sa, p, stream)
+                   : p.streams == 2 ? launch_split<T, D, 2>(sa, p, stream)
+                                    : launch_split<T, D, 1>(sa, p, stream);
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;

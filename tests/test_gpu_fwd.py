@@ -95,6 +95,40 @@ def test_cases(case):
     assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
 
 
+# The planner's other kernels, forced through its environment switches: the
+# wide kernel (one wave per SIMD, 64 rows per wave, 256-row chunks) and the
+# 8-wave kernel with one key stream.
+KERNELS = {"wide": {"TSFA_WIDE": "2"}, "one-stream": {"TSFA_WIDE": "0", "TSFA_STREAMS": "1"}}
+
+
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
+@pytest.mark.parametrize("case", [CASES[i] for i in (0, 2, 3, 5, 7, 8)], ids=[f"c{i}" for i in (0, 2, 3, 5, 7, 8)])
+def test_cases_other_kernels(case, kernel, monkeypatch):
+    for key, val in KERNELS[kernel].items():
+        monkeypatch.setenv(key, val)
+    b, hq, hkv, t, p, d, dtype, bm, bn, kind = case
+    print(f"[fwd] {kernel} case {case}", flush=True)
+    rng = np.random.default_rng(t * 31 + p)
+    mask = torch.from_numpy(_tree(kind, t, rng))
+    q, k, v = _qkv(b, hq, hkv, t, p, d, dtype, seed=t + p)
+    out = _run(q, k, v, mask, bm, bn)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
+
+
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
+def test_workload_other_kernels(kernel, monkeypatch):
+    for key, val in KERNELS[kernel].items():
+        monkeypatch.setenv(key, val)
+    w = configs.WORKLOADS["llama3-8b-eagle64-p4096"]
+    print(f"[fwd] {kernel} {w.name}", flush=True)
+    q, k, v = configs.make_qkv(w)
+    mask = configs.make_tree_mask(w)
+    out = _run(q, k, v, mask, w.block_m, w.block_n)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, w.prefix_len), w.dtype)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_per_sequence_trees(dtype):
     b, hq, hkv, t, p, d = 3, 8, 2, 45, 70, 128
