@@ -27,6 +27,8 @@ roofline     = K/V bytes / split-KV kernel duration in real calls, against
                rocprofv3 PMC summary
 cpu_baseline = the fp32 dense+mask oracle (benchmark.py:8-35 restated) on the
                host cores, over a bounded sample of calls
+metadata     = the device metadata build (no host synchronisation), graph and
+               eager, beside the CPU oracle builder
 """
 
 from __future__ import annotations
@@ -86,6 +88,59 @@ def cpu_baseline(w, q, k, v, mask, seconds: float):
         "kind": "port",
         "sample": f"{n} full calls of the fp32 dense+mask oracle on the same inputs (torch CPU, {cores} threads)",
     }
+
+
+def metadata_timing(w, mask_dev, mask_cpu, reps: int = 200):
+    """Device metadata build (tsfa_meta_build via prepare_tree_sparse_metadata_batched):
+    graph-captured (device time) and eager (what a caller pays per call), beside
+    the CPU oracle builder (numpy restatement of tree_sparse_flashattn.py:67-160)."""
+    import torch
+
+    import tree_sparse_flashattn as tsf
+    from oracle import meta_oracle
+
+    build = (lambda: tsf.prepare_tree_sparse_metadata_batched(mask_dev, w.prefix_len, w.block_m, w.block_n))
+    for _ in range(5):
+        build()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        build()
+    b.record()
+    torch.cuda.synchronize()
+    eager_us = a.elapsed_time(b) * 1e3 / reps
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        build()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(reps):
+                build()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    graph_us = a.elapsed_time(b) * 1e3 / reps
+    masks = mask_cpu.numpy()
+    build_cpu = ((lambda: [meta_oracle.build_metadata(m, w.prefix_len, w.block_m, w.block_n) for m in masks])
+                 if masks.ndim == 3 else (lambda: meta_oracle.build_metadata(masks, w.prefix_len, w.block_m, w.block_n)))
+    build_cpu()
+    n = 0
+    t0 = time.perf_counter()
+    while n < 5 or time.perf_counter() - t0 < 1.0:
+        build_cpu()
+        n += 1
+    cpu_us = (time.perf_counter() - t0) / n * 1e6
+    return {"hip_graph_us_per_build": round(graph_us, 3), "hip_eager_us_per_build": round(eager_us, 3),
+            "cpu_oracle_us_per_build": round(cpu_us, 1),
+            "sample": f"{reps} device builds per timing; {n} CPU oracle builds (numpy, 1 thread)"}
 
 
 def calibrate_copy(mib: int, reps: int):
@@ -228,7 +283,10 @@ def main():
             "combine_kernel_us": round(secs["combine"] * 1e6, 3),
         },
         "cpu_baseline": None,
+        "metadata": None,
     }
+    _log("[bench] metadata build ...")
+    result["metadata"] = metadata_timing(w, mask.to(dev), mask)
     if not args.no_cpu_baseline:
         _log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, q, k, v, mask, args.cpu_seconds)

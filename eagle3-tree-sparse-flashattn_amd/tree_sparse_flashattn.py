@@ -13,15 +13,16 @@ Public API (reference citations):
   block_sparse_tree_fwd_kernel[grid](...)  tree_sparse_flashattn.py:163-339
 Extensions (no reference counterpart):
   BatchedTreeSparseMetadata / prepare_tree_sparse_metadata_batched: one tree
-  per sequence; slice b is bit-identical to prepare_tree_sparse_metadata of
-  tree b.
+  per sequence (or one tree broadcast over the batch) in capacity layout,
+  built without a host synchronisation; slice b is bit-identical to
+  prepare_tree_sparse_metadata of tree b.
   tree_sparse_attention_fwd: allocate O and launch with either record.
 """
 
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import List, Optional
 
 import torch
@@ -60,11 +61,15 @@ class TreeSparseMetadata:
 
 @dataclass
 class BatchedTreeSparseMetadata:
-    """One tree per sequence, in capacity layout (cap = n_q_blocks*n_tree_blocks).
+    """Trees in capacity layout (cap = n_q_blocks*n_tree_blocks), on the device.
 
-    row_ptr [B, n_q_blocks+1]; col_idx, blk_type, mixed_mask_offset [B, cap];
-    mixed_mask_payload [B, cap*W]; nnz[b] / n_mixed[b] entries of sequence b are
-    valid.  ``sequence(b)`` returns the reference-shaped record of tree b.
+    row_ptr [S, n_q_blocks+1]; col_idx, blk_type, mixed_mask_offset [S, cap];
+    mixed_mask_payload [S, cap*W]; counts [S, 2] int32 = (nnz, n_mixed) of
+    each tree, left on the device: the forward reads only the entries below
+    row_ptr[n_q_blocks], so building and using the record never waits for the
+    host.  S is the batch (one tree per sequence) or 1 (one tree for every
+    sequence).  ``nnz`` / ``n_mixed`` read the counts back on first use;
+    ``sequence(b)`` returns the reference-shaped record of tree b.
     """
 
     row_ptr: torch.Tensor
@@ -72,17 +77,34 @@ class BatchedTreeSparseMetadata:
     blk_type: torch.Tensor
     mixed_mask_payload: torch.Tensor
     mixed_mask_offset: torch.Tensor
-    nnz: List[int]
-    n_mixed: List[int]
+    counts: torch.Tensor
     n_q_blocks: int
     n_tree_blocks: int
     block_m: int
     block_n: int
     prefix_len: int
+    _host_counts: Optional[List[List[int]]] = field(default=None, repr=False, compare=False)
+
+    @property
+    def n_trees(self) -> int:
+        return self.row_ptr.shape[0]
 
     @property
     def words_per_block(self) -> int:
         return (self.block_m * self.block_n + 31) // 32
+
+    def _counts(self) -> List[List[int]]:
+        if self._host_counts is None:
+            self._host_counts = [[int(x) for x in row] for row in self.counts.cpu().tolist()]
+        return self._host_counts
+
+    @property
+    def nnz(self) -> List[int]:
+        return [c[0] for c in self._counts()]
+
+    @property
+    def n_mixed(self) -> List[int]:
+        return [c[1] for c in self._counts()]
 
     def sequence(self, b: int) -> TreeSparseMetadata:
         nnz, nmx, w = self.nnz[b], self.n_mixed[b], self.words_per_block
@@ -204,19 +226,22 @@ def prepare_tree_sparse_metadata_batched(
     BLOCK_M: int,
     BLOCK_N: int,
 ) -> BatchedTreeSparseMetadata:
-    """Per-sequence metadata for [B, q_len, q_len] masks, built in one launch."""
+    """Metadata for [S, q_len, q_len] masks (one tree per sequence), or for one
+    [q_len, q_len] mask shared by the whole batch (S = 1), in one launch and
+    without a host synchronisation (the record stays in capacity layout)."""
+    if tree_masks.ndim == 2:
+        tree_masks = tree_masks.unsqueeze(0)
     if tree_masks.ndim != 3 or tree_masks.shape[1] != tree_masks.shape[2]:
-        raise ValueError("tree_masks must be shape [batch, q_len, q_len].")
+        raise ValueError("tree_masks must be shape [batch, q_len, q_len] or [q_len, q_len].")
     if BLOCK_M <= 0 or BLOCK_N <= 0:
         raise ValueError("BLOCK_M and BLOCK_N must be positive.")
     dev = _hip_device(tree_masks)
     masks = _masks_u8(tree_masks, dev)
     row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N, dev)
-    cnt = counts.cpu()
     return BatchedTreeSparseMetadata(
         row_ptr=row_ptr, col_idx=col_idx, blk_type=blk_type, mixed_mask_payload=payload,
-        mixed_mask_offset=offset, nnz=[int(x) for x in cnt[:, 0]], n_mixed=[int(x) for x in cnt[:, 1]],
-        n_q_blocks=nqb, n_tree_blocks=ntb, block_m=BLOCK_M, block_n=BLOCK_N, prefix_len=prefix_len)
+        mixed_mask_offset=offset, counts=counts, n_q_blocks=nqb, n_tree_blocks=ntb, block_m=BLOCK_M,
+        block_n=BLOCK_N, prefix_len=prefix_len)
 
 
 def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_strides, strides, sm_scale,
@@ -296,7 +321,8 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """O = tree-sparse attention of q [B,Hq,T,D] over k/v [B,Hkv,P+T,D].
 
     ``meta`` is a TreeSparseMetadata (one tree for the whole batch) or a
-    BatchedTreeSparseMetadata (one tree per sequence), already on q's device.
+    BatchedTreeSparseMetadata (one tree per sequence, or one tree for every
+    sequence), already on q's device.
     """
     q, k, v = _row_contig(q), _row_contig(k), _row_contig(v)
     bsz, n_heads, q_len, head_dim = q.shape
@@ -306,10 +332,10 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(head_dim)
     if isinstance(meta, BatchedTreeSparseMetadata):
-        if meta.row_ptr.shape[0] != bsz:
-            raise ValueError("batched metadata must have one tree per sequence")
+        if meta.n_trees not in (1, bsz):
+            raise ValueError("batched metadata must have one tree per sequence, or one tree for all")
         tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
-        meta_strides = tuple(t.stride(0) for t in tensors)
+        meta_strides = tuple(t.stride(0) for t in tensors) if meta.n_trees > 1 else (0, 0, 0, 0, 0)
     else:
         tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
         meta_strides = (0, 0, 0, 0, 0)
