@@ -30,6 +30,9 @@ cpu_baseline = the fp32 dense+mask oracle (benchmark.py:8-35 restated) on the
                host cores, over a bounded sample of calls
 metadata     = the device metadata build (no host synchronisation), graph and
                eager, beside the CPU oracle builder
+paged        = the same forward reading FlashInfer's paged cache in place
+               (page_size 16, scattered pages), its rate beside the
+               contiguous call's
 """
 
 from __future__ import annotations
@@ -152,6 +155,51 @@ def metadata_timing(w, mask_dev, mask_cpu, reps: int = 200):
             "sample": f"{reps} device builds per timing; {n} CPU oracle builds (numpy, 1 thread)"}
 
 
+def paged_timing(w, qd, ks, vs, meta, steps: int, page_size: int, contiguous_us: float):
+    """The same forward over FlashInfer's paged cache ([pages, 2, page_size, Hkv, D],
+    benchmark.py:67-91) with each sequence's pages scattered in seeded random
+    order, read in place by tree_sparse_attention_fwd_paged: graph of `steps`
+    calls cycling the same number of cache copies as the contiguous timing."""
+    import torch
+
+    import tree_sparse_flashattn as tsf
+    from tsfa import configs
+
+    caches = [configs.make_paged_kv(k, v, page_size, seed=i) for i, (k, v) in enumerate(zip(ks, vs))]
+    out = torch.empty_like(qd)
+
+    def call(i):
+        cache, indptr, indices = caches[i % len(caches)]
+        tsf.tree_sparse_attention_fwd_paged(qd, cache, indices, meta, kv_len=w.kv_len, kv_indptr=indptr, out=out)
+
+    for i in range(5):
+        call(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call(0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                call(i)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps
+    del caches
+    return {"page_size": page_size, "layout": "NHD", "pages": "scattered (seeded permutation), CSR page lists",
+            "us_per_call": round(us, 3), "value": round(w.kv_bytes() / (us * 1e-6) / 1e12, 4), "unit": "TB/s",
+            "vs_contiguous": round(contiguous_us / us, 4)}
+
+
 def calibrate_copy(mib: int, reps: int):
     """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -173,6 +221,8 @@ def main():
     ap.add_argument("--cold-mib", type=int, default=512, help="K/V bytes cycled through (defeats the MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--paged-page-size", type=int, default=16,
+                    help="also time the paged-cache forward at this page size (0: skip)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (rocprofv3 PMC calibration) and exit")
     args = ap.parse_args()
@@ -300,9 +350,14 @@ def main():
         },
         "cpu_baseline": None,
         "metadata": None,
+        "paged": None,
     }
     _log("[bench] metadata build ...")
     result["metadata"] = metadata_timing(w, mask.to(dev), mask)
+    if args.paged_page_size > 0:
+        _log(f"[bench] paged cache, page_size {args.paged_page_size} ...")
+        del regions
+        result["paged"] = paged_timing(w, qd, ks, vs, meta, steps, args.paged_page_size, per_call_s * 1e6)
     if not args.no_cpu_baseline:
         _log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, q, k, v, mask, args.cpu_seconds)

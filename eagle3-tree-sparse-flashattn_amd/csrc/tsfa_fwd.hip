@@ -78,6 +78,14 @@ struct SplitArgs {
   int vt_max;          // tree units per mask batch
   void* ws_o;          // [B*Hkv][n_slots][q_len*G][D] partial O / l in the input dtype
   float2* ws_ml;       // [B*Hkv][n_slots][q_len*G] (m, l) of each partial
+  // Paged K/V (split_kernel<..., PAGED = true> only; k and v unused).
+  const void* kv_cache;
+  const int32_t* kv_indptr;   // [B + 1] page-list offsets into kv_indices, or null
+  const int32_t* kv_indices;  // page ids
+  int64_t pt_stride;          // kv_indptr null: sequence b's list starts at b * pt_stride
+  int64_t n_indices;          // entries of kv_indices
+  int64_t cps, css, crs, chs; // cache strides (elements): page, K/V slot, row, kv head
+  int page_shift, n_pages;
 };
 
 struct CombineArgs {
@@ -214,6 +222,60 @@ __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst,
   }
 }
 
+// Paged K/V (FlashInfer's [pages, 2, page_size, Hkv, D] cache, the serving
+// layout of benchmark.py:67-91, or any other strides): key `key` of sequence
+// b lives in page list[key >> page_shift] at row key & (page_size - 1), K in
+// slot 0 and V in slot 1 of the page.  The page list of sequence b starts at
+// kv_indices[kv_indptr[b]] (CSR, FlashInfer's form) or, without kv_indptr,
+// at kv_indices[b * pt_stride] (a dense [B, pages] table).  Page-table reads
+// go through the scalar cache (the addresses are wave-uniform) and are
+// clamped, index and page id both, so no table content can send a load out
+// of the cache.
+__device__ inline int ld_uniform(const int32_t* p, int64_t i) {
+  typedef const __attribute__((address_space(4))) int32_t CI;
+  return ((CI*)p)[i];
+}
+__device__ inline int64_t page_id(const SplitArgs& a, int64_t pt_base, int pg) {
+  const int64_t i = min(max(pt_base + pg, (int64_t)0), a.n_indices - 1);
+  return (int64_t)min(max(ld_uniform(a.kv_indices, i), 0), a.n_pages - 1);
+}
+
+// dma_half over the paged cache (hbase: the kv head's K or V at page 0, row
+// 0).  The loads of one wave cover NL*RPL <= 16 consecutive keys, so with
+// pages of 16 keys or more they touch at most two pages: two page-table
+// reads, then each 1 KB load takes a scalar row base when its RPL rows sit
+// in one page below kv_len (the lane offsets of the contiguous fast path,
+// built from the cache's row stride, apply unchanged) and per-lane clamped
+// addresses otherwise (a load straddling a page boundary, or reaching past
+// kv_len: those keys are masked).
+template <typename T, int D, bool IS_V, int NL>
+__device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_t pt_base, uint32_t lds_dst,
+                                      int key0, int lane, int u_lo, const uint32_t* loff) {
+  constexpr int CPR = D / 8;
+  constexpr int RPL = 64 / CPR;
+  constexpr int NOFF = IS_V ? 1 : (D == 128 ? 4 : 2);
+  static_assert(NL * RPL <= 16, "a wave's share of a unit spans at most two pages of 16+ keys");
+  const int kv_len = a.kv_len, ps = a.page_shift, pmask = (1 << ps) - 1;
+  const int kw = key0 + u_lo * RPL;  // first key of the wave's share
+  const int pg0 = min(kw, kv_len - 1) >> ps;
+  const int pg1 = min(kw + NL * RPL - 1, kv_len - 1) >> ps;
+  const int64_t pid0 = page_id(a, pt_base, pg0), pid1 = page_id(a, pt_base, pg1);
+  auto row_ptr = [&](int64_t pid, int key) { return hbase + pid * a.cps + (int64_t)(key & pmask) * a.crs; };
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int u = u_lo + i;
+    const int r0 = kw + i * RPL;  // first key of this load
+    if (r0 + RPL <= kv_len && (r0 & pmask) + RPL <= pmask + 1) {
+      dma16_s(row_ptr((r0 >> ps) == pg0 ? pid0 : pid1, r0), loff[u % NOFF], lds_dst + u * 1024);
+    } else {
+      const int row = u * RPL + lane / CPR, pos = lane % CPR;
+      const int key = min(key0 + row, kv_len - 1);
+      const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
+      dma16(row_ptr((key >> ps) == pg0 ? pid0 : pid1, key) + ((pos ^ sw) << 3), lds_dst + u * 1024);
+    }
+  }
+}
+
 // Lane offsets (bytes from the load's first key row) of dma_half's fast path.
 template <int D, bool IS_V> __device__ inline uint32_t dma_lane_off(int u, int64_t stride, int lane) {
   constexpr int CPR = D / 8;
@@ -228,7 +290,7 @@ template <int D> constexpr size_t lds_bytes_for() {
 }
 
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.
-template <typename T, int D, int S>
+template <typename T, int D, int S, bool PAGED>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
@@ -285,8 +347,13 @@ void split_kernel(const SplitArgs a) {
   const float sl2 = a.scale_log2;
   const float thr_raw = kRescaleLog2 / sl2;  // re-base the running max past 2^8 growth
 
-  const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
-  const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  const T* kbase = PAGED ? static_cast<const T*>(a.kv_cache) + kvh * a.chs
+                        : static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
+  const T* vbase = PAGED ? kbase + a.css : static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  const int64_t kstride = PAGED ? a.crs : a.skn, vstride = PAGED ? a.crs : a.svn;
+  int64_t pt_base = 0;  // sequence b's page list in kv_indices
+  if (PAGED)
+    pt_base = a.kv_indptr ? (int64_t)ld_uniform(a.kv_indptr, b) : (int64_t)b * a.pt_stride;
   unsigned char* sring = ring + ks * RB;
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
 
@@ -297,16 +364,22 @@ void split_kernel(const SplitArgs a) {
   uint32_t loff[D == 128 ? 4 : 2];
 #pragma unroll
   for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
-    loff[u] = dma_v ? dma_lane_off<D, true>(u, a.svn, lane) : dma_lane_off<D, false>(u, a.skn, lane);
+    loff[u] = dma_v ? dma_lane_off<D, true>(u, vstride, lane) : dma_lane_off<D, false>(u, kstride, lane);
 
   // HBM -> LDS: this wave's share of one unit (keys key0 .. key0+31) into
   // stage st of its stream's ring.
   auto issue = [&](int st, int key0) {
     const uint32_t sb = sring_lds + st * SB;
-    if (dma_v)
+    if (PAGED) {
+      if (dma_v)
+        dma_half_paged<T, D, true, LPU>(vbase, a, pt_base, sb + HALF, key0, lane, dma_u0, loff);
+      else
+        dma_half_paged<T, D, false, LPU>(kbase, a, pt_base, sb, key0, lane, dma_u0, loff);
+    } else if (dma_v) {
       dma_half<T, D, true, LPU>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
-    else
+    } else {
       dma_half<T, D, false, LPU>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
+    }
   };
 
   // Q^T operand fragments of the wave's row tile: row r = row0 + rg*32 + ln,
@@ -1373,7 +1446,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   return TSFA_OK;
 }
 
-template <typename T, int D, int S>
+template <typename T, int D, int S, bool PAGED>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -1382,12 +1455,12 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((split_kernel<T, D, S>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
+  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -1411,12 +1484,13 @@ int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
 
-template <typename T, int D>
+// The paged forward always runs the 8-wave split kernel.
+template <typename T, int D, bool PAGED>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
-    const int st = p.wide           ? launch_wide<T, D>(sa, p, stream)
-                   : p.streams == 2 ? launch_split<T, D, 2>(sa, p, stream)
-                                    : launch_split<T, D, 1>(sa, p, stream);
+    const int st = (p.wide && !PAGED) ? launch_wide<T, D>(sa, p, stream)
+                   : p.streams == 2   ? launch_split<T, D, 2, PAGED>(sa, p, stream)
+                                      : launch_split<T, D, 1, PAGED>(sa, p, stream);
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;
@@ -1477,30 +1551,64 @@ extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_l
   return TSFA_OK;
 }
 
-extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, const int32_t* row_ptr,
-                        const int32_t* col_idx, const int8_t* blk_type, const int32_t* mixed_mask_payload,
-                        const int32_t* mixed_mask_offset, const int64_t* meta_seq_stride, const int64_t* strides,
-                        float sm_scale, int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
-                        int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size, int block_m,
-                        int block_n, int head_dim, int dtype, void* workspace, size_t workspace_bytes,
-                        tsfa_stream_t stream_) {
+namespace {
+
+// K/V of one call: contiguous per-head tensors, or the paged cache.
+struct KvSource {
+  const void* k = nullptr;
+  const void* v = nullptr;
+  const int64_t* k_strides = nullptr;  // [4]: b, h, n, d
+  const int64_t* v_strides = nullptr;
+  const void* cache = nullptr;  // paged: [pages, 2, page_size, Hkv, D] by cache_strides
+  const int64_t* cache_strides = nullptr;  // [5]: page, slot, row, head, d
+  const int32_t* kv_indptr = nullptr;
+  const int32_t* kv_indices = nullptr;
+  int64_t pt_stride = 0, n_indices = 0;
+  int n_pages = 0, page_size = 0;
+  bool paged() const { return cache != nullptr; }
+};
+
+int fwd_impl(const void* q, const KvSource& kv, void* o, const int32_t* row_ptr, const int32_t* col_idx,
+             const int8_t* blk_type, const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+             const int64_t* meta_seq_stride, const int64_t* q_strides, const int64_t* o_strides, float sm_scale,
+             int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int n_q_blocks,
+             int n_tree_blocks, int gqa_group_size, int block_m, int block_n, int head_dim, int dtype,
+             void* workspace, size_t workspace_bytes, tsfa_stream_t stream_) {
   int st = tsfa_fwd_check_args(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
                                n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype);
   if (st != TSFA_OK) return st;
   if (batch == 0 || q_len == 0) return TSFA_OK;
-  if (strides == nullptr || meta_seq_stride == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
-  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || row_ptr == nullptr)
+  if (q_strides == nullptr || o_strides == nullptr || meta_seq_stride == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  if (q == nullptr || o == nullptr || row_ptr == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  if (kv.paged() ? (kv.cache_strides == nullptr || kv.kv_indices == nullptr)
+                 : (kv.k == nullptr || kv.v == nullptr || kv.k_strides == nullptr || kv.v_strides == nullptr))
     return TSFA_ERR_INVALID_ARGUMENT;
-  for (int i = 0; i < 4; ++i) {
-    if (strides[4 * i + 3] != 1) return TSFA_ERR_UNSUPPORTED;  // contiguous head_dim
-    for (int j = 0; j < 3; ++j)
-      if (strides[4 * i + j] % 8 != 0) return TSFA_ERR_UNSUPPORTED;  // 16-byte aligned rows
+  // contiguous head_dim, 16-byte aligned rows and bases
+  auto rows_ok = [](const int64_t* sd, int n) {
+    if (sd[n - 1] != 1) return false;
+    for (int j = 0; j < n - 1; ++j)
+      if (sd[j] % 8 != 0) return false;
+    return true;
+  };
+  auto aligned = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+  if (!rows_ok(q_strides, 4) || !rows_ok(o_strides, 4) || !aligned(q) || !aligned(o)) return TSFA_ERR_UNSUPPORTED;
+  if (kv.paged()) {
+    if (!rows_ok(kv.cache_strides, 5) || !aligned(kv.cache)) return TSFA_ERR_UNSUPPORTED;
+    if (kv.cache_strides[2] >= ((int64_t)1 << 26)) return TSFA_ERR_UNSUPPORTED;  // 32-bit lane offsets
+    // pages of 16 keys or more, a power of two: a wave's 16-key DMA share
+    // then spans at most two pages
+    if (kv.page_size < 16 || (kv.page_size & (kv.page_size - 1)) != 0) return TSFA_ERR_UNSUPPORTED;
+    if (kv.pt_stride < 0 || (kv_len > 0 && (kv.n_pages <= 0 || kv.n_indices <= 0))) return TSFA_ERR_INVALID_ARGUMENT;
+    // a dense page table holds every sequence's ceil(kv_len / page_size) pages
+    if (kv.kv_indptr == nullptr && kv_len > 0 &&
+        (int64_t)(batch - 1) * kv.pt_stride + ceil_div(kv_len, kv.page_size) > kv.n_indices)
+      return TSFA_ERR_INVALID_ARGUMENT;
+  } else {
+    if (!rows_ok(kv.k_strides, 4) || !rows_ok(kv.v_strides, 4) || !aligned(kv.k) || !aligned(kv.v))
+      return TSFA_ERR_UNSUPPORTED;
+    // K/V row strides must keep a 32-bit lane offset of 8 rows
+    if (kv.k_strides[2] >= ((int64_t)1 << 26) || kv.v_strides[2] >= ((int64_t)1 << 26)) return TSFA_ERR_UNSUPPORTED;
   }
-  // K/V row strides must keep a 32-bit lane offset of 8 rows
-  if (strides[6] >= ((int64_t)1 << 26) || strides[10] >= ((int64_t)1 << 26)) return TSFA_ERR_UNSUPPORTED;
-  const void* ptrs[4] = {q, k, v, o};
-  for (const void* ptr : ptrs)
-    if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0) return TSFA_ERR_UNSUPPORTED;
   for (int i = 0; i < 5; ++i)
     if (meta_seq_stride[i] < 0) return TSFA_ERR_INVALID_ARGUMENT;
 
@@ -1511,10 +1619,8 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   if (workspace == nullptr || workspace_bytes < p.ws_acc_bytes + p.ws_ml_bytes) return TSFA_ERR_WORKSPACE;
   if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return TSFA_ERR_WORKSPACE;
 
-  SplitArgs sa;
+  SplitArgs sa = {};
   sa.q = q;
-  sa.k = k;
-  sa.v = v;
   sa.row_ptr = row_ptr;
   sa.col_idx = col_idx;
   sa.blk_type = blk_type;
@@ -1525,15 +1631,33 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   sa.ms_blk_type = meta_seq_stride[2];
   sa.ms_payload = meta_seq_stride[3];
   sa.ms_offset = meta_seq_stride[4];
-  sa.sqb = strides[0];
-  sa.sqh = strides[1];
-  sa.sqm = strides[2];
-  sa.skb = strides[4];
-  sa.skh = strides[5];
-  sa.skn = strides[6];
-  sa.svb = strides[8];
-  sa.svh = strides[9];
-  sa.svn = strides[10];
+  sa.sqb = q_strides[0];
+  sa.sqh = q_strides[1];
+  sa.sqm = q_strides[2];
+  if (kv.paged()) {
+    sa.kv_cache = kv.cache;
+    sa.kv_indptr = kv.kv_indptr;
+    sa.kv_indices = kv.kv_indices;
+    sa.pt_stride = kv.pt_stride;
+    sa.n_indices = kv.n_indices;
+    sa.cps = kv.cache_strides[0];
+    sa.css = kv.cache_strides[1];
+    sa.crs = kv.cache_strides[2];
+    sa.chs = kv.cache_strides[3];
+    sa.n_pages = kv.n_pages;
+    int shift = 0;
+    while ((1 << shift) < kv.page_size) ++shift;
+    sa.page_shift = shift;
+  } else {
+    sa.k = kv.k;
+    sa.v = kv.v;
+    sa.skb = kv.k_strides[0];
+    sa.skh = kv.k_strides[1];
+    sa.skn = kv.k_strides[2];
+    sa.svb = kv.v_strides[0];
+    sa.svh = kv.v_strides[1];
+    sa.svn = kv.v_strides[2];
+  }
   // Scores enter the exponent as s * |sm_scale| * log2(e) with Q negated for a
   // negative scale; a zero scale becomes a vanishing one (every visible p = 1
   // and masked keys still get p = 0).
@@ -1562,9 +1686,9 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
 
   CombineArgs ca;
   ca.o = o;
-  ca.sob = strides[12];
-  ca.soh = strides[13];
-  ca.som = strides[14];
+  ca.sob = o_strides[0];
+  ca.soh = o_strides[1];
+  ca.som = o_strides[2];
   ca.scale_log2 = sa.scale_log2;
   ca.batch = batch;
   ca.num_heads = num_heads;
@@ -1576,9 +1700,59 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   ca.ws_ml = sa.ws_ml;
 
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
-  if (dtype == TSFA_DTYPE_BF16)
-    return head_dim == 128 ? launch_all<__bf16, 128>(sa, ca, p, stream) : launch_all<__bf16, 64>(sa, ca, p, stream);
-  return head_dim == 128 ? launch_all<_Float16, 128>(sa, ca, p, stream) : launch_all<_Float16, 64>(sa, ca, p, stream);
+  const bool bf = dtype == TSFA_DTYPE_BF16, d128 = head_dim == 128;
+  if (kv.paged()) {
+    if (bf) return d128 ? launch_all<__bf16, 128, true>(sa, ca, p, stream) : launch_all<__bf16, 64, true>(sa, ca, p, stream);
+    return d128 ? launch_all<_Float16, 128, true>(sa, ca, p, stream) : launch_all<_Float16, 64, true>(sa, ca, p, stream);
+  }
+  if (bf) return d128 ? launch_all<__bf16, 128, false>(sa, ca, p, stream) : launch_all<__bf16, 64, false>(sa, ca, p, stream);
+  return d128 ? launch_all<_Float16, 128, false>(sa, ca, p, stream) : launch_all<_Float16, 64, false>(sa, ca, p, stream);
+}
+
+}  // namespace
+
+extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, const int32_t* row_ptr,
+                        const int32_t* col_idx, const int8_t* blk_type, const int32_t* mixed_mask_payload,
+                        const int32_t* mixed_mask_offset, const int64_t* meta_seq_stride, const int64_t* strides,
+                        float sm_scale, int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                        int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size, int block_m,
+                        int block_n, int head_dim, int dtype, void* workspace, size_t workspace_bytes,
+                        tsfa_stream_t stream_) {
+  KvSource kv;
+  kv.k = k;
+  kv.v = v;
+  kv.k_strides = strides ? strides + 4 : nullptr;
+  kv.v_strides = strides ? strides + 8 : nullptr;
+  return fwd_impl(q, kv, o, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset, meta_seq_stride,
+                  strides, strides ? strides + 12 : nullptr, sm_scale, batch, num_heads, num_kv_heads, q_len,
+                  kv_len, prefix_len, n_q_blocks, n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype,
+                  workspace, workspace_bytes, stream_);
+}
+
+extern "C" int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, int64_t n_indices, int64_t page_table_stride, int n_pages,
+                              int page_size, void* o, const int32_t* row_ptr, const int32_t* col_idx,
+                              const int8_t* blk_type, const int32_t* mixed_mask_payload,
+                              const int32_t* mixed_mask_offset, const int64_t* meta_seq_stride,
+                              const int64_t* q_strides, const int64_t* cache_strides, const int64_t* o_strides,
+                              float sm_scale, int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                              int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size, int block_m,
+                              int block_n, int head_dim, int dtype, void* workspace, size_t workspace_bytes,
+                              tsfa_stream_t stream_) {
+  if (kv_cache == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  KvSource kv;
+  kv.cache = kv_cache;
+  kv.cache_strides = cache_strides;
+  kv.kv_indptr = kv_indptr;
+  kv.kv_indices = kv_indices;
+  kv.n_indices = n_indices;
+  kv.pt_stride = page_table_stride;
+  kv.n_pages = n_pages;
+  kv.page_size = page_size;
+  return fwd_impl(q, kv, o, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset, meta_seq_stride,
+                  q_strides, o_strides, sm_scale, batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
+                  n_q_blocks, n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype, workspace,
+                  workspace_bytes, stream_);
 }
 
 extern "C" int tsfa_fwd_set_kernel_mask(int mask) {

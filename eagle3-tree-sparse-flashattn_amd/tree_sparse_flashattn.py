@@ -17,6 +17,9 @@ Extensions (no reference counterpart):
   built without a host synchronisation; slice b is bit-identical to
   prepare_tree_sparse_metadata of tree b.
   tree_sparse_attention_fwd: allocate O and launch with either record.
+  tree_sparse_attention_fwd_paged: the same forward over a paged K/V cache
+  (FlashInfer's [pages, 2, page_size, Hkv, D] layout, benchmark.py:67-91)
+  with per-sequence page lists, read in place.
 """
 
 from __future__ import annotations
@@ -316,6 +319,17 @@ def _row_contig(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _meta_arrays(meta, bsz: int):
+    """The five metadata arrays and their per-sequence strides (0: one tree for all)."""
+    tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
+    if isinstance(meta, BatchedTreeSparseMetadata):
+        if meta.n_trees not in (1, bsz):
+            raise ValueError("batched metadata must have one tree per sequence, or one tree for all")
+        if meta.n_trees > 1:
+            return tensors, tuple(t.stride(0) for t in tensors)
+    return tensors, (0, 0, 0, 0, 0)
+
+
 def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta, *,
                               sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """O = tree-sparse attention of q [B,Hq,T,D] over k/v [B,Hkv,P+T,D].
@@ -331,15 +345,100 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out = torch.empty_like(q)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(head_dim)
-    if isinstance(meta, BatchedTreeSparseMetadata):
-        if meta.n_trees not in (1, bsz):
-            raise ValueError("batched metadata must have one tree per sequence, or one tree for all")
-        tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
-        meta_strides = tuple(t.stride(0) for t in tensors) if meta.n_trees > 1 else (0, 0, 0, 0, 0)
-    else:
-        tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
-        meta_strides = (0, 0, 0, 0, 0)
+    tensors, meta_strides = _meta_arrays(meta, bsz)
     strides = (*q.stride(), *k.stride(), *v.stride(), *out.stride())
     return _launch_fwd(q, k, v, out, *tensors, meta_strides, strides, sm_scale, bsz, n_heads, n_kv_heads, q_len,
                        kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, n_heads // n_kv_heads,
                        meta.block_m, meta.block_n, head_dim)
+
+
+def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_indices: torch.Tensor, meta, *,
+                                    kv_len: int, kv_indptr: Optional[torch.Tensor] = None,
+                                    kv_layout: str = "NHD", sm_scale: Optional[float] = None,
+                                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """tree_sparse_attention_fwd with K/V read in place from a paged cache.
+
+    kv_cache: [pages, 2, page_size, Hkv, D] (kv_layout "NHD": FlashInfer's
+        default, the cache benchmark.py:67-91 builds) or [pages, 2, Hkv,
+        page_size, D] ("HND"); slot 0 holds K, slot 1 V.  page_size must be
+        a power of two >= 16.
+    kv_indices / kv_indptr: FlashInfer's page lists -- sequence b's pages are
+        kv_indices[kv_indptr[b]:kv_indptr[b + 1]] (int32, kv_indptr [B + 1]);
+        without kv_indptr, kv_indices is a dense int32 [B, pages_per_seq]
+        table.  Key j of sequence b is row j % page_size of its page
+        j // page_size.
+    kv_len: keys of every sequence (prefix_len + tree tokens).
+    The metadata, scale and output are those of tree_sparse_attention_fwd;
+    O equals tree_sparse_attention_fwd over the gathered [B, Hkv, kv_len, D]
+    K/V bit for bit.  Page ids outside the cache and list positions outside
+    kv_indices are clamped in the kernel (wrong O, never an invalid read).
+    """
+    q = _row_contig(q)
+    bsz, n_heads, q_len, head_dim = q.shape
+    if kv_cache.dim() != 5 or kv_cache.shape[1] != 2:
+        raise ValueError("kv_cache must be [pages, 2, page_size, Hkv, D] (NHD) or [pages, 2, Hkv, page_size, D] (HND)")
+    if kv_layout == "NHD":
+        n_pages, _, page_size, n_kv_heads, kv_dim = kv_cache.shape
+        cache_strides = tuple(kv_cache.stride())
+    elif kv_layout == "HND":
+        n_pages, _, n_kv_heads, page_size, kv_dim = kv_cache.shape
+        sp, ss, sh, sr, sd = kv_cache.stride()
+        cache_strides = (sp, ss, sr, sh, sd)
+    else:
+        raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
+    if kv_dim != head_dim:
+        raise ValueError(f"kv_cache head_dim {kv_dim} != q head_dim {head_dim}")
+    if n_kv_heads <= 0 or n_heads % n_kv_heads:
+        raise ValueError("num_heads must be a multiple of the cache's kv heads")
+    if page_size < 16 or page_size & (page_size - 1):
+        raise NotImplementedError(f"page_size must be a power of two >= 16, got {page_size}")
+    if kv_indices.dtype != torch.int32 or (kv_indptr is not None and kv_indptr.dtype != torch.int32):
+        raise ValueError("kv_indices and kv_indptr must be int32")
+    if kv_len < meta.prefix_len:
+        raise ValueError("kv_len must be >= prefix_len")
+    pages_per_seq = -(-kv_len // page_size)
+    if kv_indptr is None:
+        if kv_indices.dim() != 2 or kv_indices.shape[0] != bsz or kv_indices.shape[1] < pages_per_seq:
+            raise ValueError(f"a dense page table must be [{bsz}, >= {pages_per_seq}] int32")
+        if kv_indices.stride(1) != 1:
+            kv_indices = kv_indices.contiguous()
+        pt_stride = kv_indices.stride(0)
+    else:
+        if kv_indptr.dim() != 1 or kv_indptr.numel() != bsz + 1:
+            raise ValueError(f"kv_indptr must be int32 [{bsz + 1}]")
+        kv_indptr, kv_indices = kv_indptr.contiguous(), kv_indices.contiguous().view(-1)
+        pt_stride = 0
+    if kv_indices.numel() == 0 and bsz > 0 and kv_len > 0:
+        raise ValueError("kv_indices is empty")
+    if out is None:
+        out = torch.empty_like(q)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    tensors, meta_strides = _meta_arrays(meta, bsz)
+
+    lib = _lib.load()
+    for name, t in (("q", q), ("kv_cache", kv_cache), ("o", out), ("kv_indices", kv_indices)):
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a HIP device tensor")
+    dev = q.device
+    for name, t in (("kv_cache", kv_cache), ("kv_indices", kv_indices), ("kv_indptr", kv_indptr),
+                    ("row_ptr", tensors[0]), ("col_idx", tensors[1]), ("blk_type", tensors[2]),
+                    ("mixed_mask_payload", tensors[3]), ("mixed_mask_offset", tensors[4])):
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} must be on {dev}")
+    if not (q.dtype == kv_cache.dtype == out.dtype):
+        raise NotImplementedError("q, kv_cache and o must share one dtype")
+    dt = _lib.dtype_code(q.dtype)
+    args = (bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks,
+            n_heads // n_kv_heads, meta.block_m, meta.block_n, head_dim, dt)
+    _lib.check("tree_sparse_attention_fwd_paged", lib.tsfa_fwd_check_args(*args))
+    ws_bytes = lib.tsfa_fwd_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, head_dim)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        st = lib.tsfa_fwd_paged(
+            _lib.ptr(q), _lib.ptr(kv_cache), _lib.ptr(kv_indptr), _lib.ptr(kv_indices), kv_indices.numel(),
+            pt_stride, n_pages, page_size, _lib.ptr(out), *(_lib.ptr(t) for t in tensors),
+            _lib.i64_array(meta_strides), _lib.i64_array(q.stride()), _lib.i64_array(cache_strides),
+            _lib.i64_array(out.stride()), float(sm_scale), *args, _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
+    _lib.check("tree_sparse_attention_fwd_paged", st)
+    return out

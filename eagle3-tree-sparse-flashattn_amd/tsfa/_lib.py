@@ -36,6 +36,7 @@ EXPORTS = (
     "tsfa_fwd_check_args",
     "tsfa_fwd_workspace_bytes",
     "tsfa_fwd",
+    "tsfa_fwd_paged",
     "tsfa_fwd_plan",
     "tsfa_fwd_set_kernel_mask",
 )
@@ -55,6 +56,9 @@ _SIGNATURES = {
     "tsfa_fwd": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                           ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
+    "tsfa_fwd_paged": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp,
+                                _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]
+                       + [ctypes.POINTER(_c_i64)] * 4 + [_c_float] + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
     "tsfa_fwd_plan": (_c_int, [_c_int] * 7 + [ctypes.POINTER(ctypes.c_int32)]),
     "tsfa_fwd_set_kernel_mask": (_c_int, [_c_int]),
 }

@@ -103,3 +103,38 @@ def make_qkv(w: Workload, seed: int = 42, device="cpu"):
     k = torch.randn((w.batch, w.kv_heads, w.kv_len, w.head_dim), generator=g, dtype=torch.float32)
     v = torch.randn((w.batch, w.kv_heads, w.kv_len, w.head_dim), generator=g, dtype=torch.float32)
     return tuple(x.to(w.dtype).to(device) for x in (q, k, v))
+
+
+def make_paged_kv(k: torch.Tensor, v: torch.Tensor, page_size: int, *, layout: str = "NHD", seed=None,
+                  spare_pages: int = 0, dense_table: bool = False):
+    """K/V [B,Hkv,L,D] laid into FlashInfer's paged cache, as benchmark.py:67-91 builds it.
+
+    Returns (cache, kv_indptr, kv_indices): cache [pages, 2, page_size, Hkv, D]
+    ("NHD") or [pages, 2, Hkv, page_size, D] ("HND"), K in slot 0 and V in
+    slot 1, rows past L in a sequence's last page zero.  Sequence b owns
+    ceil(L / page_size) pages; with ``seed`` the pages are scattered over the
+    pool in a seeded random order (plus ``spare_pages`` never referenced),
+    otherwise sequence b holds pages b*n .. b*n + n - 1 as in the reference.
+    kv_indptr is None and kv_indices a [B, n] table with ``dense_table``.
+    """
+    bsz, hkv, kv_len, d = k.shape
+    n = -(-kv_len // page_size)
+    total = bsz * n + spare_pages
+    if seed is None:
+        order = torch.arange(total, dtype=torch.int64)
+    else:
+        order = torch.randperm(total, generator=torch.Generator().manual_seed(seed))
+    ids = order[: bsz * n].view(bsz, n)
+    shape = (total, 2, page_size, hkv, d) if layout == "NHD" else (total, 2, hkv, page_size, d)
+    cache = torch.zeros(shape, dtype=k.dtype, device=k.device)
+    pad = n * page_size - kv_len
+    for slot, x in ((0, k), (1, v)):
+        xs = torch.nn.functional.pad(x, (0, 0, 0, pad))  # [B, Hkv, n*ps, D]
+        xs = xs.view(bsz, hkv, n, page_size, d)
+        xs = xs.permute(0, 2, 3, 1, 4) if layout == "NHD" else xs.permute(0, 2, 1, 3, 4)
+        cache[ids.reshape(-1).to(k.device), slot] = xs.reshape(bsz * n, *shape[2:])
+    kv_indices = ids.to(torch.int32).to(k.device)
+    if dense_table:
+        return cache, None, kv_indices
+    kv_indptr = (torch.arange(bsz + 1, dtype=torch.int32) * n).to(k.device)
+    return cache, kv_indptr, kv_indices.reshape(-1).contiguous()

@@ -119,6 +119,44 @@ int tsfa_fwd(const void* q, const void* k, const void* v, void* o,
              int block_m, int block_n, int head_dim, int dtype,
              void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
 
+/* tsfa_fwd over a paged K/V cache.  No counterpart in the reference's tree
+ * kernel (it reads contiguous [B, Hkv, kv_len, D] tensors); it replaces the
+ * gather a serving caller would otherwise run to turn its page pool into
+ * that layout -- the FlashInfer cache that benchmark.py:67-91 builds
+ * ([max_pages, 2, page_size, Hkv, D]) and hands to the paged decode
+ * wrapper with indptr/indices (benchmark.py:114-133).  Same semantics and
+ * metadata as tsfa_fwd, with key j of sequence b read from page
+ * list_b[j / page_size], row j % page_size (K in slot 0, V in slot 1):
+ *
+ * kv_cache       pages of `dtype`, addressed by cache_strides
+ * cache_strides  int64[5] in elements: page, K/V slot, row in page, kv head,
+ *                d (d stride 1).  [pages, 2, page_size, Hkv, D] contiguous
+ *                is FlashInfer's NHD layout; HND ([pages, 2, Hkv,
+ *                page_size, D]) is the same call with the row and head
+ *                strides swapped
+ * kv_indptr      int32[batch + 1]: list_b = kv_indices[kv_indptr[b] ...]
+ *                (FlashInfer's CSR form), or NULL for a dense table:
+ *                list_b = kv_indices[b * page_table_stride ...]
+ * kv_indices     int32 page ids, n_indices entries; list_b must hold
+ *                ceil(kv_len / page_size) ids
+ * n_pages        pages in kv_cache; page ids and list positions are clamped
+ *                to the pool and to kv_indices, so no table content reads
+ *                outside them (a bad table gives wrong O, never a fault)
+ * page_size      keys per page: a power of two, >= 16
+ * q_strides, o_strides  int64[4] each: b, h, n, d
+ * Every sequence has kv_len keys (prefix_len + tree), as in tsfa_fwd. */
+int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr,
+                   const int32_t* kv_indices, int64_t n_indices, int64_t page_table_stride,
+                   int n_pages, int page_size, void* o,
+                   const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
+                   const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+                   const int64_t* meta_seq_stride, const int64_t* q_strides,
+                   const int64_t* cache_strides, const int64_t* o_strides, float sm_scale,
+                   int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
+                   int n_q_blocks, int n_tree_blocks, int gqa_group_size,
+                   int block_m, int block_n, int head_dim, int dtype,
+                   void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
+
 /* Work decomposition tsfa_fwd would use (for reports and tests):
  * out[0] = prefix splits per (batch, kv head, row chunk), out[1] = prefix
  * units (32 keys) per split, out[2] = query rows (token x head of a GQA

@@ -98,3 +98,31 @@ def test_tree_limits_reported_unsupported():
                       n_tree_blocks=512) == _lib.TSFA_ERR_UNSUPPORTED
     assert _fwd_check(q_len=8192, kv_len=12288, block_m=1, n_q_blocks=8192, block_n=32,
                       n_tree_blocks=256) == _lib.TSFA_OK
+
+
+def _paged_call(page_size=16, n_pages=8, n_indices=16, pt_stride=4, indptr=None, cache=0x1000, **kw):
+    """tsfa_fwd_paged with fake (aligned, never dereferenced) device pointers:
+    every case here is refused on the host before any device work."""
+    args = dict(FWD_OK)
+    args.update(kw)
+    fake = 0x2000
+    ms = (ctypes.c_int64 * 5)()
+    qs = (ctypes.c_int64 * 4)(4096 * 128 * 32, 64 * 128, 128, 1)
+    cs = (ctypes.c_int64 * 5)(2 * page_size * 8 * 128, page_size * 8 * 128, 8 * 128, 128, 1)
+    return _lib.load().tsfa_fwd_paged(fake, cache, indptr, fake, n_indices, pt_stride, n_pages, page_size, fake,
+                                      fake, fake, fake, fake, fake, ms, qs, cs, qs, ctypes.c_float(0.1),
+                                      *args.values(), fake, 1 << 30, None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(page_size=8), _lib.TSFA_ERR_UNSUPPORTED),          # a wave's 16-key share would span 3 pages
+    (dict(page_size=48), _lib.TSFA_ERR_UNSUPPORTED),         # not a power of two
+    (dict(cache=None), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(n_pages=0), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(pt_stride=-1), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    # dense table: sequence 0 needs ceil(4160 / 16) = 260 ids, 16 are given
+    (dict(), _lib.TSFA_ERR_INVALID_ARGUMENT),
+    (dict(head_dim=96), _lib.TSFA_ERR_UNSUPPORTED),
+])
+def test_fwd_paged_rejects_on_host(kw, status):
+    assert _paged_call(**kw) == status
