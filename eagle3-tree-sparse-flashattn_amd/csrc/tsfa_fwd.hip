@@ -82,9 +82,9 @@ struct SplitArgs {
   const void* kv_cache;
   const int32_t* kv_indptr;   // [B + 1] page-list offsets into kv_indices, or null
   const int32_t* kv_indices;  // page ids
-  int64_t pt_stride;          // kv_indptr null: sequence b's list starts at b * pt_stride
-  int64_t n_indices;          // entries of kv_indices
   int64_t cps, css, crs, chs; // cache strides (elements): page, K/V slot, row, kv head
+  int pt_stride;              // kv_indptr null: sequence b's list starts at b * pt_stride
+  int n_indices;              // entries of kv_indices (< 2^31)
   int page_shift, n_pages;
 };
 
@@ -235,32 +235,53 @@ __device__ inline int ld_uniform(const int32_t* p, int64_t i) {
   typedef const __attribute__((address_space(4))) int32_t CI;
   return ((CI*)p)[i];
 }
-__device__ inline int64_t page_id(const SplitArgs& a, int64_t pt_base, int pg) {
-  const int64_t i = min(max(pt_base + pg, (int64_t)0), a.n_indices - 1);
-  return (int64_t)min(max(ld_uniform(a.kv_indices, i), 0), a.n_pages - 1);
+// Pages of a wave's DMA share of the unit at key0 (keys kw .. kw + 15, kw =
+// key0 + u_lo*RPL, clamped to kv_len - 1): list positions pg0 <= pg1 <= pg0+1.
+template <int D, int NL>
+__device__ inline void share_pages(const SplitArgs& a, int key0, int u_lo, int& pg0, int& pg1) {
+  constexpr int RPL = 64 / (D / 8);
+  const int kw = key0 + u_lo * RPL;
+  pg0 = min(kw, a.kv_len - 1) >> a.page_shift;
+  pg1 = min(kw + NL * RPL - 1, a.kv_len - 1) >> a.page_shift;
 }
+// Raw page-table entry at list position pg (position clamped to kv_indices,
+// which the host keeps below 2^31 entries).
+__device__ inline int page_entry(const SplitArgs& a, int pt_base, int pg) {
+  return ld_uniform(a.kv_indices, min(max(pt_base + pg, 0), a.n_indices - 1));
+}
+__device__ inline int64_t clamp_page(const SplitArgs& a, int raw) { return (int64_t)min(max(raw, 0), a.n_pages - 1); }
 
 // dma_half over the paged cache (hbase: the kv head's K or V at page 0, row
-// 0).  The loads of one wave cover NL*RPL <= 16 consecutive keys, so with
-// pages of 16 keys or more they touch at most two pages: two page-table
-// reads, then each 1 KB load takes a scalar row base when its RPL rows sit
-// in one page below kv_len (the lane offsets of the contiguous fast path,
-// built from the cache's row stride, apply unchanged) and per-lane clamped
-// addresses otherwise (a load straddling a page boundary, or reaching past
-// kv_len: those keys are masked).
+// 0; pid0/pid1: the pages at list positions pg0/pg1 of share_pages).  The
+// loads of one wave cover NL*RPL <= 16 consecutive keys, so with pages of
+// 16 keys or more they touch at most two pages.  A share inside one page and
+// below kv_len (every prefix unit with page_size >= 16) is addressed like
+// the contiguous fast path: one scalar row base, the lane offsets built from
+// the cache's row stride.  Otherwise each 1 KB load takes a scalar base when
+// its RPL rows sit in one page below kv_len and per-lane clamped addresses
+// when it straddles a page boundary or reaches past kv_len (those keys are
+// masked).
 template <typename T, int D, bool IS_V, int NL>
-__device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_t pt_base, uint32_t lds_dst,
-                                      int key0, int lane, int u_lo, const uint32_t* loff) {
+__device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_t pid0, int64_t pid1, int pg0,
+                                      uint32_t lds_dst, int key0, int lane, int u_lo, const uint32_t* loff) {
   constexpr int CPR = D / 8;
   constexpr int RPL = 64 / CPR;
   constexpr int NOFF = IS_V ? 1 : (D == 128 ? 4 : 2);
   static_assert(NL * RPL <= 16, "a wave's share of a unit spans at most two pages of 16+ keys");
   const int kv_len = a.kv_len, ps = a.page_shift, pmask = (1 << ps) - 1;
   const int kw = key0 + u_lo * RPL;  // first key of the wave's share
-  const int pg0 = min(kw, kv_len - 1) >> ps;
-  const int pg1 = min(kw + NL * RPL - 1, kv_len - 1) >> ps;
-  const int64_t pid0 = page_id(a, pt_base, pg0), pid1 = page_id(a, pt_base, pg1);
   auto row_ptr = [&](int64_t pid, int key) { return hbase + pid * a.cps + (int64_t)(key & pmask) * a.crs; };
+  if (kw + NL * RPL <= kv_len && (kw & pmask) + NL * RPL <= pmask + 1) {
+    const char* rowp = reinterpret_cast<const char*>(row_ptr(pid0, kw));
+    const int64_t step = (int64_t)RPL * a.crs * 2;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int u = u_lo + i;
+      dma16_s(rowp, loff[u % NOFF], lds_dst + u * 1024);
+      rowp += step;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int u = u_lo + i;
@@ -351,9 +372,8 @@ void split_kernel(const SplitArgs a) {
                         : static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
   const T* vbase = PAGED ? kbase + a.css : static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
   const int64_t kstride = PAGED ? a.crs : a.skn, vstride = PAGED ? a.crs : a.svn;
-  int64_t pt_base = 0;  // sequence b's page list in kv_indices
-  if (PAGED)
-    pt_base = a.kv_indptr ? (int64_t)ld_uniform(a.kv_indptr, b) : (int64_t)b * a.pt_stride;
+  int pt_base = 0;  // sequence b's page list in kv_indices (b * pt_stride < n_indices by the host check)
+  if (PAGED) pt_base = a.kv_indptr ? ld_uniform(a.kv_indptr, b) : b * a.pt_stride;
   unsigned char* sring = ring + ks * RB;
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
 
@@ -366,15 +386,38 @@ void split_kernel(const SplitArgs a) {
   for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
     loff[u] = dma_v ? dma_lane_off<D, true>(u, vstride, lane) : dma_lane_off<D, false>(u, kstride, lane);
 
+  // Paged: the raw page-table entries of the next unit this wave issues,
+  // read one step early (prefetch) so their scalar loads land behind the
+  // step's compute.  A lookup is a function of key0 alone, so a stale or
+  // missing prefetch only costs a fresh lookup.
+  int pf_key = -1, pf_raw0 = 0, pf_raw1 = 0;
+  auto prefetch = [&](int key0) {
+    if (PAGED) {
+      int pg0, pg1;
+      share_pages<D, LPU>(a, key0, dma_u0, pg0, pg1);
+      pf_key = key0;
+      pf_raw0 = page_entry(a, pt_base, pg0);
+      pf_raw1 = page_entry(a, pt_base, pg1);
+    }
+  };
+
   // HBM -> LDS: this wave's share of one unit (keys key0 .. key0+31) into
   // stage st of its stream's ring.
   auto issue = [&](int st, int key0) {
     const uint32_t sb = sring_lds + st * SB;
     if (PAGED) {
+      int pg0, pg1;
+      share_pages<D, LPU>(a, key0, dma_u0, pg0, pg1);
+      int raw0 = pf_raw0, raw1 = pf_raw1;
+      if (key0 != pf_key) {
+        raw0 = page_entry(a, pt_base, pg0);
+        raw1 = page_entry(a, pt_base, pg1);
+      }
+      const int64_t pid0 = clamp_page(a, raw0), pid1 = clamp_page(a, raw1);
       if (dma_v)
-        dma_half_paged<T, D, true, LPU>(vbase, a, pt_base, sb + HALF, key0, lane, dma_u0, loff);
+        dma_half_paged<T, D, true, LPU>(vbase, a, pid0, pid1, pg0, sb + HALF, key0, lane, dma_u0, loff);
       else
-        dma_half_paged<T, D, false, LPU>(kbase, a, pt_base, sb, key0, lane, dma_u0, loff);
+        dma_half_paged<T, D, false, LPU>(kbase, a, pid0, pid1, pg0, sb, key0, lane, dma_u0, loff);
     } else if (dma_v) {
       dma_half<T, D, true, LPU>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
     } else {
@@ -559,6 +602,7 @@ void split_kernel(const SplitArgs a) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + S * j));
+    if (PAGED && NS - 1 < mine) prefetch(key0_of(ks + S * (NS - 1)));
     f32x16 s_cur;
     if (mine > 0) wait_units<LPU, NS - 2>(min(mine - 1, NS - 2));  // unit 0 landed
     sync_lds();
@@ -578,6 +622,7 @@ void split_kernel(const SplitArgs a) {
         sync_lds();
         __builtin_amdgcn_sched_barrier(0);
         if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+        if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
       };
       if (!late) ring_step();
       V8 pb[2];
@@ -1598,7 +1643,9 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, const int32_t* row_ptr,
     // pages of 16 keys or more, a power of two: a wave's 16-key DMA share
     // then spans at most two pages
     if (kv.page_size < 16 || (kv.page_size & (kv.page_size - 1)) != 0) return TSFA_ERR_UNSUPPORTED;
-    if (kv.pt_stride < 0 || (kv_len > 0 && (kv.n_pages <= 0 || kv.n_indices <= 0))) return TSFA_ERR_INVALID_ARGUMENT;
+    if (kv.pt_stride < 0 || kv.n_indices > INT32_MAX || kv.pt_stride > INT32_MAX ||
+        (kv_len > 0 && (kv.n_pages <= 0 || kv.n_indices <= 0)))
+      return TSFA_ERR_INVALID_ARGUMENT;
     // a dense page table holds every sequence's ceil(kv_len / page_size) pages
     if (kv.kv_indptr == nullptr && kv_len > 0 &&
         (int64_t)(batch - 1) * kv.pt_stride + ceil_div(kv_len, kv.page_size) > kv.n_indices)
@@ -1638,8 +1685,8 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, const int32_t* row_ptr,
     sa.kv_cache = kv.cache;
     sa.kv_indptr = kv.kv_indptr;
     sa.kv_indices = kv.kv_indices;
-    sa.pt_stride = kv.pt_stride;
-    sa.n_indices = kv.n_indices;
+    sa.pt_stride = (int)kv.pt_stride;
+    sa.n_indices = (int)kv.n_indices;
     sa.cps = kv.cache_strides[0];
     sa.css = kv.cache_strides[1];
     sa.crs = kv.cache_strides[2];
