@@ -1,0 +1,743 @@
+// Tree-sparse attention backward for gfx950 (MI355X).
+//
+// The reference has no backward (README.md:198 lists it as missing).  This is
+// the gradient of the function its forward computes
+// (block_sparse_tree_fwd_kernel, tree_sparse_flashattn.py:163-339): with
+// z = sm_scale * q.k over a row's visible keys (the dense prefix [0, P) and the
+// tree keys its CSR row marks), P = softmax(z), O = P V,
+//   dV = P^T dO,  dP = dO V^T,  dS = P * (dP - rowsum(dO * O)),
+//   dQ = sm_scale * dS K,  dK = sm_scale * dS^T Q,
+// summed over the G query heads of each kv head.  P is recomputed from the
+// forward's per-row log-sum-exp (tsfa_fwd_lse).
+//
+// Kernels (one call = four launches, no host synchronisation):
+//   * bwd_prep_kernel: per query row (16 lanes): Dv = rowsum(dO * O) in fp32,
+//     the log2-domain LSE, and the row of the fp32 dQ accumulator cleared.
+//     Rows with no visible key (LSE = -inf) and the padding rows of the last
+//     32-row tile get LSE = +inf and Dv = 0, so their P and dS are exactly 0;
+//   * bwd_vis_kernel: per (32-row tile, tree key) a visibility word (bit m:
+//     row 32*tile + m sees the key), from the CSR metadata;
+//   * bwd_kv_kernel (key-parallel): a workgroup owns 128 keys of one (batch,
+//     kv head) -- prefix keys and tree keys in separate blocks -- as 4 waves x
+//     32 keys, keeps dK^T and dV^T of its keys in registers and walks every
+//     32-row tile of the (batch, kv head) (rows token-major, r = t*G + g, as
+//     in the forward).  Per tile, on v_mfma_f32_32x32x16:
+//       S = Q K^T and dP = dO V^T (a lane holds one key, so the LSE / Dv of
+//       a row are per-element LDS reads and the key's mask word is one read),
+//       dV^T += dO^T P and dK^T += Q^T dS with P and dS taken straight from
+//       the S / dP accumulators (the MFMA k order is permuted to the order
+//       the accumulator holds rows in; the dO^T / Q^T operands come from
+//       ds_read_b64_tr_b16 in the same order), then dQ^T = K^T dS^T over the
+//       workgroup's 128 keys (dS through LDS, one d-tile per wave) added to
+//       the fp32 accumulator with global atomics.  Q / dO tiles, their row
+//       statistics and the tree block's mask words move HBM -> LDS with
+//       global_load_lds, double-buffered; one LDS copy of each tile serves
+//       both the row reads of S / dP and the transposed reads of dV / dK
+//       (a swizzle that is conflict-free for both patterns);
+//   * bwd_dq_kernel: dQ = sm_scale * accumulator in the input dtype.
+
+#include <math.h>
+
+#include <algorithm>
+#include <atomic>
+
+#include "tsfa_internal.h"
+
+namespace tsfa {
+namespace bwd {
+
+constexpr int kWaves = 4;                 // 32 keys each
+constexpr int kBlockKeys = 32 * kWaves;   // keys per workgroup
+constexpr int kTileRows = 32;             // query rows per tile
+constexpr int kMaxStateInts = 8192;       // block-state table of one tile (bwd_vis_kernel)
+
+// 16-byte-chunk XOR swizzle of a row-major [rows][D] LDS tile (row period
+// 16), conflict-free for both read patterns of the kernel:
+//   * row reads (ds_read_b128, a quarter-wave reads chunk c of 16 rows): the
+//     16 rows land on 16 distinct 16-byte bank slots;
+//   * transposed reads (ds_read_b64_tr_b16, a half-wave reads 4 consecutive
+//     rows x 64 bytes): the 4 rows land on 4 distinct 64-byte bank windows.
+template <int D> __device__ inline int swz(int row) {
+  if constexpr (D == 128) {
+    return ((row & 3) << 2) | ((row >> 2) & 3);
+  } else {
+    const int j = row >> 1;
+    return ((j & 1) << 2) | ((j >> 1) & 3);
+  }
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; the clobber documents the write
+// 16 bytes per active lane HBM -> LDS: lane i's bytes land at lds_base + 16*i.
+__device__ inline void dma16(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_base)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ inline void vm_wait0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const TSFA_LDS void*)p; }
+template <typename V, typename U> __device__ inline V bit_cast(U u) { return __builtin_bit_cast(V, u); }
+
+struct BwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* dout;
+  void* dk;
+  void* dv;
+  float* dq_acc;            // [B*Hkv][TG][D] fp32
+  const float2* rowstat;    // [B*Hkv][n_tiles*32] (log2 LSE, Dv)
+  const uint32_t* vis;      // [n_trees][n_tiles][n_tkeys] visibility words of tree keys
+  int64_t sqb, sqh, sqm, skb, skh, skn, svb, svh, svn, sdob, sdoh, sdom, sdkb, sdkh, sdkn, sdvb, sdvh, sdvn;
+  int64_t vis_tree_stride;  // 0: one tree for the batch
+  float scale_log2;         // |sm_scale| * log2(e), never 0
+  float dk_scale;           // |sm_scale| (Q enters negated for a negative scale)
+  int neg_q;
+  int num_kv_heads, group, q_len, kv_len, prefix_len;
+  int n_tiles, n_pb, n_tb, n_tkeys;
+  int n_items, items_per_xcd;
+};
+
+template <int D> constexpr size_t kv_lds_bytes() {
+  // K block | 2 x (Q tile, dO tile) | 2 x 32 row stats | 2 x 128 mask words | dS [128 keys][32 rows]
+  return (size_t)kBlockKeys * D * 2 + 4 * (size_t)kTileRows * D * 2 + 2 * kTileRows * 8 + 2 * kBlockKeys * 4 +
+         (size_t)kBlockKeys * kTileRows * 2;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void bwd_kv_kernel(const BwdArgs a) {
+  typedef typename Mma<T>::vec8 V8;
+  constexpr int ROWB = D * 2;                 // bytes of one row
+  constexpr int KSTEPS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  constexpr int RPL = 64 / CPR;               // rows per 1 KB load
+  constexpr int TILE_B = kTileRows * ROWB;
+  constexpr int KBLK_B = kBlockKeys * ROWB;
+  constexpr int LPT = TILE_B / 1024;          // 1 KB loads per Q (or dO) tile
+  constexpr int TPW = 2 * LPT / kWaves;       // tile loads per wave
+  constexpr int KPW = KBLK_B / 1024 / kWaves; // K block loads per wave
+  static_assert(TPW >= 1 && KPW >= 1 && 2 * LPT == TPW * kWaves, "load split");
+  static_assert(DT <= kWaves, "one dQ d-tile per wave");
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* kblk = smem;
+  unsigned char* tiles = kblk + KBLK_B;  // buffer s: Q at tiles + 2*s*TILE_B, dO right after
+  float2* rs = reinterpret_cast<float2*>(tiles + 4 * TILE_B);
+  uint32_t* visw = reinterpret_cast<uint32_t*>(rs + 2 * kTileRows);
+  unsigned char* dsl = reinterpret_cast<unsigned char*>(visw + 2 * kBlockKeys);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, lh = lane >> 5;
+
+  // XCD-aware item order: consecutive block ids go to different XCDs and each
+  // XCD gets a contiguous item range, so the key blocks of one (b, kv head),
+  // which read the same Q / dO tiles, share an L2.
+  const int item = (blockIdx.x & 7) * a.items_per_xcd + (blockIdx.x >> 3);
+  if (item >= a.n_items) return;
+  const int nkb = a.n_pb + a.n_tb;
+  const int kb = item % nkb;
+  const int bk = item / nkb;
+  const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
+  const bool tree_blk = kb >= a.n_pb;
+  const int tkb = kb - a.n_pb;
+  const int key0 = tree_blk ? a.prefix_len + tkb * kBlockKeys : kb * kBlockKeys;
+  const int key_end = tree_blk ? a.kv_len : a.prefix_len;  // keys of this block: [key0, min(key0 + 128, key_end))
+  const int G = a.group;
+  const int TG = a.q_len * G;
+  const int TGP = a.n_tiles * kTileRows;
+  const float sl2 = a.scale_log2;
+  const short qsgn = a.neg_q ? (short)0x8000 : (short)0;
+
+  const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  const T* qbase = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)kvh * G * a.sqh;
+  const T* dobase = static_cast<const T*>(a.dout) + b * a.sdob + (int64_t)kvh * G * a.sdoh;
+  const float2* rsbase = a.rowstat + (int64_t)bk * TGP;
+  const uint32_t* visbase =
+      a.vis + (int64_t)b * a.vis_tree_stride + (tree_blk ? (int64_t)tkb * kBlockKeys : 0);
+
+  // K block HBM -> LDS (keys past the end repeat the last key; masked).
+  {
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int u = wave * KPW + i;
+      const int row = u * RPL + lane / CPR, pos = lane % CPR;
+      const int key = min(key0 + row, a.kv_len - 1);
+      dma16(kbase + (int64_t)key * a.skn + ((pos ^ swz<D>(row)) << 3), lds_addr(kblk + u * 1024));
+    }
+  }
+  // Q / dO tile j HBM -> LDS buffer s, with its row statistics and (tree
+  // blocks) the 128 keys' mask words.  Rows past the end repeat the last row;
+  // their statistics make P = dS = 0.
+  auto issue_tile = [&](int j, int s) {
+    unsigned char* qt = tiles + 2 * s * TILE_B;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int u = wave * TPW + i;  // 0 .. 2*LPT-1: Q loads, then dO loads
+      const bool is_do = u >= LPT;
+      const int ul = is_do ? u - LPT : u;
+      const int row = ul * RPL + lane / CPR, pos = lane % CPR;
+      const int R = min(j * kTileRows + row, TG - 1);
+      const int t = R / G;
+      const int g = R - t * G;
+      const T* src = is_do ? dobase + g * a.sdoh + (int64_t)t * a.sdom : qbase + g * a.sqh + (int64_t)t * a.sqm;
+      dma16(src + ((pos ^ swz<D>(row)) << 3), lds_addr(qt + (is_do ? TILE_B : 0) + ul * 1024));
+    }
+    if (wave == 0 && lane < kTileRows * 8 / 16)
+      dma16(rsbase + j * kTileRows + 2 * lane, lds_addr(rs + s * kTileRows));
+    if (tree_blk && wave == 1 && lane < kBlockKeys * 4 / 16)
+      dma16(visbase + (int64_t)j * a.n_tkeys + 4 * lane, lds_addr(visw + s * kBlockKeys));
+  };
+  issue_tile(0, 0);
+
+  // V^T operand of dP = dO V^T (B[d][key]: lane (key ln, lh) holds d = 16kk +
+  // 8lh + [0, 8)), in registers for the whole walk.  Loaded after the DMAs
+  // and consumed at once: the compiler's wait for them then covers the DMAs
+  // too, which the first tile needs anyway.
+  const int mykey = key0 + 32 * wave + ln;
+  const bool key_ok = mykey < key_end && mykey < key0 + kBlockKeys;
+  i16x8 vf[KSTEPS];
+  {
+    const T* vp = vbase + (int64_t)min(mykey, a.kv_len - 1) * a.svn + 8 * lh;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) vf[kk] = *reinterpret_cast<const i16x8*>(vp + kk * 16);
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(vf[kk]));
+  }
+
+  // LDS offsets (bytes).  Row reads: lane (row ln, lh) reads chunk 2kk + lh.
+  // Transposed reads: lane (x = lane>>4, i = lane&15) reads 8 bytes of row
+  // 8jj + 4(x>>1) + (i>>2) (+16 per k-step) at d = dt*32 + 16(x&1) + 4(i&3);
+  // after the transpose it holds rows +[0,4) of d = dt*32 + 16(x&1) + i.
+  // The offsets are recomputed where they are used (a few VALU ops) rather
+  // than held across the tile loop: registers are the scarce resource here.
+  const int vx = lane >> 4, vi = lane & 15;
+  auto r_off = [&](int kk) { return ln * ROWB + (((2 * kk + lh) ^ swz<D>(ln)) << 4); };
+  auto t_off = [&](int dt, int jj) {
+    const int r = 8 * jj + 4 * (vx >> 1) + (vi >> 2);
+    const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
+    return r * ROWB + (((d >> 3) ^ swz<D>(r)) << 4) + ((d & 7) << 1);
+  };
+  // dS [key][row] (64 bytes per key): transposed read of keys 8jj + 4(x>>1) +
+  // (i>>2) at rows 16(x&1) + 4(i&3).
+  int ds_toff[2];
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj)
+    ds_toff[jj] = (8 * jj + 4 * (vx >> 1) + (vi >> 2)) * 64 + (16 * (vx & 1) + 4 * (vi & 3)) * 2;
+  const unsigned char* kmine = kblk + 32 * wave * ROWB;
+
+  f32x16 dk[DT], dv[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dk[dt][i] = dv[dt][i] = 0.f;
+
+  // rows (keys) +0..3 and +8..11 of a transposed read: the two halves of
+  // one operand (jj = 0, 1; the swizzle differs between them)
+  auto tr_pair = [&](const unsigned char* base, int dt) {
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(base + t_off(dt, 0)));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(base + t_off(dt, 1)));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  for (int j = 0; j < a.n_tiles; ++j) {
+    const int s = j & 1;
+    // tile j (and on j = 0 the K block) landed for every wave; every wave is
+    // done with tile j-1, so buffer s^1 and the dS area are free
+    vm_wait0();
+    sync_lds();
+    if (j + 1 < a.n_tiles) issue_tile(j + 1, s ^ 1);
+    const unsigned char* qt = tiles + 2 * s * TILE_B;
+    const unsigned char* dot = qt + TILE_B;
+
+    // S = Q K^T, dP = dO V^T: M = rows, N = keys; lane (key ln, lh) holds
+    // rows 8(i/4) + 4lh + i%4 of its key.
+    f32x16 sc, dp;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = dp[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const int ro = r_off(kk);
+      const i16x8 qa = *reinterpret_cast<const i16x8*>(qt + ro) ^ qsgn;
+      const i16x8 kf = *reinterpret_cast<const i16x8*>(kmine + ro);
+      const i16x8 da = *reinterpret_cast<const i16x8*>(dot + ro);
+      sc = Mma<T>::run(bit_cast<V8>(qa), bit_cast<V8>(kf), sc);
+      dp = Mma<T>::run(bit_cast<V8>(da), bit_cast<V8>(vf[kk]), dp);
+    }
+    // P and dS from the row statistics of the lane's 16 rows (read one group
+    // of 4 rows at a time) and its key's mask word.
+    uint32_t w = key_ok ? 0xffffffffu : 0u;
+    if (tree_blk) w &= visw[s * kBlockKeys + 32 * wave + ln];
+    V8 pb[2], db[2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4* rp = reinterpret_cast<const float4*>(rs + s * kTileRows + 8 * q + 4 * lh);
+      const float4 st0 = rp[0], st1 = rp[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * q + e, m = 8 * q + 4 * lh + e;
+        const float4 pr = (e < 2) ? st0 : st1;
+        const float lse2 = (e & 1) ? pr.z : pr.x;
+        const float dvr = (e & 1) ? pr.w : pr.y;
+        const float p = ((w >> m) & 1u) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], sl2, -lse2)) : 0.f;
+        pb[i >> 3][i & 7] = (T)p;
+        db[i >> 3][i & 7] = (T)(p * (dp[i] - dvr));
+      }
+    }
+    // dV^T += dO^T P, dK^T += Q^T dS: M = d, N = keys, k-step s2 covers rows
+    // 16s2 + 8(e/4) + 4lh + e%4 -- elements 8s2 .. 8s2+7 of the accumulator.
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const i16x8 doT = tr_pair(dot + 16 * s2 * ROWB, dt);
+        const i16x8 qT = tr_pair(qt + 16 * s2 * ROWB, dt) ^ qsgn;
+        dv[dt] = Mma<T>::run(bit_cast<V8>(doT), pb[s2], dv[dt]);
+        dk[dt] = Mma<T>::run(bit_cast<V8>(qT), db[s2], dk[dt]);
+      }
+    // dS of the wave's keys -> LDS [key][row]: rows 8q + 4lh + [0, 4) are
+    // elements 4q .. 4q+3.
+    {
+      unsigned char* dst = dsl + (32 * wave + ln) * 64 + 8 * lh;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const i16x8 e = bit_cast<i16x8>(db[q >> 1]);
+        const i16x4 v4 = (q & 1) ? __builtin_shufflevector(e, e, 4, 5, 6, 7) : __builtin_shufflevector(e, e, 0, 1, 2, 3);
+        *reinterpret_cast<i16x4*>(dst + 16 * q) = v4;
+      }
+    }
+    sync_lds();
+    // dQ^T = K^T dS^T over the workgroup's 128 keys (M = d-tile `wave`, N =
+    // rows, 8 k-steps), added to the fp32 accumulator.
+    if (wave < DT) {
+      f32x16 acc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < kBlockKeys / 16; ++ks) {
+        const i16x8 kT = tr_pair(kblk + 16 * ks * ROWB, wave);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsl + ds_toff[0] + 16 * ks * 64));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsl + ds_toff[1] + 16 * ks * 64));
+        const i16x8 dsT = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc = Mma<T>::run(bit_cast<V8>(kT), bit_cast<V8>(dsT), acc);
+      }
+      // lane (row ln, lh) holds d = wave*32 + 8(i/4) + 4lh + i%4
+      const int R = j * kTileRows + ln;
+      if (R < TG) {
+        float* dst = a.dq_acc + ((int64_t)bk * TG + R) * D + wave * 32 + 4 * lh;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) atomicAdd(dst + 8 * (i >> 2) + (i & 3), acc[i]);
+      }
+    }
+  }
+
+  // dK = |sm_scale| dK^T, dV = dV^T: lane (key ln, lh) holds d = dt*32 +
+  // 8(i/4) + 4lh + i%4 of its key.
+  if (key_ok) {
+    T* dkp = static_cast<T*>(a.dk) + b * a.sdkb + kvh * a.sdkh + (int64_t)mykey * a.sdkn + 4 * lh;
+    T* dvp = static_cast<T*>(a.dv) + b * a.sdvb + kvh * a.sdvh + (int64_t)mykey * a.sdvn + 4 * lh;
+    typedef T T4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        T4 x, y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] = (T)(dk[dt][4 * q + e] * a.dk_scale);
+          y[e] = (T)dv[dt][4 * q + e];
+        }
+        *reinterpret_cast<T4*>(dkp + dt * 32 + 8 * q) = x;
+        *reinterpret_cast<T4*>(dvp + dt * 32 + 8 * q) = y;
+      }
+  }
+}
+
+// ------------------------------------------------------------ prep / dq / vis
+struct PrepArgs {
+  const void* o;
+  const void* dout;
+  const float* lse;  // [B, Hq, q_len]
+  float2* rowstat;   // [B*Hkv][n_tiles*32]
+  float* dq_acc;     // [B*Hkv][TG][D]
+  int64_t sob, soh, som, sdob, sdoh, sdom;
+  int batch, num_heads, num_kv_heads, group, q_len, n_tiles;
+};
+
+// 16 lanes per row of the padded row space B*Hkv*TGP.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const PrepArgs a) {
+  constexpr int EPL = D / 16;  // elements per lane
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = gid >> 4;
+  const int part = (int)(gid & 15);
+  const int TG = a.q_len * a.group;
+  const int TGP = a.n_tiles * kTileRows;
+  const int64_t nrows = (int64_t)a.batch * a.num_kv_heads * TGP;
+  const bool live = row < nrows;
+  const int64_t bk = live ? row / TGP : 0;
+  const int R = live ? (int)(row - bk * TGP) : 0;
+  const bool real = live && R < TG;
+  float acc = 0.f, lse = -INFINITY;
+  if (real) {
+    const int t = R / a.group, g = R - t * a.group;
+    const int kvh = (int)(bk % a.num_kv_heads), b = (int)(bk / a.num_kv_heads);
+    const int h = kvh * a.group + g;
+    typedef T TV __attribute__((ext_vector_type(EPL)));
+    const TV ov = *reinterpret_cast<const TV*>(static_cast<const T*>(a.o) + b * a.sob + (int64_t)h * a.soh +
+                                               (int64_t)t * a.som + part * EPL);
+    const TV dv = *reinterpret_cast<const TV*>(static_cast<const T*>(a.dout) + b * a.sdob + (int64_t)h * a.sdoh +
+                                               (int64_t)t * a.sdom + part * EPL);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc += (float)ov[e] * (float)dv[e];
+    lse = a.lse[((int64_t)b * a.num_heads + h) * a.q_len + t];
+    float* dq = a.dq_acc + ((int64_t)bk * TG + R) * D + part * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4) *reinterpret_cast<float4*>(dq + e) = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+  if (live && part == 0) {
+    const bool empty = !(lse > -INFINITY);  // no visible key (or a padding row)
+    a.rowstat[row] = empty ? make_float2(INFINITY, 0.f) : make_float2(lse * 1.4426950408889634f, acc);
+  }
+}
+
+struct DqArgs {
+  const float* dq_acc;
+  void* dq;
+  int64_t sqb, sqh, sqm;
+  float scale;
+  int batch, num_kv_heads, group, q_len;
+};
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(const DqArgs a) {
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t TG = (int64_t)a.q_len * a.group;
+  const int64_t row = gid / (D / 8);
+  const int part = (int)(gid % (D / 8));
+  if (row >= (int64_t)a.batch * a.num_kv_heads * TG) return;
+  const int64_t bk = row / TG;
+  const int R = (int)(row - bk * TG);
+  const int t = R / a.group, g = R - t * a.group;
+  const int kvh = (int)(bk % a.num_kv_heads), b = (int)(bk / a.num_kv_heads);
+  const float4* src = reinterpret_cast<const float4*>(a.dq_acc + row * D + part * 8);
+  const float4 x0 = src[0], x1 = src[1];
+  typedef T T8 __attribute__((ext_vector_type(8)));
+  T8 o;
+  o[0] = (T)(x0.x * a.scale);
+  o[1] = (T)(x0.y * a.scale);
+  o[2] = (T)(x0.z * a.scale);
+  o[3] = (T)(x0.w * a.scale);
+  o[4] = (T)(x1.x * a.scale);
+  o[5] = (T)(x1.y * a.scale);
+  o[6] = (T)(x1.z * a.scale);
+  o[7] = (T)(x1.w * a.scale);
+  *reinterpret_cast<T8*>(static_cast<T*>(a.dq) + b * a.sqb + (int64_t)(kvh * a.group + g) * a.sqh +
+                         (int64_t)t * a.sqm + part * 8) = o;
+}
+
+struct VisArgs {
+  const int32_t* row_ptr;
+  const int32_t* col_idx;
+  const int8_t* blk_type;
+  const int32_t* payload;
+  const int32_t* offset;
+  int64_t ms_row_ptr, ms_col_idx, ms_blk_type, ms_payload, ms_offset;
+  uint32_t* vis;  // [n_trees][n_tiles][n_tkeys]
+  int64_t tree_stride;
+  int group, q_len, block_m, block_n, n_tree_blocks, tree_key_limit, n_tiles, n_tkeys;
+};
+
+// One workgroup per (tile, tree): the block states of the tile's q-blocks
+// (0 ZERO, -1 FULL, 1 + offset MIXED) expand into LDS, then each thread
+// writes the 32-row visibility words of its tree keys.
+__global__ __launch_bounds__(256) void bwd_vis_kernel(const VisArgs a) {
+  __shared__ int st[kMaxStateInts];
+  __shared__ int rps[72];
+  const int tile = blockIdx.x, tree = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int G = a.group, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
+  const int TG = a.q_len * G;
+  const int r_lo = tile * kTileRows;
+  const int r_hi = min(r_lo + kTileRows, TG) - 1;
+  uint32_t* out = a.vis + (int64_t)tree * a.tree_stride + (int64_t)tile * a.n_tkeys;
+  if (r_lo > r_hi) {  // a padding tile: nothing visible
+    for (int c = tid; c < a.n_tkeys; c += 256) out[c] = 0u;
+    return;
+  }
+  const int qb_lo = (r_lo / G) / BM, qb_hi = (r_hi / G) / BM, nqbc = qb_hi - qb_lo + 1;
+  const int32_t* rp = a.row_ptr + tree * a.ms_row_ptr;
+  const int32_t* ci = a.col_idx + tree * a.ms_col_idx;
+  const int8_t* bt = a.blk_type + tree * a.ms_blk_type;
+  const int32_t* pl = a.payload + tree * a.ms_payload;
+  const int32_t* of = a.offset + tree * a.ms_offset;
+  for (int i = tid; i < nqbc * ntb; i += 256) st[i] = 0;
+  if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
+  __syncthreads();
+  for (int e = rps[0] + tid; e < rps[nqbc]; e += 256) {
+    int qq = 0;
+    while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
+    const int tb = ci[e];
+    if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
+  }
+  __syncthreads();
+  for (int c = tid; c < a.n_tkeys; c += 256) {
+    uint32_t w = 0;
+    if (c < a.tree_key_limit) {
+      const int tb = c / BN, cc = c - tb * BN;
+      for (int R = r_lo; R <= r_hi; ++R) {
+        const int t = R / G, qb = t / BM;
+        const int e = st[(qb - qb_lo) * ntb + tb];
+        bool bit = e < 0;
+        if (e > 0) {
+          const int flat = (t - qb * BM) * BN + cc;
+          bit = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 1u;
+        }
+        w |= (uint32_t)bit << (R - r_lo);
+      }
+    }
+    out[c] = w;
+  }
+}
+
+// ------------------------------------------------------------------- host
+struct BwdPlan {
+  int n_tiles, n_pb, n_tb, n_tkeys, n_trees, nqbc_max;
+  size_t rowstat_bytes, dq_bytes, vis_bytes;
+};
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int make_bwd_plan(int batch, int num_kv_heads, int q_len, int kv_len, int prefix_len, int gqa, int head_dim,
+                  int block_m, int n_tree_blocks, int n_trees, BwdPlan* p) {
+  const int64_t TG = (int64_t)q_len * gqa;
+  p->n_tiles = (int)((TG + kTileRows - 1) / kTileRows);
+  p->n_pb = ceil_div(prefix_len, kBlockKeys);
+  p->n_tb = ceil_div(kv_len - prefix_len, kBlockKeys);
+  p->n_tkeys = p->n_tb * kBlockKeys;
+  p->n_trees = n_trees;
+  // q-blocks a 32-row tile spans: tokens t_lo .. t_lo + ceil(32/G)
+  const int toks = (kTileRows + gqa - 1) / gqa + 1;
+  p->nqbc_max = std::min(ceil_div(q_len, block_m), toks / block_m + 2);
+  if ((int64_t)p->nqbc_max * n_tree_blocks > kMaxStateInts || p->nqbc_max + 1 > 72) return TSFA_ERR_UNSUPPORTED;
+  const int64_t rows = (int64_t)batch * num_kv_heads;
+  p->rowstat_bytes = align256((size_t)rows * p->n_tiles * kTileRows * 8);
+  p->dq_bytes = align256((size_t)rows * TG * head_dim * 4);
+  p->vis_bytes = align256((size_t)n_trees * p->n_tiles * p->n_tkeys * 4 + 16);
+  const int64_t items = rows * (p->n_pb + p->n_tb);
+  if (items > (int64_t)INT32_MAX / 2 || (int64_t)n_trees * p->n_tiles * p->n_tkeys > ((int64_t)1 << 28))
+    return TSFA_ERR_UNSUPPORTED;
+  return TSFA_OK;
+}
+
+template <typename T, int D>
+int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const DqArgs& da, const BwdPlan& p,
+               bool has_tree, hipStream_t stream) {
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
+  const uint64_t bit = 1ull << (dev & 63);
+  if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_kv_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kv_lds_bytes<D>()) != hipSuccess)
+      return TSFA_ERR_LAUNCH;
+    attr_set.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  const int64_t prep_threads = (int64_t)pa.batch * pa.num_kv_heads * p.n_tiles * kTileRows * 16;
+  hipLaunchKernelGGL((bwd_prep_kernel<T, D>), dim3((unsigned)((prep_threads + 255) / 256)), dim3(256), 0, stream,
+                     pa);
+  if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  if (has_tree) {
+    hipLaunchKernelGGL(bwd_vis_kernel, dim3(p.n_tiles, p.n_trees), dim3(256), 0, stream, va);
+    if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  }
+  const unsigned grid = (unsigned)ba.items_per_xcd * 8;
+  hipLaunchKernelGGL((bwd_kv_kernel<T, D>), dim3(grid), dim3(kWaves * 64), kv_lds_bytes<D>(), stream, ba);
+  if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  const int64_t dq_threads = (int64_t)da.batch * da.num_kv_heads * da.q_len * da.group * (D / 8);
+  hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3((unsigned)((dq_threads + 255) / 256)), dim3(256), 0, stream, da);
+  return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+}
+
+}  // namespace bwd
+}  // namespace tsfa
+
+using namespace tsfa;
+using namespace tsfa::bwd;
+
+extern "C" size_t tsfa_bwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                                           int prefix_len, int block_m, int n_tree_blocks, int head_dim,
+                                           int n_trees) {
+  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || block_m <= 0 ||
+      kv_len < prefix_len || prefix_len < 0 || n_trees <= 0)
+    return 0;
+  BwdPlan p;
+  if (make_bwd_plan(batch, num_kv_heads, q_len, kv_len, prefix_len, num_heads / num_kv_heads, head_dim, block_m,
+                    n_tree_blocks, n_trees, &p) != TSFA_OK)
+    return 0;
+  return p.rowstat_bytes + p.dq_bytes + p.vis_bytes;
+}
+
+extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, const int32_t* row_ptr,
+                        const int32_t* col_idx, const int8_t* blk_type, const int32_t* mixed_mask_payload,
+                        const int32_t* mixed_mask_offset, const int64_t* meta_seq_stride, const int64_t* strides,
+                        float sm_scale, int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                        int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size, int block_m,
+                        int block_n, int head_dim, int dtype, void* workspace, size_t workspace_bytes,
+                        tsfa_stream_t stream_) {
+  int st = tsfa_fwd_check_args(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
+                               n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype);
+  if (st != TSFA_OK) return st;
+  if (batch == 0 || q_len == 0) return TSFA_OK;
+  if (strides == nullptr || meta_seq_stride == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  const void* ptrs[9] = {q, k, v, o, dout, dq, dk, dv, lse};
+  for (const void* ptr : ptrs)
+    if (ptr == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  if (row_ptr == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  // strides: q, k, v, o, dout, dq, dk, dv -- (b, h, n, d) each
+  for (int i = 0; i < 8; ++i) {
+    if (strides[4 * i + 3] != 1) return TSFA_ERR_UNSUPPORTED;
+    for (int j = 0; j < 3; ++j)
+      if (strides[4 * i + j] % 8 != 0) return TSFA_ERR_UNSUPPORTED;
+  }
+  for (int i = 0; i < 8; ++i)
+    if (reinterpret_cast<uintptr_t>(ptrs[i]) % 16 != 0) return TSFA_ERR_UNSUPPORTED;
+  bool per_seq = false;
+  for (int i = 0; i < 5; ++i) {
+    if (meta_seq_stride[i] < 0) return TSFA_ERR_INVALID_ARGUMENT;
+    per_seq = per_seq || meta_seq_stride[i] != 0;
+  }
+  const int n_trees = per_seq ? batch : 1;
+  BwdPlan p;
+  st = make_bwd_plan(batch, num_kv_heads, q_len, kv_len, prefix_len, gqa_group_size, head_dim, block_m,
+                     n_tree_blocks, n_trees, &p);
+  if (st != TSFA_OK) return st;
+  if (workspace == nullptr || workspace_bytes < p.rowstat_bytes + p.dq_bytes + p.vis_bytes)
+    return TSFA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return TSFA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  float2* rowstat = reinterpret_cast<float2*>(ws);
+  float* dq_acc = reinterpret_cast<float*>(ws + p.rowstat_bytes);
+  uint32_t* vis = reinterpret_cast<uint32_t*>(ws + p.rowstat_bytes + p.dq_bytes);
+  const int tree_key_limit =
+      (int)std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
+
+  float sl2 = fabsf(sm_scale) * 1.4426950408889634f;
+  if (sl2 == 0.f) sl2 = 1e-30f;
+
+  PrepArgs pa;
+  pa.o = o;
+  pa.dout = dout;
+  pa.lse = lse;
+  pa.rowstat = rowstat;
+  pa.dq_acc = dq_acc;
+  pa.sob = strides[12];
+  pa.soh = strides[13];
+  pa.som = strides[14];
+  pa.sdob = strides[16];
+  pa.sdoh = strides[17];
+  pa.sdom = strides[18];
+  pa.batch = batch;
+  pa.num_heads = num_heads;
+  pa.num_kv_heads = num_kv_heads;
+  pa.group = gqa_group_size;
+  pa.q_len = q_len;
+  pa.n_tiles = p.n_tiles;
+
+  VisArgs va;
+  va.row_ptr = row_ptr;
+  va.col_idx = col_idx;
+  va.blk_type = blk_type;
+  va.payload = mixed_mask_payload;
+  va.offset = mixed_mask_offset;
+  va.ms_row_ptr = meta_seq_stride[0];
+  va.ms_col_idx = meta_seq_stride[1];
+  va.ms_blk_type = meta_seq_stride[2];
+  va.ms_payload = meta_seq_stride[3];
+  va.ms_offset = meta_seq_stride[4];
+  va.vis = vis;
+  va.tree_stride = (int64_t)p.n_tiles * p.n_tkeys;
+  va.group = gqa_group_size;
+  va.q_len = q_len;
+  va.block_m = block_m;
+  va.block_n = block_n;
+  va.n_tree_blocks = n_tree_blocks;
+  va.tree_key_limit = tree_key_limit;
+  va.n_tiles = p.n_tiles;
+  va.n_tkeys = p.n_tkeys;
+
+  BwdArgs ba;
+  ba.q = q;
+  ba.k = k;
+  ba.v = v;
+  ba.dout = dout;
+  ba.dk = dk;
+  ba.dv = dv;
+  ba.dq_acc = dq_acc;
+  ba.rowstat = rowstat;
+  ba.vis = vis;
+  ba.sqb = strides[0];
+  ba.sqh = strides[1];
+  ba.sqm = strides[2];
+  ba.skb = strides[4];
+  ba.skh = strides[5];
+  ba.skn = strides[6];
+  ba.svb = strides[8];
+  ba.svh = strides[9];
+  ba.svn = strides[10];
+  ba.sdob = strides[16];
+  ba.sdoh = strides[17];
+  ba.sdom = strides[18];
+  ba.sdkb = strides[24];
+  ba.sdkh = strides[25];
+  ba.sdkn = strides[26];
+  ba.sdvb = strides[28];
+  ba.sdvh = strides[29];
+  ba.sdvn = strides[30];
+  ba.vis_tree_stride = n_trees > 1 ? va.tree_stride : 0;
+  ba.scale_log2 = sl2;
+  ba.dk_scale = fabsf(sm_scale);
+  ba.neg_q = sm_scale < 0.f ? 1 : 0;
+  ba.num_kv_heads = num_kv_heads;
+  ba.group = gqa_group_size;
+  ba.q_len = q_len;
+  ba.kv_len = kv_len;
+  ba.prefix_len = prefix_len;
+  ba.n_tiles = p.n_tiles;
+  ba.n_pb = p.n_pb;
+  ba.n_tb = p.n_tb;
+  ba.n_tkeys = p.n_tkeys;
+  ba.n_items = batch * num_kv_heads * (p.n_pb + p.n_tb);
+  ba.items_per_xcd = (ba.n_items + 7) / 8;
+
+  DqArgs da;
+  da.dq_acc = dq_acc;
+  da.dq = dq;
+  da.sqb = strides[20];
+  da.sqh = strides[21];
+  da.sqm = strides[22];
+  da.scale = sm_scale;
+  da.batch = batch;
+  da.num_kv_heads = num_kv_heads;
+  da.group = gqa_group_size;
+  da.q_len = q_len;
+
+  const bool has_tree = p.n_tb > 0;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  if (dtype == TSFA_DTYPE_BF16)
+    return head_dim == 128 ? launch_bwd<__bf16, 128>(ba, pa, va, da, p, has_tree, stream)
+                           : launch_bwd<__bf16, 64>(ba, pa, va, da, p, has_tree, stream);
+  return head_dim == 128 ? launch_bwd<_Float16, 128>(ba, pa, va, da, p, has_tree, stream)
+                         : launch_bwd<_Float16, 64>(ba, pa, va, da, p, has_tree, stream);
+}

@@ -91,6 +91,7 @@ struct SplitArgs {
 struct CombineArgs {
   void* o;
   int64_t sob, soh, som;
+  float* lse;  // optional [B, Hq, q_len] natural-log log-sum-exp of each row's scaled scores
   float scale_log2;
   int batch, num_heads, num_kv_heads, group, q_len, n_slots;
   const void* ws_o;
@@ -1400,6 +1401,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
   TV out;
 #pragma unroll
   for (int i = 0; i < kEpt; ++i) out[i] = (T)(acc[i] / l);
+  if (a.lse != nullptr && part == 0) {
+    // log-sum-exp of sm_scale * q.k over the row's visible keys: M and l are
+    // in the exp2 domain of |sm_scale| * log2(e); -inf for a row with no key
+    const float lse2 = (l > 0.f) ? mx * a.scale_log2 + __log2f(l) : -INFINITY;
+    a.lse[((int64_t)b * a.num_heads + h) * a.q_len + t] = lse2 * 0.69314718055994531f;
+  }
   T* dst = static_cast<T*>(a.o) + b * a.sob + (int64_t)h * a.soh + (int64_t)t * a.som + part * kEpt;
   *reinterpret_cast<TV*>(dst) = out;
 }
@@ -1613,7 +1620,7 @@ struct KvSource {
   bool paged() const { return cache != nullptr; }
 };
 
-int fwd_impl(const void* q, const KvSource& kv, void* o, const int32_t* row_ptr, const int32_t* col_idx,
+int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32_t* row_ptr, const int32_t* col_idx,
              const int8_t* blk_type, const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
              const int64_t* meta_seq_stride, const int64_t* q_strides, const int64_t* o_strides, float sm_scale,
              int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int n_q_blocks,
@@ -1733,6 +1740,7 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, const int32_t* row_ptr,
 
   CombineArgs ca;
   ca.o = o;
+  ca.lse = lse;
   ca.sob = o_strides[0];
   ca.soh = o_strides[1];
   ca.som = o_strides[2];
@@ -1770,10 +1778,29 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
   kv.v = v;
   kv.k_strides = strides ? strides + 4 : nullptr;
   kv.v_strides = strides ? strides + 8 : nullptr;
-  return fwd_impl(q, kv, o, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset, meta_seq_stride,
-                  strides, strides ? strides + 12 : nullptr, sm_scale, batch, num_heads, num_kv_heads, q_len,
+  return fwd_impl(q, kv, o, nullptr, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset,
+                  meta_seq_stride, strides, strides ? strides + 12 : nullptr, sm_scale, batch, num_heads, num_kv_heads, q_len,
                   kv_len, prefix_len, n_q_blocks, n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype,
                   workspace, workspace_bytes, stream_);
+}
+
+extern "C" int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
+                            const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
+                            const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+                            const int64_t* meta_seq_stride, const int64_t* strides, float sm_scale, int batch,
+                            int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int n_q_blocks,
+                            int n_tree_blocks, int gqa_group_size, int block_m, int block_n, int head_dim, int dtype,
+                            void* workspace, size_t workspace_bytes, tsfa_stream_t stream_) {
+  if (lse == nullptr && batch > 0 && q_len > 0) return TSFA_ERR_INVALID_ARGUMENT;
+  KvSource kv;
+  kv.k = k;
+  kv.v = v;
+  kv.k_strides = strides ? strides + 4 : nullptr;
+  kv.v_strides = strides ? strides + 8 : nullptr;
+  return fwd_impl(q, kv, o, lse, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset,
+                  meta_seq_stride, strides, strides ? strides + 12 : nullptr, sm_scale, batch, num_heads,
+                  num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks, gqa_group_size, block_m,
+                  block_n, head_dim, dtype, workspace, workspace_bytes, stream_);
 }
 
 extern "C" int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr,
@@ -1796,8 +1823,8 @@ extern "C" int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t
   kv.pt_stride = page_table_stride;
   kv.n_pages = n_pages;
   kv.page_size = page_size;
-  return fwd_impl(q, kv, o, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset, meta_seq_stride,
-                  q_strides, o_strides, sm_scale, batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
+  return fwd_impl(q, kv, o, nullptr, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset,
+                  meta_seq_stride, q_strides, o_strides, sm_scale, batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
                   n_q_blocks, n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype, workspace,
                   workspace_bytes, stream_);
 }

@@ -17,6 +17,9 @@ Extensions (no reference counterpart):
   built without a host synchronisation; slice b is bit-identical to
   prepare_tree_sparse_metadata of tree b.
   tree_sparse_attention_fwd: allocate O and launch with either record.
+  tree_sparse_attention_fwd(..., return_lse=True), tree_sparse_attention_bwd,
+  tree_sparse_attention (autograd): the backward, which the reference lacks
+  (README.md:198): dQ, dK, dV on HIP kernels from the forward's O and LSE.
   tree_sparse_attention_fwd_paged: the same forward over a paged K/V cache
   (FlashInfer's [pages, 2, page_size, Hkv, D] layout, benchmark.py:67-91)
   with per-sequence page lists, read in place.
@@ -249,7 +252,7 @@ def prepare_tree_sparse_metadata_batched(
 
 def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_strides, strides, sm_scale,
                 batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks,
-                gqa_group_size, block_m, block_n, head_dim):
+                gqa_group_size, block_m, block_n, head_dim, lse=None):
     lib = _lib.load()
     for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
         if not t.is_cuda:
@@ -269,10 +272,16 @@ def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_st
                                             head_dim)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        st = lib.tsfa_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(row_ptr), _lib.ptr(col_idx),
-                          _lib.ptr(blk_type), _lib.ptr(payload), _lib.ptr(offset), _lib.i64_array(meta_strides),
-                          _lib.i64_array(strides), float(sm_scale), *args, _lib.ptr(ws), ws_bytes,
-                          _lib.stream_handle(dev))
+        if lse is None:
+            st = lib.tsfa_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(row_ptr),
+                              _lib.ptr(col_idx), _lib.ptr(blk_type), _lib.ptr(payload), _lib.ptr(offset),
+                              _lib.i64_array(meta_strides), _lib.i64_array(strides), float(sm_scale), *args,
+                              _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
+        else:
+            st = lib.tsfa_fwd_lse(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(lse),
+                                  _lib.ptr(row_ptr), _lib.ptr(col_idx), _lib.ptr(blk_type), _lib.ptr(payload),
+                                  _lib.ptr(offset), _lib.i64_array(meta_strides), _lib.i64_array(strides),
+                                  float(sm_scale), *args, _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
     _lib.check("block_sparse_tree_fwd_kernel", st)
     return o
 
@@ -331,12 +340,16 @@ def _meta_arrays(meta, bsz: int):
 
 
 def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta, *,
-                              sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                              sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                              return_lse: bool = False):
     """O = tree-sparse attention of q [B,Hq,T,D] over k/v [B,Hkv,P+T,D].
 
     ``meta`` is a TreeSparseMetadata (one tree for the whole batch) or a
     BatchedTreeSparseMetadata (one tree per sequence, or one tree for every
-    sequence), already on q's device.
+    sequence), already on q's device.  With ``return_lse`` the result is
+    ``(O, lse)``: lse [B, Hq, T] fp32 is the natural-log log-sum-exp of each
+    row's visible scaled scores (-inf for a row with no visible key), what
+    tree_sparse_attention_bwd needs.
     """
     q, k, v = _row_contig(q), _row_contig(k), _row_contig(v)
     bsz, n_heads, q_len, head_dim = q.shape
@@ -347,9 +360,99 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         sm_scale = 1.0 / math.sqrt(head_dim)
     tensors, meta_strides = _meta_arrays(meta, bsz)
     strides = (*q.stride(), *k.stride(), *v.stride(), *out.stride())
-    return _launch_fwd(q, k, v, out, *tensors, meta_strides, strides, sm_scale, bsz, n_heads, n_kv_heads, q_len,
-                       kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, n_heads // n_kv_heads,
-                       meta.block_m, meta.block_n, head_dim)
+    lse = torch.empty((bsz, n_heads, q_len), dtype=torch.float32, device=q.device) if return_lse else None
+    _launch_fwd(q, k, v, out, *tensors, meta_strides, strides, sm_scale, bsz, n_heads, n_kv_heads, q_len,
+                kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, n_heads // n_kv_heads,
+                meta.block_m, meta.block_n, head_dim, lse=lse)
+    return (out, lse) if return_lse else out
+
+
+def tree_sparse_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                              lse: torch.Tensor, dout: torch.Tensor, meta, *, sm_scale: Optional[float] = None,
+                              dq: Optional[torch.Tensor] = None, dk: Optional[torch.Tensor] = None,
+                              dv: Optional[torch.Tensor] = None):
+    """(dQ, dK, dV) of tree-sparse attention for the upstream gradient ``dout``.
+
+    ``o`` and ``lse`` are the forward's outputs (tree_sparse_attention_fwd
+    with return_lse=True) for the same q, k, v, meta and sm_scale.  dK / dV
+    sum over the query heads of each kv head (GQA); rows with no visible key
+    contribute nothing and get dQ = 0.  No counterpart in the reference, which
+    has no backward (README.md:198).
+    """
+    q, k, v, o, dout = (_row_contig(t) for t in (q, k, v, o, dout))
+    bsz, n_heads, q_len, head_dim = q.shape
+    _, n_kv_heads, kv_len, _ = k.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if tuple(o.shape) != tuple(q.shape) or tuple(dout.shape) != tuple(q.shape):
+        raise ValueError("o and dout must have q's shape")
+    if tuple(v.shape) != tuple(k.shape):
+        raise ValueError("k and v must have the same shape")
+    if lse.dtype != torch.float32 or tuple(lse.shape) != (bsz, n_heads, q_len):
+        raise ValueError(f"lse must be float32 [{bsz}, {n_heads}, {q_len}]")
+    lse = lse.contiguous()
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(v) if dv is None else dv
+    lib = _lib.load()
+    tensors, meta_strides = _meta_arrays(meta, bsz)
+    for name, t in (("q", q), ("k", k), ("v", v), ("o", o), ("lse", lse), ("dout", dout), ("dq", dq), ("dk", dk),
+                    ("dv", dv)):
+        if not t.is_cuda:
+            raise ValueError(f"{name} must be a HIP device tensor")
+        if t.device != q.device:
+            raise ValueError(f"{name} must be on {q.device}")
+    for name, t in zip(("row_ptr", "col_idx", "blk_type", "mixed_mask_payload", "mixed_mask_offset"), tensors):
+        if t.device != q.device:
+            raise ValueError(f"{name} must be on {q.device} (move the metadata to the device first)")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype == dout.dtype == dq.dtype == dk.dtype == dv.dtype):
+        raise NotImplementedError("q, k, v, o, dout and the gradients must share one dtype")
+    dt = _lib.dtype_code(q.dtype)
+    args = (bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks,
+            n_heads // n_kv_heads, meta.block_m, meta.block_n, head_dim, dt)
+    _lib.check("tree_sparse_attention_bwd", lib.tsfa_fwd_check_args(*args))
+    n_trees = bsz if any(meta_strides) else 1
+    ws_bytes = lib.tsfa_bwd_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, meta.block_m,
+                                            meta.n_tree_blocks, head_dim, n_trees)
+    if ws_bytes == 0 and bsz > 0 and q_len > 0:
+        raise NotImplementedError("tree_sparse_attention_bwd: tree too large for the backward's tables")
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=q.device)
+    strides = (*q.stride(), *k.stride(), *v.stride(), *o.stride(), *dout.stride(), *dq.stride(), *dk.stride(),
+               *dv.stride())
+    with torch.cuda.device(q.device):
+        st = lib.tsfa_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(lse), _lib.ptr(dout),
+                          _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), *(_lib.ptr(t) for t in tensors),
+                          _lib.i64_array(meta_strides), _lib.i64_array(strides), float(sm_scale), *args,
+                          _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device))
+    _lib.check("tree_sparse_attention_bwd", st)
+    return dq, dk, dv
+
+
+class TreeSparseAttentionFunction(torch.autograd.Function):
+    """Differentiable tree-sparse attention: forward = tree_sparse_attention_fwd
+    (saving O and the row LSE), backward = tree_sparse_attention_bwd."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, meta, sm_scale):
+        o, lse = tree_sparse_attention_fwd(q, k, v, meta, sm_scale=sm_scale, return_lse=True)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.meta = meta
+        ctx.sm_scale = sm_scale
+        return o
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = tree_sparse_attention_bwd(q, k, v, o, lse, dout, ctx.meta, sm_scale=ctx.sm_scale)
+        return dq, dk, dv, None, None
+
+
+def tree_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta,
+                          sm_scale: Optional[float] = None) -> torch.Tensor:
+    """tree_sparse_attention_fwd with autograd support (dQ, dK, dV on the HIP backward)."""
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    return TreeSparseAttentionFunction.apply(q, k, v, meta, sm_scale)
 
 
 def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_indices: torch.Tensor, meta, *,

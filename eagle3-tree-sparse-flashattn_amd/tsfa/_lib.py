@@ -36,6 +36,9 @@ EXPORTS = (
     "tsfa_fwd_check_args",
     "tsfa_fwd_workspace_bytes",
     "tsfa_fwd",
+    "tsfa_fwd_lse",
+    "tsfa_bwd",
+    "tsfa_bwd_workspace_bytes",
     "tsfa_fwd_paged",
     "tsfa_fwd_plan",
     "tsfa_fwd_set_kernel_mask",
@@ -55,6 +58,11 @@ _SIGNATURES = {
     "tsfa_fwd_workspace_bytes": (_c_size, [_c_int] * 7),
     "tsfa_fwd": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                           ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
+                 + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
+    "tsfa_fwd_lse": (_c_int, [_c_vp] * 10 + [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
+                     + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
+    "tsfa_bwd_workspace_bytes": (_c_size, [_c_int] * 10),
+    "tsfa_bwd": (_c_int, [_c_vp] * 14 + [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
     "tsfa_fwd_paged": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp,
                                 _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]

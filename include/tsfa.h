@@ -119,6 +119,46 @@ int tsfa_fwd(const void* q, const void* k, const void* v, void* o,
              int block_m, int block_n, int head_dim, int dtype,
              void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
 
+/* tsfa_fwd that also writes the log-sum-exp of every query row:
+ * lse[(b*num_heads + h)*q_len + t] = log sum_j exp(sm_scale * q.k_j) over the
+ * row's visible keys (natural log, fp32, -inf for a row with no visible key).
+ * No counterpart in the reference (its kernel keeps m_i / l_i in registers,
+ * tree_sparse_flashattn.py:228-329, and has no backward); tsfa_bwd needs it. */
+int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,
+                 const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
+                 const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+                 const int64_t* meta_seq_stride, const int64_t* strides, float sm_scale,
+                 int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
+                 int n_q_blocks, int n_tree_blocks, int gqa_group_size,
+                 int block_m, int block_n, int head_dim, int dtype,
+                 void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
+
+/* Backward of tsfa_fwd.  No counterpart in the reference (README.md:198 lists
+ * the backward kernel as missing).  Given q, k, v, the forward's o and lse
+ * (tsfa_fwd_lse) and dout = dL/dO, writes
+ *   dq = sm_scale * dS K,  dk = sm_scale * dS^T Q,  dv = P^T dO
+ * with P = softmax of the visible scaled scores and dS = P * (dO V^T -
+ * rowsum(dO * O)), dk / dv summed over the gqa_group_size query heads of each
+ * kv head.  Rows with no visible key contribute nothing (their dq is 0).
+ * strides  int64[32]: q, k, v, o, dout, dq, dk, dv -- (b, h, n, d) each, in
+ *          elements, d stride 1, 16-byte aligned rows
+ * Every other argument as in tsfa_fwd; workspace of
+ * tsfa_bwd_workspace_bytes(..., n_trees) bytes, n_trees = batch when
+ * meta_seq_stride is non-zero (one tree per sequence), else 1.  Four kernel
+ * launches on `stream`, no host synchronisation. */
+size_t tsfa_bwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                                int prefix_len, int block_m, int n_tree_blocks, int head_dim,
+                                int n_trees);
+int tsfa_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+             const void* dout, void* dq, void* dk, void* dv,
+             const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
+             const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+             const int64_t* meta_seq_stride, const int64_t* strides, float sm_scale,
+             int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
+             int n_q_blocks, int n_tree_blocks, int gqa_group_size,
+             int block_m, int block_n, int head_dim, int dtype,
+             void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
+
 /* tsfa_fwd over a paged K/V cache.  No counterpart in the reference's tree
  * kernel (it reads contiguous [B, Hkv, kv_len, D] tensors); it replaces the
  * gather a serving caller would otherwise run to turn its page pool into
