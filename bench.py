@@ -30,6 +30,8 @@ cpu_baseline = the fp32 dense+mask oracle (benchmark.py:8-35 restated) on the
                host cores, over a bounded sample of calls
 metadata     = the device metadata build (no host synchronisation), graph and
                eager, beside the CPU oracle builder
+backward     = tree_sparse_attention_bwd (dQ, dK, dV) over the same cycled
+               K/V, against the MFMA and HBM peaks
 paged        = the same forward reading FlashInfer's paged cache in place
                (page_size 16, scattered pages), its rate beside the
                contiguous call's
@@ -200,6 +202,56 @@ def paged_timing(w, qd, ks, vs, meta, steps: int, page_size: int, contiguous_us:
             "vs_contiguous": round(contiguous_us / us, 4)}
 
 
+def backward_timing(w, mask, qd, ks, vs, meta, steps: int, fwd_flops: float):
+    """tree_sparse_attention_bwd (dQ, dK, dV from O, the row LSE and dO) over the
+    same cycled K/V copies: graph of `steps` calls, HIP events on the replay
+    stream.  Algorithmic figures: five products per visible (row, key) pair --
+    S recomputed, dP, dV, dK, dQ -- i.e. 2.5x the forward's flops; bytes = Q, O,
+    dO, K, V read once and dQ, dK, dV written once."""
+    import torch
+
+    import tree_sparse_flashattn as tsf
+
+    do = torch.randn(qd.shape, generator=torch.Generator().manual_seed(7)).to(w.dtype).to(qd.device)
+    fwd = [tsf.tree_sparse_attention_fwd(qd, k, v, meta, return_lse=True) for k, v in zip(ks[:1], vs[:1])][0]
+    o, lse = fwd
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(ks[0]), torch.empty_like(vs[0])
+
+    def call(i):
+        tsf.tree_sparse_attention_bwd(qd, ks[i % len(ks)], vs[i % len(vs)], o, lse, do, meta, dq=dq, dk=dk, dv=dv)
+
+    for i in range(3):
+        call(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        call(0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                call(i)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps
+    flops = 2.5 * fwd_flops
+    nbytes = 2 * w.kv_bytes() + 4 * qd.numel() * qd.element_size()
+    tflops = flops / (us * 1e-6) / 1e12
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"us_per_call": round(us, 3), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
+            "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "achieved_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "kernels": "prep + tree visibility + key-parallel dK/dV/dQ + dQ convert (four launches)"}
+
+
 def calibrate_copy(mib: int, reps: int):
     """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
     import torch
@@ -221,6 +273,7 @@ def main():
     ap.add_argument("--cold-mib", type=int, default=512, help="K/V bytes cycled through (defeats the MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-backward", action="store_true", help="skip the backward timing")
     ap.add_argument("--paged-page-size", type=int, default=16,
                     help="also time the paged-cache forward at this page size (0: skip)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -351,9 +404,13 @@ def main():
         "cpu_baseline": None,
         "metadata": None,
         "paged": None,
+        "backward": None,
     }
     _log("[bench] metadata build ...")
     result["metadata"] = metadata_timing(w, mask.to(dev), mask)
+    if not args.no_backward:
+        _log("[bench] backward ...")
+        result["backward"] = backward_timing(w, mask, qd, ks, vs, meta, steps, flops)
     if args.paged_page_size > 0:
         _log(f"[bench] paged cache, page_size {args.paged_page_size} ...")
         del regions

@@ -50,6 +50,8 @@ constexpr int kWaves = 4;                 // 32 keys each
 constexpr int kBlockKeys = 32 * kWaves;   // keys per workgroup
 constexpr int kTileRows = 32;             // query rows per tile
 constexpr int kMaxStateInts = 8192;       // block-state table of one tile (bwd_vis_kernel)
+constexpr int kBufs = 4;                  // Q / dO tile buffers: loads run 3 tiles ahead
+constexpr int kDqAtomics = 16;            // atomic instructions per wave per tile (one 32x32 dQ^T tile)
 
 // 16-byte-chunk XOR swizzle of a row-major [rows][D] LDS tile (row period
 // 16), conflict-free for both read patterns of the kernel:
@@ -77,7 +79,19 @@ __device__ inline void dma16(const void* src, uint32_t lds_base) {
 }
 #pragma clang diagnostic pop
 
-__device__ inline void vm_wait0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt vmcnt(n) for a wave-uniform n in [LO, HI] (binary search over
+// the immediate forms).
+template <int LO, int HI> __device__ inline void vm_wait_n(int n) {
+  if constexpr (LO == HI) {
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(LO) : "memory");
+  } else {
+    constexpr int MID = (LO + HI) / 2;
+    if (n <= MID)
+      vm_wait_n<LO, MID>(n);
+    else
+      vm_wait_n<MID + 1, HI>(n);
+  }
+}
 __device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const TSFA_LDS void*)p; }
 template <typename V, typename U> __device__ inline V bit_cast(U u) { return __builtin_bit_cast(V, u); }
@@ -89,7 +103,7 @@ struct BwdArgs {
   const void* dout;
   void* dk;
   void* dv;
-  float* dq_acc;            // [B*Hkv][TG][D] fp32
+  float* dq_acc;            // [B*Hkv][D][n_tiles*32] fp32 (d-major: a wave's atomics cover whole lines)
   const float2* rowstat;    // [B*Hkv][n_tiles*32] (log2 LSE, Dv)
   const uint32_t* vis;      // [n_trees][n_tiles][n_tkeys] visibility words of tree keys
   int64_t sqb, sqh, sqm, skb, skh, skn, svb, svh, svn, sdob, sdoh, sdom, sdkb, sdkh, sdkn, sdvb, sdvh, sdvn;
@@ -103,9 +117,9 @@ struct BwdArgs {
 };
 
 template <int D> constexpr size_t kv_lds_bytes() {
-  // K block | 2 x (Q tile, dO tile) | 2 x 32 row stats | 2 x 128 mask words | dS [128 keys][32 rows]
-  return (size_t)kBlockKeys * D * 2 + 4 * (size_t)kTileRows * D * 2 + 2 * kTileRows * 8 + 2 * kBlockKeys * 4 +
-         (size_t)kBlockKeys * kTileRows * 2;
+  // K block | kBufs x (Q tile, dO tile) | kBufs x 32 row stats | kBufs x 128 mask words | dS [128 keys][32 rows]
+  return (size_t)kBlockKeys * D * 2 + 2 * kBufs * (size_t)kTileRows * D * 2 + kBufs * kTileRows * 8 +
+         kBufs * kBlockKeys * 4 + (size_t)kBlockKeys * kTileRows * 2;
 }
 
 template <typename T, int D>
@@ -128,9 +142,9 @@ void bwd_kv_kernel(const BwdArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   unsigned char* kblk = smem;
   unsigned char* tiles = kblk + KBLK_B;  // buffer s: Q at tiles + 2*s*TILE_B, dO right after
-  float2* rs = reinterpret_cast<float2*>(tiles + 4 * TILE_B);
-  uint32_t* visw = reinterpret_cast<uint32_t*>(rs + 2 * kTileRows);
-  unsigned char* dsl = reinterpret_cast<unsigned char*>(visw + 2 * kBlockKeys);
+  float2* rs = reinterpret_cast<float2*>(tiles + 2 * kBufs * TILE_B);
+  uint32_t* visw = reinterpret_cast<uint32_t*>(rs + kBufs * kTileRows);
+  unsigned char* dsl = reinterpret_cast<unsigned char*>(visw + kBufs * kBlockKeys);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -196,7 +210,17 @@ void bwd_kv_kernel(const BwdArgs a) {
     if (tree_blk && wave == 1 && lane < kBlockKeys * 4 / 16)
       dma16(visbase + (int64_t)j * a.n_tkeys + 4 * lane, lds_addr(visw + s * kBlockKeys));
   };
-  issue_tile(0, 0);
+  // The key blocks of one (b, kv head) start their walk at different tiles
+  // (block kb at tile kb * n_tiles / nkb), so the dQ atomics of concurrent
+  // blocks land on different rows instead of queueing on the same ones.
+  const int j0 = (int)((int64_t)kb * a.n_tiles / nkb);
+  auto tile_at = [&](int i) {
+    const int j = j0 + i;
+    return j >= a.n_tiles ? j - a.n_tiles : j;
+  };
+  // vector-memory instructions this wave issues per tile (wave-uniform)
+  const int lpw = TPW + (wave == 0 ? 1 : 0) + ((tree_blk && wave == 1) ? 1 : 0);
+  for (int i = 0; i < kBufs - 1 && i < a.n_tiles; ++i) issue_tile(tile_at(i), i);
 
   // V^T operand of dP = dO V^T (B[d][key]: lane (key ln, lh) holds d = 16kk +
   // 8lh + [0, 8)), in registers for the whole walk.  Loaded after the DMAs
@@ -248,13 +272,22 @@ void bwd_kv_kernel(const BwdArgs a) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
-  for (int j = 0; j < a.n_tiles; ++j) {
-    const int s = j & 1;
-    // tile j (and on j = 0 the K block) landed for every wave; every wave is
-    // done with tile j-1, so buffer s^1 and the dS area are free
-    vm_wait0();
+  for (int it = 0; it < a.n_tiles; ++it) {
+    const int s = it & (kBufs - 1);
+    const int j = tile_at(it);
+    // Wait for tile `it` (and on the first step the K block and V): vector
+    // memory completes in issue order, and issued after this tile's loads
+    // are the loads of the next min(2, left) tiles and the dQ atomics of the
+    // last min(it, 3) steps, none of which this step needs.
+    {
+      const int later_tiles = min(kBufs - 2, a.n_tiles - 1 - it);
+      const int later_atomics = wave < DT ? min(it, kBufs - 1) * kDqAtomics : 0;
+      vm_wait_n<0, 63>(it == 0 ? later_tiles * lpw : later_tiles * lpw + later_atomics);
+    }
+    // every wave is done with tile it-1: its buffer (the one tile it+3 goes
+    // to) and the dS area are free
     sync_lds();
-    if (j + 1 < a.n_tiles) issue_tile(j + 1, s ^ 1);
+    if (it + kBufs - 1 < a.n_tiles) issue_tile(tile_at(it + kBufs - 1), (it + kBufs - 1) & (kBufs - 1));
     const unsigned char* qt = tiles + 2 * s * TILE_B;
     const unsigned char* dot = qt + TILE_B;
 
@@ -329,13 +362,12 @@ void bwd_kv_kernel(const BwdArgs a) {
         const i16x8 dsT = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         acc = Mma<T>::run(bit_cast<V8>(kT), bit_cast<V8>(dsT), acc);
       }
-      // lane (row ln, lh) holds d = wave*32 + 8(i/4) + 4lh + i%4
-      const int R = j * kTileRows + ln;
-      if (R < TG) {
-        float* dst = a.dq_acc + ((int64_t)bk * TG + R) * D + wave * 32 + 4 * lh;
+      // lane (row ln, lh) holds d = wave*32 + 8(i/4) + 4lh + i%4; the
+      // accumulator is d-major, so each instruction's 64 lanes cover two
+      // whole 128-byte lines (32 rows at two d).  Padding rows add 0.
+      float* dst = a.dq_acc + ((int64_t)bk * D + wave * 32 + 4 * lh) * TGP + j * kTileRows + ln;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) atomicAdd(dst + 8 * (i >> 2) + (i & 3), acc[i]);
-      }
+      for (int i = 0; i < kDqAtomics; ++i) atomicAdd(dst + (int64_t)(8 * (i >> 2) + (i & 3)) * TGP, acc[i]);
     }
   }
 
@@ -367,7 +399,7 @@ struct PrepArgs {
   const void* dout;
   const float* lse;  // [B, Hq, q_len]
   float2* rowstat;   // [B*Hkv][n_tiles*32]
-  float* dq_acc;     // [B*Hkv][TG][D]
+  float* dq_acc;     // [B*Hkv][D][TGP]
   int64_t sob, soh, som, sdob, sdoh, sdom;
   int batch, num_heads, num_kv_heads, group, q_len, n_tiles;
 };
@@ -399,9 +431,11 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const PrepArgs a) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc += (float)ov[e] * (float)dv[e];
     lse = a.lse[((int64_t)b * a.num_heads + h) * a.q_len + t];
-    float* dq = a.dq_acc + ((int64_t)bk * TG + R) * D + part * EPL;
+  }
+  if (live) {
+    float* dq = a.dq_acc + ((int64_t)bk * D + part * EPL) * TGP + R;
 #pragma unroll
-    for (int e = 0; e < EPL; e += 4) *reinterpret_cast<float4*>(dq + e) = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int e = 0; e < EPL; ++e) dq[(int64_t)e * TGP] = 0.f;
   }
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
@@ -412,36 +446,31 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const PrepArgs a) {
 }
 
 struct DqArgs {
-  const float* dq_acc;
+  const float* dq_acc;  // [B*Hkv][D][tgp]
   void* dq;
   int64_t sqb, sqh, sqm;
   float scale;
-  int batch, num_kv_heads, group, q_len;
+  int batch, num_kv_heads, group, q_len, tgp;
 };
 
+// Thread (bk, part, R), R fastest: 8 d of one row, read d-major (coalesced
+// across the threads of a part).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void bwd_dq_kernel(const DqArgs a) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t TG = (int64_t)a.q_len * a.group;
-  const int64_t row = gid / (D / 8);
-  const int part = (int)(gid % (D / 8));
-  if (row >= (int64_t)a.batch * a.num_kv_heads * TG) return;
-  const int64_t bk = row / TG;
-  const int R = (int)(row - bk * TG);
+  const int TG = a.q_len * a.group;
+  const int64_t per_bk = (int64_t)(D / 8) * TG;
+  if (gid >= (int64_t)a.batch * a.num_kv_heads * per_bk) return;
+  const int64_t bk = gid / per_bk;
+  const int rem = (int)(gid - bk * per_bk);
+  const int part = rem / TG, R = rem - part * TG;
   const int t = R / a.group, g = R - t * a.group;
   const int kvh = (int)(bk % a.num_kv_heads), b = (int)(bk / a.num_kv_heads);
-  const float4* src = reinterpret_cast<const float4*>(a.dq_acc + row * D + part * 8);
-  const float4 x0 = src[0], x1 = src[1];
+  const float* src = a.dq_acc + ((int64_t)bk * D + part * 8) * a.tgp + R;
   typedef T T8 __attribute__((ext_vector_type(8)));
   T8 o;
-  o[0] = (T)(x0.x * a.scale);
-  o[1] = (T)(x0.y * a.scale);
-  o[2] = (T)(x0.z * a.scale);
-  o[3] = (T)(x0.w * a.scale);
-  o[4] = (T)(x1.x * a.scale);
-  o[5] = (T)(x1.y * a.scale);
-  o[6] = (T)(x1.z * a.scale);
-  o[7] = (T)(x1.w * a.scale);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (T)(src[(int64_t)e * a.tgp] * a.scale);
   *reinterpret_cast<T8*>(static_cast<T*>(a.dq) + b * a.sqb + (int64_t)(kvh * a.group + g) * a.sqh +
                          (int64_t)t * a.sqm + part * 8) = o;
 }
@@ -458,23 +487,20 @@ struct VisArgs {
   int group, q_len, block_m, block_n, n_tree_blocks, tree_key_limit, n_tiles, n_tkeys;
 };
 
-// One workgroup per (tile, tree): the block states of the tile's q-blocks
-// (0 ZERO, -1 FULL, 1 + offset MIXED) expand into LDS, then each thread
-// writes the 32-row visibility words of its tree keys.
+// One workgroup per (tile, tree, 64 tree keys): the block states of the
+// tile's q-blocks (0 ZERO, -1 FULL, 1 + offset MIXED) expand into LDS, then
+// each thread decides one (key, row) bit and a ballot assembles the 32-row
+// words (lanes 0-31: one key, lanes 32-63: the next).
 __global__ __launch_bounds__(256) void bwd_vis_kernel(const VisArgs a) {
   __shared__ int st[kMaxStateInts];
   __shared__ int rps[72];
-  const int tile = blockIdx.x, tree = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int tile = blockIdx.x, tree = blockIdx.y, c0 = blockIdx.z * 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = a.group, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
   const int TG = a.q_len * G;
   const int r_lo = tile * kTileRows;
   const int r_hi = min(r_lo + kTileRows, TG) - 1;
   uint32_t* out = a.vis + (int64_t)tree * a.tree_stride + (int64_t)tile * a.n_tkeys;
-  if (r_lo > r_hi) {  // a padding tile: nothing visible
-    for (int c = tid; c < a.n_tkeys; c += 256) out[c] = 0u;
-    return;
-  }
   const int qb_lo = (r_lo / G) / BM, qb_hi = (r_hi / G) / BM, nqbc = qb_hi - qb_lo + 1;
   const int32_t* rp = a.row_ptr + tree * a.ms_row_ptr;
   const int32_t* ci = a.col_idx + tree * a.ms_col_idx;
@@ -491,22 +517,23 @@ __global__ __launch_bounds__(256) void bwd_vis_kernel(const VisArgs a) {
     if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
   }
   __syncthreads();
-  for (int c = tid; c < a.n_tkeys; c += 256) {
-    uint32_t w = 0;
-    if (c < a.tree_key_limit) {
-      const int tb = c / BN, cc = c - tb * BN;
-      for (int R = r_lo; R <= r_hi; ++R) {
-        const int t = R / G, qb = t / BM;
-        const int e = st[(qb - qb_lo) * ntb + tb];
-        bool bit = e < 0;
-        if (e > 0) {
-          const int flat = (t - qb * BM) * BN + cc;
-          bit = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 1u;
-        }
-        w |= (uint32_t)bit << (R - r_lo);
+  const int R = r_lo + (lane & 31);
+  const int t = R / G, qb = t / BM;
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {
+    const int c = c0 + pass * 8 + wave * 2 + (lane >> 5);  // this thread's tree key
+    bool bit = false;
+    if (R <= r_hi && c < a.tree_key_limit) {
+      const int tb = c / BN;
+      const int e = st[(qb - qb_lo) * ntb + tb];
+      bit = e < 0;
+      if (e > 0) {
+        const int flat = (t - qb * BM) * BN + (c - tb * BN);
+        bit = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 1u;
       }
     }
-    out[c] = w;
+    const uint64_t bal = __ballot(bit);
+    if ((lane & 31) == 0 && c < a.n_tkeys) out[c] = (uint32_t)(bal >> (lane & 32));
   }
 }
 
@@ -532,7 +559,7 @@ int make_bwd_plan(int batch, int num_kv_heads, int q_len, int kv_len, int prefix
   if ((int64_t)p->nqbc_max * n_tree_blocks > kMaxStateInts || p->nqbc_max + 1 > 72) return TSFA_ERR_UNSUPPORTED;
   const int64_t rows = (int64_t)batch * num_kv_heads;
   p->rowstat_bytes = align256((size_t)rows * p->n_tiles * kTileRows * 8);
-  p->dq_bytes = align256((size_t)rows * TG * head_dim * 4);
+  p->dq_bytes = align256((size_t)rows * p->n_tiles * kTileRows * head_dim * 4);
   p->vis_bytes = align256((size_t)n_trees * p->n_tiles * p->n_tkeys * 4 + 16);
   const int64_t items = rows * (p->n_pb + p->n_tb);
   if (items > (int64_t)INT32_MAX / 2 || (int64_t)n_trees * p->n_tiles * p->n_tkeys > ((int64_t)1 << 28))
@@ -558,7 +585,7 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
                      pa);
   if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
   if (has_tree) {
-    hipLaunchKernelGGL(bwd_vis_kernel, dim3(p.n_tiles, p.n_trees), dim3(256), 0, stream, va);
+    hipLaunchKernelGGL(bwd_vis_kernel, dim3(p.n_tiles, p.n_trees, p.n_tkeys / 64), dim3(256), 0, stream, va);
     if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
   }
   const unsigned grid = (unsigned)ba.items_per_xcd * 8;
@@ -732,6 +759,7 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   da.num_kv_heads = num_kv_heads;
   da.group = gqa_group_size;
   da.q_len = q_len;
+  da.tgp = p.n_tiles * kTileRows;
 
   const bool has_tree = p.n_tb > 0;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
