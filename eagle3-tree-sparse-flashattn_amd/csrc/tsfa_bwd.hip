@@ -46,11 +46,11 @@
 namespace tsfa {
 namespace bwd {
 
-constexpr int kWaves = 4;                 // 32 keys each
-constexpr int kBlockKeys = 32 * kWaves;   // keys per workgroup
+constexpr int kWaves = 8;                 // 4 key groups x 2 row groups
+constexpr int kBlockKeys = 128;           // keys per workgroup (32 per key group)
 constexpr int kTileRows = 32;             // query rows per tile
 constexpr int kMaxStateInts = 8192;       // block-state table of one tile (bwd_vis_kernel)
-constexpr int kBufs = 4;                  // Q / dO tile buffers: loads run 3 tiles ahead
+constexpr int kBufs = 2;                  // Q / dO tile buffers per row group: loads run one step ahead
 constexpr int kDqAtomics = 16;            // atomic instructions per wave per tile (one 32x32 dQ^T tile)
 
 // 16-byte-chunk XOR swizzle of a row-major [rows][D] LDS tile (row period
@@ -77,20 +77,19 @@ __device__ inline void dma16(const void* src, uint32_t lds_base) {
                : "v"(src), "s"(lds_base)
                : "memory", "m0");
 }
+// The same with a scalar base and a 32-bit lane offset (no per-lane 64-bit
+// address held in registers).
+__device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
-// s_waitcnt vmcnt(n) for a wave-uniform n in [LO, HI] (binary search over
-// the immediate forms).
-template <int LO, int HI> __device__ inline void vm_wait_n(int n) {
-  if constexpr (LO == HI) {
-    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(LO) : "memory");
-  } else {
-    constexpr int MID = (LO + HI) / 2;
-    if (n <= MID)
-      vm_wait_n<LO, MID>(n);
-    else
-      vm_wait_n<MID + 1, HI>(n);
-  }
+template <int N> __device__ inline void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 __device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const TSFA_LDS void*)p; }
@@ -108,22 +107,28 @@ struct BwdArgs {
   const uint32_t* vis;      // [n_trees][n_tiles][n_tkeys] visibility words of tree keys
   int64_t sqb, sqh, sqm, skb, skh, skn, svb, svh, svn, sdob, sdoh, sdom, sdkb, sdkh, sdkn, sdvb, sdvh, sdvn;
   int64_t vis_tree_stride;  // 0: one tree for the batch
-  float scale_log2;         // |sm_scale| * log2(e), never 0
-  float dk_scale;           // |sm_scale| (Q enters negated for a negative scale)
-  int neg_q;
+  float scale_log2;         // sm_scale * log2(e) (signed), never 0
+  float dk_scale;           // sm_scale
   int num_kv_heads, group, q_len, kv_len, prefix_len;
   int n_tiles, n_pb, n_tb, n_tkeys;
   int n_items, items_per_xcd;
+  uint32_t group_magic;     // floor(2^32 / group) + 1 (group > 1): R / group = umulhi(R, magic) for R < 2^21
 };
 
 template <int D> constexpr size_t kv_lds_bytes() {
-  // K block | kBufs x (Q tile, dO tile) | kBufs x 32 row stats | kBufs x 128 mask words | dS [128 keys][32 rows]
-  return (size_t)kBlockKeys * D * 2 + 2 * kBufs * (size_t)kTileRows * D * 2 + kBufs * kTileRows * 8 +
-         kBufs * kBlockKeys * 4 + (size_t)kBlockKeys * kTileRows * 2;
+  // K block | V block | 2 groups x kBufs x (Q tile, dO tile) | 2 x kBufs x 32 row stats |
+  // 2 x kBufs x 128 mask words | 2 x dS [128 keys][32 rows] | 64 bytes of dummy load targets
+  return 2 * (size_t)kBlockKeys * D * 2 + 2 * 2 * kBufs * (size_t)kTileRows * D * 2 + 2 * kBufs * kTileRows * 8 +
+         2 * kBufs * kBlockKeys * 4 + 2 * (size_t)kBlockKeys * kTileRows * 2 + 64;
 }
 
+// Workgroup = 8 waves: key group kg = wave & 3 owns keys key0 + 32kg + [0, 32);
+// row group rg = wave >> 2 takes every other 32-row tile.  Each SIMD runs one
+// wave of each row group, so one wave's softmax-like VALU work and LDS waits
+// overlap the other's MFMAs.  Both groups accumulate dK^T / dV^T of the same
+// keys; group 1 hands its sums to group 0 through LDS at the end.
 template <typename T, int D>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void bwd_kv_kernel(const BwdArgs a) {
   typedef typename Mma<T>::vec8 V8;
   constexpr int ROWB = D * 2;                 // bytes of one row
@@ -134,21 +139,25 @@ void bwd_kv_kernel(const BwdArgs a) {
   constexpr int TILE_B = kTileRows * ROWB;
   constexpr int KBLK_B = kBlockKeys * ROWB;
   constexpr int LPT = TILE_B / 1024;          // 1 KB loads per Q (or dO) tile
-  constexpr int TPW = 2 * LPT / kWaves;       // tile loads per wave
-  constexpr int KPW = KBLK_B / 1024 / kWaves; // K block loads per wave
-  static_assert(TPW >= 1 && KPW >= 1 && 2 * LPT == TPW * kWaves, "load split");
-  static_assert(DT <= kWaves, "one dQ d-tile per wave");
+  constexpr int TPW = 2 * LPT / 4;            // tile loads per wave (4 waves per row group)
+  constexpr int KPW = 2 * KBLK_B / 1024 / kWaves;  // K + V block loads per wave
+  constexpr int LPW = TPW + 1;                // vector-memory instructions a wave issues per tile
+  static_assert(TPW >= 1 && KPW >= 1 && 2 * LPT == TPW * 4, "load split");
+  static_assert(DT <= 4, "one dQ d-tile per wave of a row group");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   unsigned char* kblk = smem;
-  unsigned char* tiles = kblk + KBLK_B;  // buffer s: Q at tiles + 2*s*TILE_B, dO right after
-  float2* rs = reinterpret_cast<float2*>(tiles + 2 * kBufs * TILE_B);
-  uint32_t* visw = reinterpret_cast<uint32_t*>(rs + kBufs * kTileRows);
-  unsigned char* dsl = reinterpret_cast<unsigned char*>(visw + kBufs * kBlockKeys);
+  unsigned char* vblk = kblk + KBLK_B;
+  unsigned char* tiles = vblk + KBLK_B;  // group g, buffer s: Q at tiles + 2*(g*kBufs + s)*TILE_B, dO after
+  float2* rs = reinterpret_cast<float2*>(tiles + 2 * 2 * kBufs * TILE_B);          // [g][s][32]
+  uint32_t* visw = reinterpret_cast<uint32_t*>(rs + 2 * kBufs * kTileRows);        // [g][s][128]
+  unsigned char* dsl = reinterpret_cast<unsigned char*>(visw + 2 * kBufs * kBlockKeys);  // [g][128 keys][32 rows]
+  unsigned char* dummy = dsl + 2 * kBlockKeys * kTileRows * 2;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = wave & 3, rg = wave >> 2;
   const int ln = lane & 31, lh = lane >> 5;
 
   // XCD-aware item order: consecutive block ids go to different XCDs and each
@@ -167,8 +176,7 @@ void bwd_kv_kernel(const BwdArgs a) {
   const int G = a.group;
   const int TG = a.q_len * G;
   const int TGP = a.n_tiles * kTileRows;
-  const float sl2 = a.scale_log2;
-  const short qsgn = a.neg_q ? (short)0x8000 : (short)0;
+  const float sl2 = a.scale_log2;  // signed: exp2(s * sl2 - lse2) for either sign of sm_scale
 
   const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
@@ -178,71 +186,69 @@ void bwd_kv_kernel(const BwdArgs a) {
   const uint32_t* visbase =
       a.vis + (int64_t)b * a.vis_tree_stride + (tree_blk ? (int64_t)tkb * kBlockKeys : 0);
 
-  // K block HBM -> LDS (keys past the end repeat the last key; masked).
-  {
+  // K and V blocks HBM -> LDS (keys past the end repeat the last key; masked).
 #pragma unroll
-    for (int i = 0; i < KPW; ++i) {
-      const int u = wave * KPW + i;
-      const int row = u * RPL + lane / CPR, pos = lane % CPR;
-      const int key = min(key0 + row, a.kv_len - 1);
-      dma16(kbase + (int64_t)key * a.skn + ((pos ^ swz<D>(row)) << 3), lds_addr(kblk + u * 1024));
-    }
+  for (int i = 0; i < KPW; ++i) {
+    const int u = wave * KPW + i;  // 0 .. 2*KBLK_B/1024 - 1: K loads, then V loads
+    const bool is_v = u >= KBLK_B / 1024;
+    const int ul = is_v ? u - KBLK_B / 1024 : u;
+    const int row = ul * RPL + lane / CPR, pos = lane % CPR;
+    const int key = min(key0 + row, a.kv_len - 1);
+    const T* src = (is_v ? vbase + (int64_t)key * a.svn : kbase + (int64_t)key * a.skn) + ((pos ^ swz<D>(row)) << 3);
+    dma16(src, lds_addr((is_v ? vblk : kblk) + ul * 1024));
   }
-  // Q / dO tile j HBM -> LDS buffer s, with its row statistics and (tree
-  // blocks) the 128 keys' mask words.  Rows past the end repeat the last row;
-  // their statistics make P = dS = 0.
-  auto issue_tile = [&](int j, int s) {
-    unsigned char* qt = tiles + 2 * s * TILE_B;
-#pragma unroll
-    for (int i = 0; i < TPW; ++i) {
-      const int u = wave * TPW + i;  // 0 .. 2*LPT-1: Q loads, then dO loads
-      const bool is_do = u >= LPT;
-      const int ul = is_do ? u - LPT : u;
-      const int row = ul * RPL + lane / CPR, pos = lane % CPR;
-      const int R = min(j * kTileRows + row, TG - 1);
-      const int t = R / G;
-      const int g = R - t * G;
-      const T* src = is_do ? dobase + g * a.sdoh + (int64_t)t * a.sdom : qbase + g * a.sqh + (int64_t)t * a.sqm;
-      dma16(src + ((pos ^ swz<D>(row)) << 3), lds_addr(qt + (is_do ? TILE_B : 0) + ul * 1024));
-    }
-    if (wave == 0 && lane < kTileRows * 8 / 16)
-      dma16(rsbase + j * kTileRows + 2 * lane, lds_addr(rs + s * kTileRows));
-    if (tree_blk && wave == 1 && lane < kBlockKeys * 4 / 16)
-      dma16(visbase + (int64_t)j * a.n_tkeys + 4 * lane, lds_addr(visw + s * kBlockKeys));
-  };
-  // The key blocks of one (b, kv head) start their walk at different tiles
-  // (block kb at tile kb * n_tiles / nkb), so the dQ atomics of concurrent
-  // blocks land on different rows instead of queueing on the same ones.
+
+  // The tiles of row group rg: step n handles tile tile_at(2n + rg).  The key
+  // blocks of one (b, kv head) start their walk at different tiles (block kb
+  // at tile kb * n_tiles / nkb), so the dQ atomics of concurrent blocks land
+  // on different rows.
   const int j0 = (int)((int64_t)kb * a.n_tiles / nkb);
   auto tile_at = [&](int i) {
     const int j = j0 + i;
     return j >= a.n_tiles ? j - a.n_tiles : j;
   };
-  // vector-memory instructions this wave issues per tile (wave-uniform)
-  const int lpw = TPW + (wave == 0 ? 1 : 0) + ((tree_blk && wave == 1) ? 1 : 0);
-  for (int i = 0; i < kBufs - 1 && i < a.n_tiles; ++i) issue_tile(tile_at(i), i);
+  const int n_steps = (a.n_tiles + 1) >> 1;
+  const int my_tiles = (a.n_tiles + 1 - rg) >> 1;  // steps with a tile for this group
 
-  // V^T operand of dP = dO V^T (B[d][key]: lane (key ln, lh) holds d = 16kk +
-  // 8lh + [0, 8)), in registers for the whole walk.  Loaded after the DMAs
-  // and consumed at once: the compiler's wait for them then covers the DMAs
-  // too, which the first tile needs anyway.
-  const int mykey = key0 + 32 * wave + ln;
+  // Q / dO tile j -> this group's buffer s, with its row statistics and (tree
+  // blocks) the 128 keys' mask words.  Every wave issues exactly LPW loads
+  // per tile: its share of Q and dO plus one more (the row statistics for key
+  // group 0, the mask words for key group 1 of a tree block, else one lane
+  // into a dummy LDS slot), so the waits below are compile-time counts.
+  // Rows past the end repeat the last row; their statistics make P = dS = 0.
+  auto issue_tile = [&](int j, int s) {
+    unsigned char* qt = tiles + 2 * (rg * kBufs + s) * TILE_B;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      const int u = kg * TPW + i;  // 0 .. 2*LPT-1: Q loads, then dO loads
+      const bool is_do = u >= LPT;
+      const int ul = is_do ? u - LPT : u;
+      const int row = ul * RPL + lane / CPR, pos = lane % CPR;
+      const int R = min(j * kTileRows + row, TG - 1);
+      const int t = G == 1 ? R : (int)__umulhi((uint32_t)R, a.group_magic);
+      const int g = R - t * G;
+      const T* src = is_do ? dobase + g * a.sdoh + (int64_t)t * a.sdom : qbase + g * a.sqh + (int64_t)t * a.sqm;
+      dma16(src + ((pos ^ swz<D>(row)) << 3), lds_addr(qt + (is_do ? TILE_B : 0) + ul * 1024));
+    }
+    if (kg == 0) {
+      if (lane < kTileRows * 8 / 16)
+        dma16_s(rsbase + j * kTileRows, 16u * lane, lds_addr(rs + (rg * kBufs + s) * kTileRows));
+    } else if (kg == 1 && tree_blk) {
+      if (lane < kBlockKeys * 4 / 16)
+        dma16_s(visbase + (int64_t)j * a.n_tkeys, 16u * lane, lds_addr(visw + (rg * kBufs + s) * kBlockKeys));
+    } else if (lane == 0) {
+      dma16_s(rsbase, 0u, lds_addr(dummy + 16 * (wave & 3)));
+    }
+  };
+  for (int i = 0; i < kBufs - 1 && i < my_tiles; ++i) issue_tile(tile_at(2 * i + rg), i);
+
+  const int mykey = key0 + 32 * kg + ln;
   const bool key_ok = mykey < key_end && mykey < key0 + kBlockKeys;
-  i16x8 vf[KSTEPS];
-  {
-    const T* vp = vbase + (int64_t)min(mykey, a.kv_len - 1) * a.svn + 8 * lh;
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) vf[kk] = *reinterpret_cast<const i16x8*>(vp + kk * 16);
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(vf[kk]));
-  }
 
   // LDS offsets (bytes).  Row reads: lane (row ln, lh) reads chunk 2kk + lh.
   // Transposed reads: lane (x = lane>>4, i = lane&15) reads 8 bytes of row
   // 8jj + 4(x>>1) + (i>>2) (+16 per k-step) at d = dt*32 + 16(x&1) + 4(i&3);
   // after the transpose it holds rows +[0,4) of d = dt*32 + 16(x&1) + i.
-  // The offsets are recomputed where they are used (a few VALU ops) rather
-  // than held across the tile loop: registers are the scarce resource here.
   const int vx = lane >> 4, vi = lane & 15;
   auto r_off = [&](int kk) { return ln * ROWB + (((2 * kk + lh) ^ swz<D>(ln)) << 4); };
   auto t_off = [&](int dt, int jj) {
@@ -252,11 +258,12 @@ void bwd_kv_kernel(const BwdArgs a) {
   };
   // dS [key][row] (64 bytes per key): transposed read of keys 8jj + 4(x>>1) +
   // (i>>2) at rows 16(x&1) + 4(i&3).
-  int ds_toff[2];
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj)
-    ds_toff[jj] = (8 * jj + 4 * (vx >> 1) + (vi >> 2)) * 64 + (16 * (vx & 1) + 4 * (vi & 3)) * 2;
-  const unsigned char* kmine = kblk + 32 * wave * ROWB;
+  auto ds_toff = [&](int jj) {
+    return (8 * jj + 4 * (vx >> 1) + (vi >> 2)) * 64 + (16 * (vx & 1) + 4 * (vi & 3)) * 2;
+  };
+  const unsigned char* kmine = kblk + 32 * kg * ROWB;
+  const unsigned char* vmine = vblk + 32 * kg * ROWB;
+  unsigned char* dsg = dsl + rg * kBlockKeys * kTileRows * 2;
 
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -272,74 +279,80 @@ void bwd_kv_kernel(const BwdArgs a) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
-  for (int it = 0; it < a.n_tiles; ++it) {
-    const int s = it & (kBufs - 1);
-    const int j = tile_at(it);
-    // Wait for tile `it` (and on the first step the K block and V): vector
-    // memory completes in issue order, and issued after this tile's loads
-    // are the loads of the next min(2, left) tiles and the dQ atomics of the
-    // last min(it, 3) steps, none of which this step needs.
-    {
-      const int later_tiles = min(kBufs - 2, a.n_tiles - 1 - it);
-      const int later_atomics = wave < DT ? min(it, kBufs - 1) * kDqAtomics : 0;
-      vm_wait_n<0, 63>(it == 0 ? later_tiles * lpw : later_tiles * lpw + later_atomics);
+  for (int n = 0; n < n_steps; ++n) {
+    const int s = n & (kBufs - 1);
+    const bool has = n < my_tiles;  // group 1 has no tile on the last step of an odd count
+    // Wait for this group's tile of step n (and on the first step the K / V
+    // blocks): vector memory completes in issue order; in the steady state
+    // issued after this tile's loads are the next kBufs-2 tiles' loads and the
+    // dQ atomics of the last kBufs-1 steps.  The first and last steps wait for
+    // everything.
+    if (n >= kBufs - 1 && n + kBufs - 2 < my_tiles) {
+      if (kg < DT)
+        vm_wait<(kBufs - 2) * LPW + (kBufs - 1) * kDqAtomics>();
+      else
+        vm_wait<(kBufs - 2) * LPW>();
+    } else {
+      vm_wait<0>();
     }
-    // every wave is done with tile it-1: its buffer (the one tile it+3 goes
-    // to) and the dS area are free
+    // every wave is done with step n-1: its buffers (the ones step n+kBufs-1
+    // loads into) and the dS areas are free
     sync_lds();
-    if (it + kBufs - 1 < a.n_tiles) issue_tile(tile_at(it + kBufs - 1), (it + kBufs - 1) & (kBufs - 1));
-    const unsigned char* qt = tiles + 2 * s * TILE_B;
+    if (n + kBufs - 1 < my_tiles) issue_tile(tile_at(2 * (n + kBufs - 1) + rg), (n + kBufs - 1) & (kBufs - 1));
+    const int j = tile_at(2 * n + rg);
+    const unsigned char* qt = tiles + 2 * (rg * kBufs + s) * TILE_B;
     const unsigned char* dot = qt + TILE_B;
 
-    // S = Q K^T, dP = dO V^T: M = rows, N = keys; lane (key ln, lh) holds
-    // rows 8(i/4) + 4lh + i%4 of its key.
-    f32x16 sc, dp;
+    if (has) {
+      // S = Q K^T, dP = dO V^T: M = rows, N = keys; lane (key ln, lh) holds
+      // rows 8(i/4) + 4lh + i%4 of its key.
+      f32x16 sc, dp;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sc[i] = dp[i] = 0.f;
+      for (int i = 0; i < 16; ++i) sc[i] = dp[i] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) {
-      const int ro = r_off(kk);
-      const i16x8 qa = *reinterpret_cast<const i16x8*>(qt + ro) ^ qsgn;
-      const i16x8 kf = *reinterpret_cast<const i16x8*>(kmine + ro);
-      const i16x8 da = *reinterpret_cast<const i16x8*>(dot + ro);
-      sc = Mma<T>::run(bit_cast<V8>(qa), bit_cast<V8>(kf), sc);
-      dp = Mma<T>::run(bit_cast<V8>(da), bit_cast<V8>(vf[kk]), dp);
-    }
-    // P and dS from the row statistics of the lane's 16 rows (read one group
-    // of 4 rows at a time) and its key's mask word.
-    uint32_t w = key_ok ? 0xffffffffu : 0u;
-    if (tree_blk) w &= visw[s * kBlockKeys + 32 * wave + ln];
-    V8 pb[2], db[2];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float4* rp = reinterpret_cast<const float4*>(rs + s * kTileRows + 8 * q + 4 * lh);
-      const float4 st0 = rp[0], st1 = rp[1];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = 4 * q + e, m = 8 * q + 4 * lh + e;
-        const float4 pr = (e < 2) ? st0 : st1;
-        const float lse2 = (e & 1) ? pr.z : pr.x;
-        const float dvr = (e & 1) ? pr.w : pr.y;
-        const float p = ((w >> m) & 1u) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], sl2, -lse2)) : 0.f;
-        pb[i >> 3][i & 7] = (T)p;
-        db[i >> 3][i & 7] = (T)(p * (dp[i] - dvr));
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        const int ro = r_off(kk);
+        const i16x8 qa = *reinterpret_cast<const i16x8*>(qt + ro);
+        const i16x8 kf = *reinterpret_cast<const i16x8*>(kmine + ro);
+        const i16x8 da = *reinterpret_cast<const i16x8*>(dot + ro);
+        const i16x8 vf = *reinterpret_cast<const i16x8*>(vmine + ro);
+        sc = Mma<T>::run(bit_cast<V8>(qa), bit_cast<V8>(kf), sc);
+        dp = Mma<T>::run(bit_cast<V8>(da), bit_cast<V8>(vf), dp);
       }
-    }
-    // dV^T += dO^T P, dK^T += Q^T dS: M = d, N = keys, k-step s2 covers rows
-    // 16s2 + 8(e/4) + 4lh + e%4 -- elements 8s2 .. 8s2+7 of the accumulator.
+      // P and dS from the row statistics of the lane's 16 rows (one group of
+      // 4 rows at a time) and its key's mask word.
+      uint32_t w = key_ok ? 0xffffffffu : 0u;
+      if (tree_blk) w &= visw[(rg * kBufs + s) * kBlockKeys + 32 * kg + ln];
+      V8 pb[2], db[2];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int q = 0; q < 4; ++q) {
+        const float4* rp = reinterpret_cast<const float4*>(rs + (rg * kBufs + s) * kTileRows + 8 * q + 4 * lh);
+        const float4 st0 = rp[0], st1 = rp[1];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const i16x8 doT = tr_pair(dot + 16 * s2 * ROWB, dt);
-        const i16x8 qT = tr_pair(qt + 16 * s2 * ROWB, dt) ^ qsgn;
-        dv[dt] = Mma<T>::run(bit_cast<V8>(doT), pb[s2], dv[dt]);
-        dk[dt] = Mma<T>::run(bit_cast<V8>(qT), db[s2], dk[dt]);
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * q + e, m = 8 * q + 4 * lh + e;
+          const float4 pr = (e < 2) ? st0 : st1;
+          const float lse2 = (e & 1) ? pr.z : pr.x;
+          const float dvr = (e & 1) ? pr.w : pr.y;
+          const float p = ((w >> m) & 1u) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], sl2, -lse2)) : 0.f;
+          pb[i >> 3][i & 7] = (T)p;
+          db[i >> 3][i & 7] = (T)(p * (dp[i] - dvr));
+        }
       }
-    // dS of the wave's keys -> LDS [key][row]: rows 8q + 4lh + [0, 4) are
-    // elements 4q .. 4q+3.
-    {
-      unsigned char* dst = dsl + (32 * wave + ln) * 64 + 8 * lh;
+      // dV^T += dO^T P, dK^T += Q^T dS: M = d, N = keys, k-step s2 covers rows
+      // 16s2 + 8(e/4) + 4lh + e%4 -- elements 8s2 .. 8s2+7 of the accumulator.
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const i16x8 doT = tr_pair(dot + 16 * s2 * ROWB, dt);
+          const i16x8 qT = tr_pair(qt + 16 * s2 * ROWB, dt);
+          dv[dt] = Mma<T>::run(bit_cast<V8>(doT), pb[s2], dv[dt]);
+          dk[dt] = Mma<T>::run(bit_cast<V8>(qT), db[s2], dk[dt]);
+        }
+      // dS of the wave's keys -> this group's LDS [key][row]: rows 8q + 4lh
+      // + [0, 4) are elements 4q .. 4q+3.
+      unsigned char* dst = dsg + (32 * kg + ln) * 64 + 8 * lh;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const i16x8 e = bit_cast<i16x8>(db[q >> 1]);
@@ -348,30 +361,50 @@ void bwd_kv_kernel(const BwdArgs a) {
       }
     }
     sync_lds();
-    // dQ^T = K^T dS^T over the workgroup's 128 keys (M = d-tile `wave`, N =
-    // rows, 8 k-steps), added to the fp32 accumulator.
-    if (wave < DT) {
+    // dQ^T = K^T dS^T over the workgroup's 128 keys (M = d-tile kg, N = rows,
+    // 8 k-steps), added to the fp32 accumulator.
+    if (has && kg < DT) {
       f32x16 acc;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < kBlockKeys / 16; ++ks) {
-        const i16x8 kT = tr_pair(kblk + 16 * ks * ROWB, wave);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsl + ds_toff[0] + 16 * ks * 64));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsl + ds_toff[1] + 16 * ks * 64));
+        const i16x8 kT = tr_pair(kblk + 16 * ks * ROWB, kg);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsg + ds_toff(0) + 16 * ks * 64));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsg + ds_toff(1) + 16 * ks * 64));
         const i16x8 dsT = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         acc = Mma<T>::run(bit_cast<V8>(kT), bit_cast<V8>(dsT), acc);
       }
-      // lane (row ln, lh) holds d = wave*32 + 8(i/4) + 4lh + i%4; the
+      // lane (row ln, lh) holds d = kg*32 + 8(i/4) + 4lh + i%4; the
       // accumulator is d-major, so each instruction's 64 lanes cover two
       // whole 128-byte lines (32 rows at two d).  Padding rows add 0.
-      float* dst = a.dq_acc + ((int64_t)bk * D + wave * 32 + 4 * lh) * TGP + j * kTileRows + ln;
+      float* dq = a.dq_acc + ((int64_t)bk * D + kg * 32 + 4 * lh) * TGP + j * kTileRows + ln;
 #pragma unroll
-      for (int i = 0; i < kDqAtomics; ++i) atomicAdd(dst + (int64_t)(8 * (i >> 2) + (i & 3)) * TGP, acc[i]);
+      for (int i = 0; i < kDqAtomics; ++i) atomicAdd(dq + (int64_t)(8 * (i >> 2) + (i & 3)) * TGP, acc[i]);
     }
   }
 
-  // dK = |sm_scale| dK^T, dV = dV^T: lane (key ln, lh) holds d = dt*32 +
+  // Row group 1 hands dK^T / dV^T to row group 0 through LDS (the K / V
+  // blocks and tile buffers at the start of LDS are free now): register r of
+  // lane l at xch[kg][r][l].
+  vm_wait<0>();
+  sync_lds();
+  float* xch = reinterpret_cast<float*>(smem);
+  static_assert(4 * 2 * DT * 16 * 64 * 4 <= 2 * KBLK_B + 2 * 2 * kBufs * TILE_B, "exchange fits in K, V and tiles");
+  float* xw = xch + kg * (2 * DT * 16 * 64);
+  if (rg == 1) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        xw[((2 * dt) * 16 + i) * 64 + lane] = dk[dt][i];
+        xw[((2 * dt + 1) * 16 + i) * 64 + lane] = dv[dt][i];
+      }
+  }
+  sync_lds();
+  if (rg == 1) return;
+
+  // dK = sm_scale dK^T, dV = dV^T: lane (key ln, lh) holds d = dt*32 +
   // 8(i/4) + 4lh + i%4 of its key.
   if (key_ok) {
     T* dkp = static_cast<T*>(a.dk) + b * a.sdkb + kvh * a.sdkh + (int64_t)mykey * a.sdkn + 4 * lh;
@@ -384,8 +417,9 @@ void bwd_kv_kernel(const BwdArgs a) {
         T4 x, y;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          x[e] = (T)(dk[dt][4 * q + e] * a.dk_scale);
-          y[e] = (T)dv[dt][4 * q + e];
+          const int i = 4 * q + e;
+          x[e] = (T)((dk[dt][i] + xw[((2 * dt) * 16 + i) * 64 + lane]) * a.dk_scale);
+          y[e] = (T)(dv[dt][i] + xw[((2 * dt + 1) * 16 + i) * 64 + lane]);
         }
         *reinterpret_cast<T4*>(dkp + dt * 32 + 8 * q) = x;
         *reinterpret_cast<T4*>(dvp + dt * 32 + 8 * q) = y;
@@ -548,6 +582,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 int make_bwd_plan(int batch, int num_kv_heads, int q_len, int kv_len, int prefix_len, int gqa, int head_dim,
                   int block_m, int n_tree_blocks, int n_trees, BwdPlan* p) {
   const int64_t TG = (int64_t)q_len * gqa;
+  if (TG >= ((int64_t)1 << 22)) return TSFA_ERR_UNSUPPORTED;  // the kernel's row -> token division is exact below
   p->n_tiles = (int)((TG + kTileRows - 1) / kTileRows);
   p->n_pb = ceil_div(prefix_len, kBlockKeys);
   p->n_tb = ceil_div(kv_len - prefix_len, kBlockKeys);
@@ -660,7 +695,8 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   const int tree_key_limit =
       (int)std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
 
-  float sl2 = fabsf(sm_scale) * 1.4426950408889634f;
+  // signed: P = exp2(q.k * sl2 - lse2); a zero scale becomes a vanishing one
+  float sl2 = sm_scale * 1.4426950408889634f;
   if (sl2 == 0.f) sl2 = 1e-30f;
 
   PrepArgs pa;
@@ -734,8 +770,7 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   ba.sdvn = strides[30];
   ba.vis_tree_stride = n_trees > 1 ? va.tree_stride : 0;
   ba.scale_log2 = sl2;
-  ba.dk_scale = fabsf(sm_scale);
-  ba.neg_q = sm_scale < 0.f ? 1 : 0;
+  ba.dk_scale = sm_scale;
   ba.num_kv_heads = num_kv_heads;
   ba.group = gqa_group_size;
   ba.q_len = q_len;
@@ -746,6 +781,7 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   ba.n_tb = p.n_tb;
   ba.n_tkeys = p.n_tkeys;
   ba.n_items = batch * num_kv_heads * (p.n_pb + p.n_tb);
+  ba.group_magic = gqa_group_size > 1 ? (uint32_t)((((uint64_t)1) << 32) / (uint64_t)gqa_group_size + 1) : 0u;
   ba.items_per_xcd = (ba.n_items + 7) / 8;
 
   DqArgs da;
