@@ -249,7 +249,7 @@ def backward_timing(w, mask, qd, ks, vs, meta, steps: int, fwd_flops: float):
     return {"us_per_call": round(us, 3), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
             "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
             "achieved_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "kernels": "prep + tree visibility + key-parallel dK/dV/dQ + dQ convert (four launches)"}
+            "kernels": "prep + tree visibility + key-parallel dK/dV + row-parallel dQ + dQ convert (five launches)"}
 
 
 def calibrate_copy(mib: int, reps: int):

@@ -10,30 +10,32 @@
 // summed over the G query heads of each kv head.  P is recomputed from the
 // forward's per-row log-sum-exp (tsfa_fwd_lse).
 //
-// Kernels (one call = four launches, no host synchronisation):
+// Kernels (one call = five launches, no host synchronisation):
 //   * bwd_prep_kernel: per query row (16 lanes): Dv = rowsum(dO * O) in fp32,
 //     the log2-domain LSE, and the row of the fp32 dQ accumulator cleared.
 //     Rows with no visible key (LSE = -inf) and the padding rows of the last
 //     32-row tile get LSE = +inf and Dv = 0, so their P and dS are exactly 0;
 //   * bwd_vis_kernel: per (32-row tile, tree key) a visibility word (bit m:
 //     row 32*tile + m sees the key), from the CSR metadata;
-//   * bwd_kv_kernel (key-parallel): a workgroup owns 128 keys of one (batch,
-//     kv head) -- prefix keys and tree keys in separate blocks -- as 4 waves x
-//     32 keys, keeps dK^T and dV^T of its keys in registers and walks every
+//   * bwd_kv_kernel (key-parallel, dK and dV): a workgroup owns 128 keys of
+//     one (batch, kv head) -- prefix keys and tree keys in separate blocks --
+//     as 4 key groups x 2 row groups of waves; each wave keeps dK^T and dV^T
+//     of its 32 keys in registers while its row group walks every other
 //     32-row tile of the (batch, kv head) (rows token-major, r = t*G + g, as
-//     in the forward).  Per tile, on v_mfma_f32_32x32x16:
-//       S = Q K^T and dP = dO V^T (a lane holds one key, so the LSE / Dv of
-//       a row are per-element LDS reads and the key's mask word is one read),
-//       dV^T += dO^T P and dK^T += Q^T dS with P and dS taken straight from
-//       the S / dP accumulators (the MFMA k order is permuted to the order
-//       the accumulator holds rows in; the dO^T / Q^T operands come from
-//       ds_read_b64_tr_b16 in the same order), then dQ^T = K^T dS^T over the
-//       workgroup's 128 keys (dS through LDS, one d-tile per wave) added to
-//       the fp32 accumulator with global atomics.  Q / dO tiles, their row
-//       statistics and the tree block's mask words move HBM -> LDS with
-//       global_load_lds, double-buffered; one LDS copy of each tile serves
-//       both the row reads of S / dP and the transposed reads of dV / dK
-//       (a swizzle that is conflict-free for both patterns);
+//     in the forward).  Per tile, on v_mfma_f32_32x32x16: S = Q K^T and dP =
+//     dO V^T (a lane holds one key), then dV^T += dO^T P and dK^T += Q^T dS
+//     with P and dS taken straight from the S / dP accumulators (the MFMA k
+//     order is permuted to the order the accumulator holds rows in; the dO^T
+//     / Q^T operands come from ds_read_b64_tr_b16 in the same order).  Q / dO
+//     tiles, their row statistics and the tree block's mask words move HBM
+//     -> LDS with global_load_lds, double-buffered per row group; one LDS
+//     copy of each tile serves both the row reads and the transposed reads
+//     (a swizzle that is conflict-free for both patterns).  The row groups
+//     merge their sums through LDS at the end;
+//   * bwd_dq_main_kernel (row-parallel, dQ): a workgroup owns 128 rows and a
+//     split of the 32-key units; S^T, dP^T, dS^T recomputed per unit and dQ^T
+//     += K^T dS^T accumulated in registers, added once per workgroup to the
+//     fp32 accumulator (atomics only between the splits of one chunk);
 //   * bwd_dq_kernel: dQ = sm_scale * accumulator in the input dtype.
 
 #include <math.h>
@@ -51,7 +53,6 @@ constexpr int kBlockKeys = 128;           // keys per workgroup (32 per key grou
 constexpr int kTileRows = 32;             // query rows per tile
 constexpr int kMaxStateInts = 8192;       // block-state table of one tile (bwd_vis_kernel)
 constexpr int kBufs = 2;                  // Q / dO tile buffers per row group: loads run one step ahead
-constexpr int kDqAtomics = 16;            // atomic instructions per wave per tile (one 32x32 dQ^T tile)
 
 // 16-byte-chunk XOR swizzle of a row-major [rows][D] LDS tile (row period
 // 16), conflict-free for both read patterns of the kernel:
@@ -113,13 +114,16 @@ struct BwdArgs {
   int n_tiles, n_pb, n_tb, n_tkeys;
   int n_items, items_per_xcd;
   uint32_t group_magic;     // floor(2^32 / group) + 1 (group > 1): R / group = umulhi(R, magic) for R < 2^21
+  // row-parallel dQ kernel
+  int n_pu, n_tu;           // prefix / tree units of 32 keys
+  int n_chunks, n_splits, units_per_split, q_items, q_items_per_xcd;
 };
 
 template <int D> constexpr size_t kv_lds_bytes() {
   // K block | V block | 2 groups x kBufs x (Q tile, dO tile) | 2 x kBufs x 32 row stats |
-  // 2 x kBufs x 128 mask words | 2 x dS [128 keys][32 rows] | 64 bytes of dummy load targets
+  // 2 x kBufs x 128 mask words | 64 bytes of dummy load targets
   return 2 * (size_t)kBlockKeys * D * 2 + 2 * 2 * kBufs * (size_t)kTileRows * D * 2 + 2 * kBufs * kTileRows * 8 +
-         2 * kBufs * kBlockKeys * 4 + 2 * (size_t)kBlockKeys * kTileRows * 2 + 64;
+         2 * kBufs * kBlockKeys * 4 + 64;
 }
 
 // Workgroup = 8 waves: key group kg = wave & 3 owns keys key0 + 32kg + [0, 32);
@@ -142,8 +146,8 @@ void bwd_kv_kernel(const BwdArgs a) {
   constexpr int TPW = 2 * LPT / 4;            // tile loads per wave (4 waves per row group)
   constexpr int KPW = 2 * KBLK_B / 1024 / kWaves;  // K + V block loads per wave
   constexpr int LPW = TPW + 1;                // vector-memory instructions a wave issues per tile
+  static_assert(kBufs == 2, "the exchange at the end reuses the K, V and tile areas");
   static_assert(TPW >= 1 && KPW >= 1 && 2 * LPT == TPW * 4, "load split");
-  static_assert(DT <= 4, "one dQ d-tile per wave of a row group");
 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   unsigned char* kblk = smem;
@@ -151,8 +155,7 @@ void bwd_kv_kernel(const BwdArgs a) {
   unsigned char* tiles = vblk + KBLK_B;  // group g, buffer s: Q at tiles + 2*(g*kBufs + s)*TILE_B, dO after
   float2* rs = reinterpret_cast<float2*>(tiles + 2 * 2 * kBufs * TILE_B);          // [g][s][32]
   uint32_t* visw = reinterpret_cast<uint32_t*>(rs + 2 * kBufs * kTileRows);        // [g][s][128]
-  unsigned char* dsl = reinterpret_cast<unsigned char*>(visw + 2 * kBufs * kBlockKeys);  // [g][128 keys][32 rows]
-  unsigned char* dummy = dsl + 2 * kBlockKeys * kTileRows * 2;
+  unsigned char* dummy = reinterpret_cast<unsigned char*>(visw + 2 * kBufs * kBlockKeys);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -256,14 +259,8 @@ void bwd_kv_kernel(const BwdArgs a) {
     const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
     return r * ROWB + (((d >> 3) ^ swz<D>(r)) << 4) + ((d & 7) << 1);
   };
-  // dS [key][row] (64 bytes per key): transposed read of keys 8jj + 4(x>>1) +
-  // (i>>2) at rows 16(x&1) + 4(i&3).
-  auto ds_toff = [&](int jj) {
-    return (8 * jj + 4 * (vx >> 1) + (vi >> 2)) * 64 + (16 * (vx & 1) + 4 * (vi & 3)) * 2;
-  };
   const unsigned char* kmine = kblk + 32 * kg * ROWB;
   const unsigned char* vmine = vblk + 32 * kg * ROWB;
-  unsigned char* dsg = dsl + rg * kBlockKeys * kTileRows * 2;
 
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -283,23 +280,16 @@ void bwd_kv_kernel(const BwdArgs a) {
     const int s = n & (kBufs - 1);
     const bool has = n < my_tiles;  // group 1 has no tile on the last step of an odd count
     // Wait for this group's tile of step n (and on the first step the K / V
-    // blocks): vector memory completes in issue order; in the steady state
-    // issued after this tile's loads are the next kBufs-2 tiles' loads and the
-    // dQ atomics of the last kBufs-1 steps.  The first and last steps wait for
-    // everything.
-    if (n >= kBufs - 1 && n + kBufs - 2 < my_tiles) {
-      if (kg < DT)
-        vm_wait<(kBufs - 2) * LPW + (kBufs - 1) * kDqAtomics>();
-      else
-        vm_wait<(kBufs - 2) * LPW>();
-    } else {
+    // blocks): vector memory completes in issue order, and in the steady
+    // state issued after this tile's loads are the next kBufs-2 tiles' loads.
+    if (n >= kBufs - 1 && n + kBufs - 2 < my_tiles)
+      vm_wait<(kBufs - 2) * LPW>();
+    else
       vm_wait<0>();
-    }
     // every wave is done with step n-1: its buffers (the ones step n+kBufs-1
-    // loads into) and the dS areas are free
+    // loads into) are free
     sync_lds();
     if (n + kBufs - 1 < my_tiles) issue_tile(tile_at(2 * (n + kBufs - 1) + rg), (n + kBufs - 1) & (kBufs - 1));
-    const int j = tile_at(2 * n + rg);
     const unsigned char* qt = tiles + 2 * (rg * kBufs + s) * TILE_B;
     const unsigned char* dot = qt + TILE_B;
 
@@ -350,37 +340,6 @@ void bwd_kv_kernel(const BwdArgs a) {
           dv[dt] = Mma<T>::run(bit_cast<V8>(doT), pb[s2], dv[dt]);
           dk[dt] = Mma<T>::run(bit_cast<V8>(qT), db[s2], dk[dt]);
         }
-      // dS of the wave's keys -> this group's LDS [key][row]: rows 8q + 4lh
-      // + [0, 4) are elements 4q .. 4q+3.
-      unsigned char* dst = dsg + (32 * kg + ln) * 64 + 8 * lh;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const i16x8 e = bit_cast<i16x8>(db[q >> 1]);
-        const i16x4 v4 = (q & 1) ? __builtin_shufflevector(e, e, 4, 5, 6, 7) : __builtin_shufflevector(e, e, 0, 1, 2, 3);
-        *reinterpret_cast<i16x4*>(dst + 16 * q) = v4;
-      }
-    }
-    sync_lds();
-    // dQ^T = K^T dS^T over the workgroup's 128 keys (M = d-tile kg, N = rows,
-    // 8 k-steps), added to the fp32 accumulator.
-    if (has && kg < DT) {
-      f32x16 acc;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < kBlockKeys / 16; ++ks) {
-        const i16x8 kT = tr_pair(kblk + 16 * ks * ROWB, kg);
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsg + ds_toff(0) + 16 * ks * 64));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(dsg + ds_toff(1) + 16 * ks * 64));
-        const i16x8 dsT = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc = Mma<T>::run(bit_cast<V8>(kT), bit_cast<V8>(dsT), acc);
-      }
-      // lane (row ln, lh) holds d = kg*32 + 8(i/4) + 4lh + i%4; the
-      // accumulator is d-major, so each instruction's 64 lanes cover two
-      // whole 128-byte lines (32 rows at two d).  Padding rows add 0.
-      float* dq = a.dq_acc + ((int64_t)bk * D + kg * 32 + 4 * lh) * TGP + j * kTileRows + ln;
-#pragma unroll
-      for (int i = 0; i < kDqAtomics; ++i) atomicAdd(dq + (int64_t)(8 * (i >> 2) + (i & 3)) * TGP, acc[i]);
     }
   }
 
@@ -424,6 +383,234 @@ void bwd_kv_kernel(const BwdArgs a) {
         *reinterpret_cast<T4*>(dkp + dt * 32 + 8 * q) = x;
         *reinterpret_cast<T4*>(dvp + dt * 32 + 8 * q) = y;
       }
+  }
+}
+
+// ------------------------------------------------------------- dQ kernel
+constexpr int kQWaves = 4;   // 32 rows each: 128-row chunks
+constexpr int kRing = 4;     // LDS ring stages of 32-key units
+constexpr int kMaxDqSplits = 16;
+
+template <int D> constexpr size_t dq_lds_bytes() {
+  // kRing x (K unit, V unit, mask words of the chunk's 4 row tiles x 32 keys) | dummy load targets
+  return (size_t)kRing * (2 * 32 * D * 2 + 4 * 32 * 4) + 64;
+}
+
+// Wait until at most k units (LPU loads each) of this wave are in flight.
+template <int LPU, int K> __device__ inline void wait_units(int k) {
+  if constexpr (K == 0) {
+    vm_wait<0>();
+  } else {
+    if (k >= K) {
+      vm_wait<K * LPU>();
+      return;
+    }
+    wait_units<LPU, K - 1>(k);
+  }
+}
+
+// Row-parallel dQ: a workgroup owns a 128-row chunk of one (b, kv head) (one
+// 32-row tile per wave, Q and dO fragments in registers) and one split of its
+// 32-key units (prefix units, then the tree units), streamed through a
+// 4-stage LDS ring.  Per unit, on v_mfma_f32_32x32x16:
+//   S^T = K Q^T and dP^T = V dO^T (a lane holds one row, so its LSE and Dv
+//   are scalars), P^T and dS^T on the VALU, then dQ^T += K^T dS^T with dS^T
+//   taken straight from the accumulator (k order permuted to the order it
+//   holds keys in; K^T from ds_read_b64_tr_b16 in the same order).
+// The workgroup's dQ^T adds to the fp32 accumulator once at the end
+// (atomics: several splits of one chunk add to the same rows).
+template <typename T, int D>
+__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void bwd_dq_main_kernel(const BwdArgs a) {
+  typedef typename Mma<T>::vec8 V8;
+  constexpr int ROWB = D * 2;
+  constexpr int KSTEPS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int CPR = D / 8;
+  constexpr int RPL = 64 / CPR;
+  constexpr int HALF = 32 * ROWB;          // K (or V) bytes of one unit
+  constexpr int VISB = 4 * 32 * 4;         // mask words of the chunk's 4 row tiles for the unit's 32 keys
+  constexpr int SB = 2 * HALF + VISB;      // ring stage
+  constexpr int LPH = HALF / 1024;         // 1 KB loads per half
+  constexpr int UPW = 2 * LPH / kQWaves;   // K + V loads per wave per unit
+  constexpr int LPU = UPW + 1;             // + the mask words (wave 0, tree units) or a dummy load
+  static_assert(UPW >= 1 && UPW * kQWaves == 2 * LPH, "load split");
+
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* ring = smem;
+  unsigned char* dummy = ring + kRing * SB;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, lh = lane >> 5;
+
+  // item order: chunk fastest (the chunks of one (b, kv head) read the same
+  // K / V units), XCD-aware as in the forward
+  const int item = (blockIdx.x & 7) * a.q_items_per_xcd + (blockIdx.x >> 3);
+  if (item >= a.q_items) return;
+  const int chunk = item % a.n_chunks;
+  int rest = item / a.n_chunks;
+  const int sp = rest % a.n_splits;
+  const int bk = rest / a.n_splits;
+  const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
+  const int G = a.group;
+  const int TG = a.q_len * G;
+  const int TGP = a.n_tiles * kTileRows;
+  const int P = a.prefix_len;
+  const float sl2 = a.scale_log2;
+  const int tile = chunk * kQWaves + wave;     // this wave's 32-row tile
+  const bool active = tile < a.n_tiles;
+  const int r = tile * kTileRows + ln;         // this lane's row
+  const int n_units = a.n_pu + a.n_tu;
+  const int u_lo = sp * a.units_per_split;
+  const int mine = max(0, min(a.units_per_split, n_units - u_lo));
+
+  const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  const uint32_t* visbase = a.vis + (int64_t)b * a.vis_tree_stride;
+
+  // Q^T and dO^T operands (B[d][row]: lane (row ln, lh) holds d = 16kk + 8lh
+  // + [0, 8)) and the row's statistics, in registers for the whole walk.
+  // Loaded before any ring load and consumed at once, so the compiler's wait
+  // for them covers nothing else.
+  i16x8 qf[KSTEPS], df[KSTEPS];
+  float lse2 = INFINITY, dvr = 0.f;
+  {
+    const int R = min(r, TG - 1);
+    const int t = R / G, g = R - t * G;
+    const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm + 8 * lh;
+    const T* dp = static_cast<const T*>(a.dout) + b * a.sdob + (int64_t)(kvh * G + g) * a.sdoh +
+                  (int64_t)t * a.sdom + 8 * lh;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      qf[kk] = *reinterpret_cast<const i16x8*>(qp + 16 * kk);
+      df[kk] = *reinterpret_cast<const i16x8*>(dp + 16 * kk);
+    }
+    if (active) {
+      const float2 st = a.rowstat[(int64_t)bk * TGP + r];  // padding rows: (+inf, 0)
+      lse2 = st.x;
+      dvr = st.y;
+    }
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(qf[kk]), "v"(df[kk]));
+    asm volatile("" : : "v"(lse2), "v"(dvr));
+  }
+
+  auto key0_of = [&](int u) { return u < a.n_pu ? 32 * u : P + 32 * (u - a.n_pu); };
+  // HBM -> LDS: this wave's share of unit u into stage st.
+  auto issue = [&](int st, int u) {
+    unsigned char* sb = ring + st * SB;
+    const int key0 = key0_of(u);
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {
+      const int v = wave * UPW + i;  // 0 .. 2*LPH-1: K loads, then V loads
+      const bool is_v = v >= LPH;
+      const int vl = is_v ? v - LPH : v;
+      const int row = vl * RPL + lane / CPR, pos = lane % CPR;
+      const int key = min(key0 + row, a.kv_len - 1);
+      const T* src = (is_v ? vbase + (int64_t)key * a.svn : kbase + (int64_t)key * a.skn) + ((pos ^ swz<D>(row)) << 3);
+      dma16(src, lds_addr(sb + (is_v ? HALF : 0) + vl * 1024));
+    }
+    if (wave == 0 && u >= a.n_pu) {
+      // words [tile][tree key]: 4 tiles x 32 keys x 4 B, 8 lanes per tile
+      if (lane < 32) {
+        const int jt = min(chunk * kQWaves + (lane >> 3), a.n_tiles - 1);
+        dma16(visbase + (int64_t)jt * a.n_tkeys + 32 * (u - a.n_pu) + 4 * (lane & 7), lds_addr(sb + 2 * HALF));
+      }
+    } else if (lane == 0) {
+      dma16(a.rowstat, lds_addr(dummy + 16 * wave));
+    }
+  };
+
+  // LDS offsets: row reads of K / V (lane (key ln, lh), chunk 2kk + lh) and
+  // transposed reads of K (rows 8jj + 4(x>>1) + (i>>2), d = dt*32 + 16(x&1) +
+  // 4(i&3)); the tiles use the same swizzle as the dK / dV kernel.
+  const int vx = lane >> 4, vi = lane & 15;
+  auto r_off = [&](int kk) { return ln * ROWB + (((2 * kk + lh) ^ swz<D>(ln)) << 4); };
+  auto t_off = [&](int dt, int jj) {
+    const int rr = 8 * jj + 4 * (vx >> 1) + (vi >> 2);
+    const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
+    return rr * ROWB + (((d >> 3) ^ swz<D>(rr)) << 4) + ((d & 7) << 1);
+  };
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+
+  for (int j = 0; j < kRing - 1 && j < mine; ++j) issue(j, u_lo + j);
+  for (int j = 0; j < mine; ++j) {
+    // unit j landed for every wave (later units in flight: up to kRing-2);
+    // every wave is done with unit j-1, whose stage unit j+kRing-1 reuses
+    wait_units<LPU, kRing - 2>(min(mine - 1 - j, kRing - 2));
+    sync_lds();
+    if (j + kRing - 1 < mine) issue((j + kRing - 1) % kRing, u_lo + j + kRing - 1);
+    if (!active) continue;
+    const unsigned char* sb = ring + (j % kRing) * SB;
+    const int u = u_lo + j;
+    const bool tree_u = u >= a.n_pu;
+    // S^T = K Q^T, dP^T = V dO^T: M = keys, N = rows; lane (row ln, lh)
+    // holds keys 8(i/4) + 4lh + i%4.
+    f32x16 sc, dp;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sc[i] = dp[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KSTEPS; ++kk) {
+      const int ro = r_off(kk);
+      const i16x8 kf = *reinterpret_cast<const i16x8*>(sb + ro);
+      const i16x8 vf = *reinterpret_cast<const i16x8*>(sb + HALF + ro);
+      sc = Mma<T>::run(bit_cast<V8>(kf), bit_cast<V8>(qf[kk]), sc);
+      dp = Mma<T>::run(bit_cast<V8>(vf), bit_cast<V8>(df[kk]), dp);
+    }
+    // visibility of the lane's 16 keys from its row: prefix keys below P;
+    // tree keys: bit ln of each key's word for this wave's tile
+    uint32_t vis16 = 0;
+    if (tree_u) {
+      const uint32_t* wv = reinterpret_cast<const uint32_t*>(sb + 2 * HALF) + wave * 32;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 w4 = *reinterpret_cast<const uint4*>(wv + 8 * q + 4 * lh);
+        vis16 |= ((w4.x >> ln) & 1u) << (4 * q + 0);
+        vis16 |= ((w4.y >> ln) & 1u) << (4 * q + 1);
+        vis16 |= ((w4.z >> ln) & 1u) << (4 * q + 2);
+        vis16 |= ((w4.w >> ln) & 1u) << (4 * q + 3);
+      }
+    } else {
+      const int key0 = 32 * u;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) vis16 |= (uint32_t)(key0 + 8 * (i >> 2) + 4 * lh + (i & 3) < P) << i;
+    }
+    V8 db[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float p = ((vis16 >> i) & 1u) ? __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], sl2, -lse2)) : 0.f;
+      db[i >> 3][i & 7] = (T)(p * (dp[i] - dvr));
+    }
+    // dQ^T += K^T dS^T: M = d, N = rows, k-step s2 covers keys 16s2 + 8(e/4)
+    // + 4lh + e%4 -- elements 8s2 .. 8s2+7 of the accumulator.
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (TSFA_LDS i16x4*)(sb + 16 * s2 * ROWB + t_off(dt, 0)));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (TSFA_LDS i16x4*)(sb + 16 * s2 * ROWB + t_off(dt, 1)));
+        const i16x8 kT = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[dt] = Mma<T>::run(bit_cast<V8>(kT), db[s2], acc[dt]);
+      }
+  }
+  // lane (row ln, lh) holds d = dt*32 + 8(i/4) + 4lh + i%4; the accumulator
+  // is d-major, so each instruction's 64 lanes cover two whole 128-byte lines.
+  if (active && mine > 0) {
+    float* dq = a.dq_acc + ((int64_t)bk * D + 4 * lh) * TGP + r;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        atomicAdd(dq + (int64_t)(dt * 32 + 8 * (i >> 2) + (i & 3)) * TGP, acc[dt][i]);
   }
 }
 
@@ -613,6 +800,9 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_kv_kernel<T, D>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kv_lds_bytes<D>()) != hipSuccess)
       return TSFA_ERR_LAUNCH;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&bwd_dq_main_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)dq_lds_bytes<D>()) != hipSuccess)
+      return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
   const int64_t prep_threads = (int64_t)pa.batch * pa.num_kv_heads * p.n_tiles * kTileRows * 16;
@@ -626,6 +816,11 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
   const unsigned grid = (unsigned)ba.items_per_xcd * 8;
   hipLaunchKernelGGL((bwd_kv_kernel<T, D>), dim3(grid), dim3(kWaves * 64), kv_lds_bytes<D>(), stream, ba);
   if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  if (ba.q_items > 0) {
+    const unsigned qgrid = (unsigned)ba.q_items_per_xcd * 8;
+    hipLaunchKernelGGL((bwd_dq_main_kernel<T, D>), dim3(qgrid), dim3(kQWaves * 64), dq_lds_bytes<D>(), stream, ba);
+    if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  }
   const int64_t dq_threads = (int64_t)da.batch * da.num_kv_heads * da.q_len * da.group * (D / 8);
   hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3((unsigned)((dq_threads + 255) / 256)), dim3(256), 0, stream, da);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
@@ -781,6 +976,27 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   ba.n_tb = p.n_tb;
   ba.n_tkeys = p.n_tkeys;
   ba.n_items = batch * num_kv_heads * (p.n_pb + p.n_tb);
+  // row-parallel dQ: 128-row chunks; the 32-key units (prefix, then the tree
+  // keys up to tree_key_limit) split so the grid covers about one workgroup
+  // per CU, at most kMaxDqSplits ways (each split adds its chunk's dQ once
+  // with atomics: splits x rows x D x 4 bytes of atomic traffic)
+  ba.n_pu = ceil_div(prefix_len, 32);
+  ba.n_tu = ceil_div(tree_key_limit, 32);
+  ba.n_chunks = ceil_div(p.n_tiles, kQWaves);
+  {
+    int cus = 256;
+    if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
+    const int n_units = ba.n_pu + ba.n_tu;
+    const int64_t base = (int64_t)batch * num_kv_heads * ba.n_chunks;
+    const int64_t want = std::min<int64_t>(kMaxDqSplits, std::max<int64_t>(1, (cus + base - 1) / base));
+    int splits = (int)std::min<int64_t>(want, std::max(1, n_units));
+    ba.units_per_split = std::max(1, ceil_div(n_units, splits));
+    ba.n_splits = std::max(1, ceil_div(n_units, ba.units_per_split));
+    const int64_t q_items = n_units > 0 ? base * ba.n_splits : 0;
+    if (q_items > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
+    ba.q_items = (int)q_items;
+    ba.q_items_per_xcd = (ba.q_items + 7) / 8;
+  }
   ba.group_magic = gqa_group_size > 1 ? (uint32_t)((((uint64_t)1) << 32) / (uint64_t)gqa_group_size + 1) : 0u;
   ba.items_per_xcd = (ba.n_items + 7) / 8;
 
