@@ -1805,7 +1805,7 @@ extern "C" int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o
 
 extern "C" int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr,
                               const int32_t* kv_indices, int64_t n_indices, int64_t page_table_stride, int n_pages,
-                              int page_size, void* o, const int32_t* row_ptr, const int32_t* col_idx,
+                              int page_size, void* o, float* lse, const int32_t* row_ptr, const int32_t* col_idx,
                               const int8_t* blk_type, const int32_t* mixed_mask_payload,
                               const int32_t* mixed_mask_offset, const int64_t* meta_seq_stride,
                               const int64_t* q_strides, const int64_t* cache_strides, const int64_t* o_strides,
@@ -1823,7 +1823,7 @@ extern "C" int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t
   kv.pt_stride = page_table_stride;
   kv.n_pages = n_pages;
   kv.page_size = page_size;
-  return fwd_impl(q, kv, o, nullptr, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset,
+  return fwd_impl(q, kv, o, lse, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset,
                   meta_seq_stride, q_strides, o_strides, sm_scale, batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
                   n_q_blocks, n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype, workspace,
                   workspace_bytes, stream_);

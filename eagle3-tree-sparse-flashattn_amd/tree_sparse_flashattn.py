@@ -458,7 +458,7 @@ def tree_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, met
 def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_indices: torch.Tensor, meta, *,
                                     kv_len: int, kv_indptr: Optional[torch.Tensor] = None,
                                     kv_layout: str = "NHD", sm_scale: Optional[float] = None,
-                                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                                    out: Optional[torch.Tensor] = None, return_lse: bool = False):
     """tree_sparse_attention_fwd with K/V read in place from a paged cache.
 
     kv_cache: [pages, 2, page_size, Hkv, D] (kv_layout "NHD": FlashInfer's
@@ -475,6 +475,8 @@ def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_
     O equals tree_sparse_attention_fwd over the gathered [B, Hkv, kv_len, D]
     K/V bit for bit.  Page ids outside the cache and list positions outside
     kv_indices are clamped in the kernel (wrong O, never an invalid read).
+    With ``return_lse`` the result is ``(O, lse)`` as in
+    tree_sparse_attention_fwd.
     """
     q = _row_contig(q)
     bsz, n_heads, q_len, head_dim = q.shape
@@ -537,11 +539,12 @@ def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_
     _lib.check("tree_sparse_attention_fwd_paged", lib.tsfa_fwd_check_args(*args))
     ws_bytes = lib.tsfa_fwd_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, head_dim)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    lse = torch.empty((bsz, n_heads, q_len), dtype=torch.float32, device=dev) if return_lse else None
     with torch.cuda.device(dev):
         st = lib.tsfa_fwd_paged(
             _lib.ptr(q), _lib.ptr(kv_cache), _lib.ptr(kv_indptr), _lib.ptr(kv_indices), kv_indices.numel(),
-            pt_stride, n_pages, page_size, _lib.ptr(out), *(_lib.ptr(t) for t in tensors),
+            pt_stride, n_pages, page_size, _lib.ptr(out), _lib.ptr(lse), *(_lib.ptr(t) for t in tensors),
             _lib.i64_array(meta_strides), _lib.i64_array(q.stride()), _lib.i64_array(cache_strides),
             _lib.i64_array(out.stride()), float(sm_scale), *args, _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
     _lib.check("tree_sparse_attention_fwd_paged", st)
-    return out
+    return (out, lse) if return_lse else out

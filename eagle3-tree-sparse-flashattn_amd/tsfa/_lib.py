@@ -64,7 +64,7 @@ _SIGNATURES = {
     "tsfa_bwd_workspace_bytes": (_c_size, [_c_int] * 10),
     "tsfa_bwd": (_c_int, [_c_vp] * 14 + [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
-    "tsfa_fwd_paged": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp,
+    "tsfa_fwd_paged": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp,
                                 _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]
                        + [ctypes.POINTER(_c_i64)] * 4 + [_c_float] + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
     "tsfa_fwd_plan": (_c_int, [_c_int] * 7 + [ctypes.POINTER(ctypes.c_int32)]),

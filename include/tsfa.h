@@ -183,11 +183,13 @@ int tsfa_bwd(const void* q, const void* k, const void* v, const void* o, const f
  *                to the pool and to kv_indices, so no table content reads
  *                outside them (a bad table gives wrong O, never a fault)
  * page_size      keys per page: a power of two, >= 16
+ * lse            NULL, or fp32 [B, Hq, q_len]: each row's log-sum-exp, as
+ *                tsfa_fwd_lse writes it
  * q_strides, o_strides  int64[4] each: b, h, n, d
  * Every sequence has kv_len keys (prefix_len + tree), as in tsfa_fwd. */
 int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr,
                    const int32_t* kv_indices, int64_t n_indices, int64_t page_table_stride,
-                   int n_pages, int page_size, void* o,
+                   int n_pages, int page_size, void* o, float* lse,
                    const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
                    const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
                    const int64_t* meta_seq_stride, const int64_t* q_strides,

@@ -110,7 +110,7 @@ def _paged_call(page_size=16, n_pages=8, n_indices=16, pt_stride=4, indptr=None,
     qs = (ctypes.c_int64 * 4)(4096 * 128 * 32, 64 * 128, 128, 1)
     cs = (ctypes.c_int64 * 5)(2 * page_size * 8 * 128, page_size * 8 * 128, 8 * 128, 128, 1)
     return _lib.load().tsfa_fwd_paged(fake, cache, indptr, fake, n_indices, pt_stride, n_pages, page_size, fake,
-                                      fake, fake, fake, fake, fake, ms, qs, cs, qs, ctypes.c_float(0.1),
+                                      None, fake, fake, fake, fake, fake, ms, qs, cs, qs, ctypes.c_float(0.1),
                                       *args.values(), fake, 1 << 30, None)
 
 

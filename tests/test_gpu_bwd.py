@@ -169,3 +169,49 @@ def test_lse_matches_plain_forward_output():
     o2, _ = tsf.tree_sparse_attention_fwd(q, k, v, meta, return_lse=True)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+def test_bwd_sync_free_batched_metadata():
+    # the bridge's capacity-layout record (no host sync), one tree per sequence
+    import eagle_tree_sparse_bridge as bridge
+    b, hq, hkv, t, p, d = 2, 8, 2, 40, 96, 128
+    rng = np.random.default_rng(21)
+    mask = torch.from_numpy(np.stack([_tree("eagle", t, rng) for _ in range(b)]))
+    q, k, v, do = _inputs(b, hq, hkv, t, p, d, BF, seed=21)
+    meta = bridge.build_tree_metadata(mask.cuda(), p, 16, 64)
+    qd, kd, vd, dod = (x.cuda() for x in (q, k, v, do))
+    o, lse = tsf.tree_sparse_attention_fwd(qd, kd, vd, meta, return_lse=True)
+    dq, dk, dv = tsf.tree_sparse_attention_bwd(qd, kd, vd, o, lse, dod, meta)
+    torch.cuda.synchronize()
+    rq, rk, rv, _ = attention_grads(q, k, v, mask, p, do)
+    _check("dq", dq, rq, BF)
+    _check("dk", dk, rk, BF)
+    _check("dv", dv, rv, BF)
+
+
+def test_bwd_graph_capture_replays():
+    b, hq, hkv, t, p, d = 1, 8, 2, 48, 200, 128
+    mask = torch.from_numpy(_tree("random", t, np.random.default_rng(22)))
+    q, k, v, do = (x.cuda() for x in _inputs(b, hq, hkv, t, p, d, BF, seed=22))
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, 16, 16)
+    o, lse = tsf.tree_sparse_attention_fwd(q, k, v, meta, return_lse=True)
+    eager = tsf.tree_sparse_attention_bwd(q, k, v, o, lse, do, meta)
+    dq, dk, dv = (torch.empty_like(x) for x in (q, k, v))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm the allocator and the LDS attributes outside capture
+        tsf.tree_sparse_attention_bwd(q, k, v, o, lse, do, meta, dq=dq, dk=dk, dv=dv)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        tsf.tree_sparse_attention_bwd(q, k, v, o, lse, do, meta, dq=dq, dk=dk, dv=dv)
+    for i in range(3):
+        for x in (dq, dk, dv):
+            x.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        # dK / dV have a fixed summation order; dQ sums fp32 atomics of the key splits
+        assert torch.equal(dk, eager[1]) and torch.equal(dv, eager[2]), f"replay {i}"
+        torch.testing.assert_close(dq, eager[0], rtol=1e-2, atol=1e-3)

@@ -160,3 +160,16 @@ def test_paged_graph_capture_replays():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
+
+
+def test_paged_lse_matches_contiguous():
+    b, hq, hkv, t, p, d = 2, 8, 2, 30, 77, 128
+    mask = torch.from_numpy(_tree("random", t, np.random.default_rng(12)))
+    q, k, v = (x.cuda() for x in _qkv(b, hq, hkv, t, p, d, BF, seed=12))
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, 16, 16)
+    cache, indptr, indices = configs.make_paged_kv(k, v, 32, seed=2)
+    o_c, lse_c = tsf.tree_sparse_attention_fwd(q, k, v, meta, return_lse=True)
+    o_p, lse_p = tsf.tree_sparse_attention_fwd_paged(q, cache, indices, meta, kv_len=p + t, kv_indptr=indptr,
+                                                     return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o_c, o_p) and torch.equal(lse_c, lse_p)
