@@ -202,7 +202,7 @@ def paged_timing(w, qd, ks, vs, meta, steps: int, page_size: int, contiguous_us:
             "vs_contiguous": round(contiguous_us / us, 4)}
 
 
-def backward_timing(w, mask, qd, ks, vs, meta, steps: int, fwd_flops: float):
+def backward_timing(w, mask, qd, ks, vs, meta, steps: int, fwd_flops: float, cpu_seconds: float = 0.0):
     """tree_sparse_attention_bwd (dQ, dK, dV from O, the row LSE and dO) over the
     same cycled K/V copies: graph of `steps` calls, HIP events on the replay
     stream.  Algorithmic figures: five products per visible (row, key) pair --
@@ -246,10 +246,28 @@ def backward_timing(w, mask, qd, ks, vs, meta, steps: int, fwd_flops: float):
     nbytes = 2 * w.kv_bytes() + 4 * qd.numel() * qd.element_size()
     tflops = flops / (us * 1e-6) / 1e12
     gbps = nbytes / (us * 1e-6) / 1e9
-    return {"us_per_call": round(us, 3), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
-            "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
-            "achieved_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "kernels": "prep + tree visibility + key-parallel dK/dV + row-parallel dQ + dQ convert (five launches)"}
+    res = {"us_per_call": round(us, 3), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
+           "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
+           "achieved_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "cpu_baseline": None,
+           "kernels": "prep and tree visibility (one launch) + key-parallel dK/dV + row-parallel dQ (+ dQ convert when the key range is split)"}
+    if cpu_seconds > 0:
+        # the fp32 gradient oracle (closed forms, oracle/attn_grad_oracle.py) on the host cores
+        from oracle.attn_grad_oracle import attention_grads
+
+        cores = len(os.sched_getaffinity(0))
+        torch.set_num_threads(cores)
+        qc, kc, vc, dc = qd.cpu(), ks[0].cpu(), vs[0].cpu(), do.cpu()
+        t0 = time.perf_counter()
+        attention_grads(qc, kc, vc, mask, w.prefix_len, dc, head_chunk=8)
+        t1 = time.perf_counter() - t0
+        n = max(1, min(100, int(cpu_seconds / max(t1, 1e-6))))
+        t0 = time.perf_counter()
+        for _ in range(n):
+            attention_grads(qc, kc, vc, mask, w.prefix_len, dc, head_chunk=8)
+        dt = (time.perf_counter() - t0) / n
+        res["cpu_baseline"] = {"us_per_call": round(dt * 1e6, 1), "cores": cores, "kind": "port",
+                               "sample": f"{n} full backward calls of the fp32 gradient oracle (torch CPU, {cores} threads)"}
+    return res
 
 
 def calibrate_copy(mib: int, reps: int):
@@ -410,7 +428,8 @@ def main():
     result["metadata"] = metadata_timing(w, mask.to(dev), mask)
     if not args.no_backward:
         _log("[bench] backward ...")
-        result["backward"] = backward_timing(w, mask, qd, ks, vs, meta, steps, flops)
+        result["backward"] = backward_timing(w, mask, qd, ks, vs, meta, steps, flops,
+                                             0.0 if args.no_cpu_baseline else min(5.0, args.cpu_seconds))
     if args.paged_page_size > 0:
         _log(f"[bench] paged cache, page_size {args.paged_page_size} ...")
         del regions

@@ -10,13 +10,15 @@
 // summed over the G query heads of each kv head.  P is recomputed from the
 // forward's per-row log-sum-exp (tsfa_fwd_lse).
 //
-// Kernels (one call = five launches, no host synchronisation):
-//   * bwd_prep_kernel: per query row (16 lanes): Dv = rowsum(dO * O) in fp32,
-//     the log2-domain LSE, and the row of the fp32 dQ accumulator cleared.
-//     Rows with no visible key (LSE = -inf) and the padding rows of the last
-//     32-row tile get LSE = +inf and Dv = 0, so their P and dS are exactly 0;
-//   * bwd_vis_kernel: per (32-row tile, tree key) a visibility word (bit m:
-//     row 32*tile + m sees the key), from the CSR metadata;
+// Kernels (one call = three or four launches, no host synchronisation):
+//   * bwd_prep_vis_kernel, two jobs in one launch:
+//     prep -- per query row (16 lanes): Dv = rowsum(dO * O) in fp32, the
+//     log2-domain LSE, and (when the dQ pass is split) the row of the fp32 dQ
+//     accumulator cleared.  Rows with no visible key (LSE = -inf) and the
+//     padding rows of the last 32-row tile get LSE = +inf and Dv = 0, so their
+//     P and dS are exactly 0;
+//     visibility -- per (32-row tile, tree key) a word (bit m: row 32*tile + m
+//     sees the key), from the CSR metadata;
 //   * bwd_kv_kernel (key-parallel, dK and dV): a workgroup owns 128 keys of
 //     one (batch, kv head) -- prefix keys and tree keys in separate blocks --
 //     as 4 key groups x 2 row groups of waves; each wave keeps dK^T and dV^T
@@ -34,9 +36,10 @@
 //     merge their sums through LDS at the end;
 //   * bwd_dq_main_kernel (row-parallel, dQ): a workgroup owns 128 rows and a
 //     split of the 32-key units; S^T, dP^T, dS^T recomputed per unit and dQ^T
-//     += K^T dS^T accumulated in registers, added once per workgroup to the
-//     fp32 accumulator (atomics only between the splits of one chunk);
-//   * bwd_dq_kernel: dQ = sm_scale * accumulator in the input dtype.
+//     += K^T dS^T accumulated in registers; an unsplit chunk writes dQ
+//     directly, split chunks add once per workgroup to the fp32 accumulator;
+//   * bwd_dq_kernel (split chunks only): dQ = sm_scale * accumulator in the
+//     input dtype.
 
 #include <math.h>
 
@@ -115,6 +118,10 @@ struct BwdArgs {
   int n_items, items_per_xcd;
   uint32_t group_magic;     // floor(2^32 / group) + 1 (group > 1): R / group = umulhi(R, magic) for R < 2^21
   // row-parallel dQ kernel
+  void* dq;                 // dq_direct: the kernel writes sm_scale * dQ here (one split per chunk)
+  int64_t sdqb, sdqh, sdqm;
+  float dq_scale;
+  int dq_direct;
   int n_pu, n_tu;           // prefix / tree units of 32 keys
   int n_chunks, n_splits, units_per_split, q_items, q_items_per_xcd;
 };
@@ -602,15 +609,34 @@ void bwd_dq_main_kernel(const BwdArgs a) {
         acc[dt] = Mma<T>::run(bit_cast<V8>(kT), db[s2], acc[dt]);
       }
   }
-  // lane (row ln, lh) holds d = dt*32 + 8(i/4) + 4lh + i%4; the accumulator
-  // is d-major, so each instruction's 64 lanes cover two whole 128-byte lines.
+  // lane (row ln, lh) holds d = dt*32 + 8(i/4) + 4lh + i%4.  One split per
+  // chunk: the workgroup owns its rows' dQ and writes it in the input dtype.
+  // Otherwise it adds to the d-major fp32 accumulator (each instruction's 64
+  // lanes cover two whole 128-byte lines).
   if (active && mine > 0) {
-    float* dq = a.dq_acc + ((int64_t)bk * D + 4 * lh) * TGP + r;
+    if (a.dq_direct) {
+      if (r < TG) {
+        const int t = r / G, g = r - t * G;
+        T* dst = static_cast<T*>(a.dq) + b * a.sdqb + (int64_t)(kvh * G + g) * a.sdqh + (int64_t)t * a.sdqm + 4 * lh;
+        typedef T T4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        atomicAdd(dq + (int64_t)(dt * 32 + 8 * (i >> 2) + (i & 3)) * TGP, acc[dt][i]);
+          for (int q = 0; q < 4; ++q) {
+            T4 x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = (T)(acc[dt][4 * q + e] * a.dq_scale);
+            *reinterpret_cast<T4*>(dst + dt * 32 + 8 * q) = x;
+          }
+      }
+    } else {
+      float* dq = a.dq_acc + ((int64_t)bk * D + 4 * lh) * TGP + r;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          atomicAdd(dq + (int64_t)(dt * 32 + 8 * (i >> 2) + (i & 3)) * TGP, acc[dt][i]);
+    }
   }
 }
 
@@ -623,13 +649,15 @@ struct PrepArgs {
   float* dq_acc;     // [B*Hkv][D][TGP]
   int64_t sob, soh, som, sdob, sdoh, sdom;
   int batch, num_heads, num_kv_heads, group, q_len, n_tiles;
+  int zero_dq;       // clear the accumulator (the dQ kernel adds into it)
 };
 
-// 16 lanes per row of the padded row space B*Hkv*TGP.
+// 16 lanes per row of the padded row space B*Hkv*TGP (workgroup `blk` of the
+// prep range).
 template <typename T, int D>
-__global__ __launch_bounds__(256) void bwd_prep_kernel(const PrepArgs a) {
+__device__ inline void bwd_prep(const PrepArgs& a, int blk) {
   constexpr int EPL = D / 16;  // elements per lane
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t gid = (int64_t)blk * 256 + threadIdx.x;
   const int64_t row = gid >> 4;
   const int part = (int)(gid & 15);
   const int TG = a.q_len * a.group;
@@ -653,7 +681,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const PrepArgs a) {
     for (int e = 0; e < EPL; ++e) acc += (float)ov[e] * (float)dv[e];
     lse = a.lse[((int64_t)b * a.num_heads + h) * a.q_len + t];
   }
-  if (live) {
+  if (live && a.zero_dq) {
     float* dq = a.dq_acc + ((int64_t)bk * D + part * EPL) * TGP + R;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) dq[(int64_t)e * TGP] = 0.f;
@@ -712,10 +740,8 @@ struct VisArgs {
 // tile's q-blocks (0 ZERO, -1 FULL, 1 + offset MIXED) expand into LDS, then
 // each thread decides one (key, row) bit and a ballot assembles the 32-row
 // words (lanes 0-31: one key, lanes 32-63: the next).
-__global__ __launch_bounds__(256) void bwd_vis_kernel(const VisArgs a) {
-  __shared__ int st[kMaxStateInts];
-  __shared__ int rps[72];
-  const int tile = blockIdx.x, tree = blockIdx.y, c0 = blockIdx.z * 64;
+__device__ inline void bwd_vis(const VisArgs& a, int tile, int tree, int zc, int* st, int* rps) {
+  const int c0 = zc * 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = a.group, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
   const int TG = a.q_len * G;
@@ -756,6 +782,23 @@ __global__ __launch_bounds__(256) void bwd_vis_kernel(const VisArgs a) {
     const uint64_t bal = __ballot(bit);
     if ((lane & 31) == 0 && c < a.n_tkeys) out[c] = (uint32_t)(bal >> (lane & 32));
   }
+}
+
+// Prep and visibility words in one launch: blocks [0, prep_blocks) run the
+// prep, the rest one (tile, tree, 64-key chunk) of the visibility words each.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void bwd_prep_vis_kernel(const PrepArgs pa, const VisArgs va, int prep_blocks,
+                                                           int vis_chunks) {
+  __shared__ int st[kMaxStateInts];
+  __shared__ int rps[72];
+  const int blk = blockIdx.x;
+  if (blk < prep_blocks) {
+    bwd_prep<T, D>(pa, blk);
+    return;
+  }
+  const int v = blk - prep_blocks;
+  const int zc = v % vis_chunks, rest = v / vis_chunks;
+  bwd_vis(va, rest % va.n_tiles, rest / va.n_tiles, zc, st, rps);
 }
 
 // ------------------------------------------------------------------- host
@@ -806,13 +849,13 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
   const int64_t prep_threads = (int64_t)pa.batch * pa.num_kv_heads * p.n_tiles * kTileRows * 16;
-  hipLaunchKernelGGL((bwd_prep_kernel<T, D>), dim3((unsigned)((prep_threads + 255) / 256)), dim3(256), 0, stream,
-                     pa);
+  const int64_t prep_blocks = (prep_threads + 255) / 256;
+  const int vis_chunks = p.n_tkeys / 64;
+  const int64_t vis_blocks = has_tree ? (int64_t)p.n_tiles * p.n_trees * vis_chunks : 0;
+  if (prep_blocks + vis_blocks > INT32_MAX) return TSFA_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((bwd_prep_vis_kernel<T, D>), dim3((unsigned)(prep_blocks + vis_blocks)), dim3(256), 0, stream,
+                     pa, va, (int)prep_blocks, std::max(1, vis_chunks));
   if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
-  if (has_tree) {
-    hipLaunchKernelGGL(bwd_vis_kernel, dim3(p.n_tiles, p.n_trees, p.n_tkeys / 64), dim3(256), 0, stream, va);
-    if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
-  }
   const unsigned grid = (unsigned)ba.items_per_xcd * 8;
   hipLaunchKernelGGL((bwd_kv_kernel<T, D>), dim3(grid), dim3(kWaves * 64), kv_lds_bytes<D>(), stream, ba);
   if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
@@ -821,6 +864,7 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
     hipLaunchKernelGGL((bwd_dq_main_kernel<T, D>), dim3(qgrid), dim3(kQWaves * 64), dq_lds_bytes<D>(), stream, ba);
     if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
   }
+  if (ba.dq_direct) return TSFA_OK;
   const int64_t dq_threads = (int64_t)da.batch * da.num_kv_heads * da.q_len * da.group * (D / 8);
   hipLaunchKernelGGL((bwd_dq_kernel<T, D>), dim3((unsigned)((dq_threads + 255) / 256)), dim3(256), 0, stream, da);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
@@ -977,9 +1021,10 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   ba.n_tkeys = p.n_tkeys;
   ba.n_items = batch * num_kv_heads * (p.n_pb + p.n_tb);
   // row-parallel dQ: 128-row chunks; the 32-key units (prefix, then the tree
-  // keys up to tree_key_limit) split so the grid covers about one workgroup
-  // per CU, at most kMaxDqSplits ways (each split adds its chunk's dQ once
-  // with atomics: splits x rows x D x 4 bytes of atomic traffic)
+  // keys up to tree_key_limit) split so the grid covers about two workgroups
+  // per CU (two fit, and their waves interleave), at most kMaxDqSplits ways
+  // (each split adds its chunk's dQ once with atomics: splits x rows x D x 4
+  // bytes of atomic traffic; an unsplit chunk writes dQ directly)
   ba.n_pu = ceil_div(prefix_len, 32);
   ba.n_tu = ceil_div(tree_key_limit, 32);
   ba.n_chunks = ceil_div(p.n_tiles, kQWaves);
@@ -988,7 +1033,7 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
     if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
     const int n_units = ba.n_pu + ba.n_tu;
     const int64_t base = (int64_t)batch * num_kv_heads * ba.n_chunks;
-    const int64_t want = std::min<int64_t>(kMaxDqSplits, std::max<int64_t>(1, (cus + base - 1) / base));
+    const int64_t want = std::min<int64_t>(kMaxDqSplits, std::max<int64_t>(1, (2 * cus + base - 1) / base));
     int splits = (int)std::min<int64_t>(want, std::max(1, n_units));
     ba.units_per_split = std::max(1, ceil_div(n_units, splits));
     ba.n_splits = std::max(1, ceil_div(n_units, ba.units_per_split));
@@ -997,6 +1042,13 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
     ba.q_items = (int)q_items;
     ba.q_items_per_xcd = (ba.q_items + 7) / 8;
   }
+  ba.dq = dq;
+  ba.sdqb = strides[20];
+  ba.sdqh = strides[21];
+  ba.sdqm = strides[22];
+  ba.dq_scale = sm_scale;
+  ba.dq_direct = (ba.n_splits == 1 && ba.q_items > 0) ? 1 : 0;
+  pa.zero_dq = ba.dq_direct ? 0 : 1;
   ba.group_magic = gqa_group_size > 1 ? (uint32_t)((((uint64_t)1) << 32) / (uint64_t)gqa_group_size + 1) : 0u;
   ba.items_per_xcd = (ba.n_items + 7) / 8;
 
