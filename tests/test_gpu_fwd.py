@@ -58,6 +58,21 @@ def test_workload_sampled_heads(name, heads):
     assert not torch.isnan(out).any()
 
 
+@pytest.mark.parametrize("block_n", [32, 128])
+def test_workload_70b_block_n_sweep(block_n):
+    # the 70B-layout workload is swept over BLOCK_N in {32, 64, 128}; 64 runs above
+    w = configs.WORKLOADS["llama3-70b-b4-p32768"]
+    heads = (3, 30, 57)
+    print(f"[fwd] {w.name} BLOCK_N {block_n} heads {heads}", flush=True)
+    q, k, v = configs.make_qkv(w)
+    mask = configs.make_tree_mask(w)
+    out = _run(q, k, v, mask, w.block_m, block_n)
+    torch.cuda.synchronize()
+    err = assert_close_to_oracle(out, oracle_out(q, k, v, mask, w.prefix_len, heads=heads), w.dtype, heads=heads)
+    print(f"[fwd] {w.name} BLOCK_N {block_n} max_abs_err {err:.3e}", flush=True)
+    assert not torch.isnan(out).any()
+
+
 CASES = [
     # b, hq, hkv, t, p, d, dtype, bm, bn, tree
     (1, 4, 4, 128, 32, 64, torch.bfloat16, 64, 64, "random"),     # the CPU-runnable shape, on MFMA
