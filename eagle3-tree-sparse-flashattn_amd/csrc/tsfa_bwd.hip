@@ -54,7 +54,7 @@ namespace bwd {
 constexpr int kWaves = 8;                 // 4 key groups x 2 row groups
 constexpr int kBlockKeys = 128;           // keys per workgroup (32 per key group)
 constexpr int kTileRows = 32;             // query rows per tile
-constexpr int kMaxStateInts = 8192;       // block-state table of one tile (bwd_vis_kernel)
+constexpr int kMaxStateInts = 8192;       // block-state table of one tile (visibility words)
 constexpr int kBufs = 2;                  // Q / dO tile buffers per row group: loads run one step ahead
 
 // 16-byte-chunk XOR swizzle of a row-major [rows][D] LDS tile (row period

@@ -144,8 +144,11 @@ int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o, float* ls
  *          elements, d stride 1, 16-byte aligned rows
  * Every other argument as in tsfa_fwd; workspace of
  * tsfa_bwd_workspace_bytes(..., n_trees) bytes, n_trees = batch when
- * meta_seq_stride is non-zero (one tree per sequence), else 1.  Four kernel
- * launches on `stream`, no host synchronisation. */
+ * meta_seq_stride is non-zero (one tree per sequence), else 1.  Three or
+ * four kernel launches on `stream`, no host synchronisation.  Supported: the
+ * shapes tsfa_fwd supports with q_len * gqa_group_size < 2^22; the tree's
+ * block-state table of one 32-row tile must fit 8192 entries (otherwise
+ * TSFA_ERR_UNSUPPORTED, as tsfa_bwd_workspace_bytes returning 0 signals). */
 size_t tsfa_bwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                 int prefix_len, int block_m, int n_tree_blocks, int head_dim,
                                 int n_trees);
