@@ -59,6 +59,20 @@ constexpr int kMaxTreeUnits = 1024;  // tree keys <= 32768
 constexpr int kMiscInts = 320;       // LDS scalars: visible-unit count, row_ptr window
 constexpr float kRescaleLog2 = 8.0f;
 
+struct CombineArgs {
+  void* o;
+  int64_t sob, soh, som;
+  float* lse;  // optional [B, Hq, q_len] natural-log log-sum-exp of each row's scaled scores
+  float scale_log2;
+  int batch, num_heads, num_kv_heads, group, q_len, n_slots;
+  const void* ws_o;
+  const float2* ws_ml;
+  // Workspace rows [xcd_row[x], xcd_row[x + 1]) are merged by the blocks of
+  // XCD x (block ids with x = id % 8), the XCD whose split workgroups wrote
+  // most of their partials.
+  int64_t xcd_row[9];
+};
+
 struct SplitArgs {
   const void* q;
   const void* k;
@@ -88,15 +102,6 @@ struct SplitArgs {
   int page_shift, n_pages;
 };
 
-struct CombineArgs {
-  void* o;
-  int64_t sob, soh, som;
-  float* lse;  // optional [B, Hq, q_len] natural-log log-sum-exp of each row's scaled scores
-  float scale_log2;
-  int batch, num_heads, num_kv_heads, group, q_len, n_slots;
-  const void* ws_o;
-  const float2* ws_ml;
-};
 
 // 16-byte-chunk XOR swizzles of the K and V LDS tiles (row = key in unit).
 // K: the 16 keys of one quarter-wave of an MFMA A-operand read land on 16
@@ -1334,25 +1339,18 @@ void wide_kernel(const SplitArgs a) {
   }
 }
 
-// Merge the n_slots partials of every row and write O.  Threads walk the
-// workspace rows in order (coalesced partial loads), kEpt outputs per thread
-// (16-byte loads and stores: measured 19.0 -> 12.8 us at B=16 against 8-byte
-// accesses, no change at B=1); up to kBatch slots are loaded together (one
-// memory round trip for the usual slot counts) and folded in branch-free (an
-// empty partial has weight 0).
+// Merge of the n_slots partials of workspace row R of (batch, kv head) bk
+// into O (and the row's LSE when asked): kEpt outputs per thread, part
+// selects them.  16-byte loads and stores (measured 19.0 -> 12.8 us at B=16
+// against 8-byte accesses, no change at B=1); up to kBatch slots are loaded
+// together (one memory round trip for the usual slot counts) and folded in
+// branch-free (an empty partial has weight 0).
 constexpr int kEpt = 8;
 constexpr int kBatch = 16;
 
 template <typename T, int D>
-__global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
-  constexpr int TPR = D / kEpt;
-  const int64_t gtid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int part) {
   const int64_t TG = (int64_t)a.q_len * a.group;
-  const int64_t row = gtid / TPR;  // over B*Hkv*TG
-  const int part = (int)(gtid % TPR);
-  if (row >= (int64_t)a.batch * a.num_kv_heads * TG) return;
-  const int64_t bk = row / TG;
-  const int R = (int)(row - bk * TG);
   const int t = R / a.group, g = R - t * a.group;
   const int kvh = (int)(bk % a.num_kv_heads), b = (int)(bk / a.num_kv_heads);
   const int h = kvh * a.group + g;
@@ -1411,6 +1409,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
   }
   T* dst = static_cast<T*>(a.o) + b * a.sob + (int64_t)h * a.soh + (int64_t)t * a.som + part * kEpt;
   *reinterpret_cast<TV*>(dst) = out;
+}
+
+// Merge the n_slots partials of every row and write O.  Threads walk the
+// workspace rows in order (coalesced partial loads).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
+  constexpr int TPR = D / kEpt;
+  constexpr int RPB = 256 / TPR;  // rows per block
+  const int x = blockIdx.x & 7;
+  const int64_t TG = (int64_t)a.q_len * a.group;
+  const int64_t row = a.xcd_row[x] + (int64_t)(blockIdx.x >> 3) * RPB + threadIdx.x / TPR;  // over B*Hkv*TG
+  if (row >= a.xcd_row[x + 1]) return;
+  const int64_t bk = row / TG;
+  merge_row<T, D>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR));
 }
 
 // ------------------------------------------------------------------- plan
@@ -1556,9 +1568,34 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;
-  const int64_t threads = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group * (D / kEpt);
-  const unsigned blocks = (unsigned)((threads + 255) / 256);
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, ca);
+  // Each XCD merges the rows of the chunks its split workgroups ran (item i
+  // runs on XCD i / items_per_xcd; a chunk's rows go to the XCD of its middle
+  // slot), so the partials are read from the L2 they were written to and the
+  // next call's partial stores find no copies in other XCDs' L2s.
+  CombineArgs c = ca;
+  constexpr int RPB = 256 / (D / kEpt);
+  const int64_t TG = (int64_t)ca.q_len * ca.group;
+  const int64_t groups = (int64_t)ca.batch * ca.num_kv_heads * p.n_chunks;
+  auto first_row = [&](int64_t g) { return (g / p.n_chunks) * TG + (g % p.n_chunks) * p.rows_per_chunk; };
+  auto mid_item = [&](int64_t g) {
+    return g % p.n_chunks + (int64_t)p.n_chunks * (p.n_slots / 2 + (int64_t)p.n_slots * (g / p.n_chunks));
+  };
+  int64_t most = 0, g = 0;
+  for (int x = 0; x < 8; ++x) {
+    c.xcd_row[x] = first_row(g);
+    // first group past XCD x (mid_item is increasing in g)
+    int64_t lo = g, hi = groups;
+    while (lo < hi) {
+      const int64_t m = (lo + hi) / 2;
+      if (mid_item(m) / p.items_per_xcd > x) hi = m; else lo = m + 1;
+    }
+    g = lo;
+    most = std::max(most, (first_row(g) - c.xcd_row[x] + RPB - 1) / RPB);
+  }
+  c.xcd_row[8] = (int64_t)ca.batch * ca.num_kv_heads * TG;
+  const unsigned blocks = (unsigned)(8 * most);
+  if (blocks == 0) return TSFA_OK;
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, c);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
