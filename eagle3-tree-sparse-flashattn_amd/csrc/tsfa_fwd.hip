@@ -1347,6 +1347,7 @@ void wide_kernel(const SplitArgs a) {
 // branch-free (an empty partial has weight 0).
 constexpr int kEpt = 8;
 constexpr int kBatch = 16;
+constexpr int kCombineThreads = 128;
 
 template <typename T, int D>
 __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int part) {
@@ -1414,9 +1415,9 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
 // Merge the n_slots partials of every row and write O.  Threads walk the
 // workspace rows in order (coalesced partial loads).
 template <typename T, int D>
-__global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineArgs a) {
   constexpr int TPR = D / kEpt;
-  constexpr int RPB = 256 / TPR;  // rows per block
+  constexpr int RPB = kCombineThreads / TPR;  // rows per block
   const int x = blockIdx.x & 7;
   const int64_t TG = (int64_t)a.q_len * a.group;
   const int64_t row = a.xcd_row[x] + (int64_t)(blockIdx.x >> 3) * RPB + threadIdx.x / TPR;  // over B*Hkv*TG
@@ -1573,7 +1574,7 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   // slot), so the partials are read from the L2 they were written to and the
   // next call's partial stores find no copies in other XCDs' L2s.
   CombineArgs c = ca;
-  constexpr int RPB = 256 / (D / kEpt);
+  constexpr int RPB = kCombineThreads / (D / kEpt);
   const int64_t TG = (int64_t)ca.q_len * ca.group;
   const int64_t groups = (int64_t)ca.batch * ca.num_kv_heads * p.n_chunks;
   auto first_row = [&](int64_t g) { return (g / p.n_chunks) * TG + (g % p.n_chunks) * p.rows_per_chunk; };
@@ -1595,7 +1596,7 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   c.xcd_row[8] = (int64_t)ca.batch * ca.num_kv_heads * TG;
   const unsigned blocks = (unsigned)(8 * most);
   if (blocks == 0) return TSFA_OK;
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, c);
+  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
