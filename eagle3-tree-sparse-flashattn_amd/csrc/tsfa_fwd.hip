@@ -100,6 +100,7 @@ struct SplitArgs {
   int pt_stride;              // kv_indptr null: sequence b's list starts at b * pt_stride
   int n_indices;              // entries of kv_indices (< 2^31)
   int page_shift, n_pages;
+  int kv_nt;  // K/V loads non-temporal (each unit read by at most two row chunks)
 };
 
 
@@ -115,7 +116,11 @@ template <int D> __device__ inline int swz_v(int key) { return D == 128 ? ((key 
 // not treat every later LDS read as aliasing the in-flight copy (it would
 // insert vmcnt(0) before them and serialise the prefetch); completion is
 // ordered explicitly by wait_units().  dma16_s takes a scalar base and a
-// 32-bit lane offset (no per-lane 64-bit address arithmetic).
+// 32-bit lane offset (no per-lane 64-bit address arithmetic); NT marks the
+// load non-temporal (streamed K/V that at most one other workgroup reads:
+// measured 19.8 -> 18.6 us per call on the Llama-3-8B decode shape, and 2 %
+// slower on the 70B shape, where 16 row chunks re-read each K/V line from
+// the L2).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; the clobber documents the write
 __device__ inline void dma16(const void* src, uint32_t lds_base) {
@@ -124,11 +129,18 @@ __device__ inline void dma16(const void* src, uint32_t lds_base) {
                : "v"(src), "s"(lds_base)
                : "memory", "m0");
 }
+template <bool NT = false>
 __device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(voff), "s"(sbase), "s"(lds_base)
-               : "memory", "m0");
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(lds_base)
+                 : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -189,7 +201,7 @@ __device__ inline float pair_sum(float x) {
 // path like the fast one (scalar base, 32-bit lane offsets: fewer live VGPRs
 // for the wide kernel); otherwise per-lane 64-bit addresses (the 8-wave
 // kernel measured faster with them).
-template <typename T, int D, bool IS_V, int NL, bool OFF32 = false>
+template <typename T, int D, bool IS_V, int NL, bool OFF32 = false, bool NT = false>
 __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst, int key0, int kv_len, int lane,
                                 int u_lo, const uint32_t* loff) {
   constexpr int CPR = D / 8;
@@ -201,7 +213,7 @@ __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst,
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int u = u_lo + i;
-      dma16_s(rowp, loff[u % NOFF], lds_dst + u * 1024);
+      dma16_s<NT>(rowp, loff[u % NOFF], lds_dst + u * 1024);
       rowp += step;
     }
   } else if (OFF32) {
@@ -269,7 +281,8 @@ __device__ inline int64_t clamp_page(const SplitArgs& a, int raw) { return (int6
 // masked).
 template <typename T, int D, bool IS_V, int NL>
 __device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_t pid0, int64_t pid1, int pg0,
-                                      uint32_t lds_dst, int key0, int lane, int u_lo, const uint32_t* loff) {
+                                      uint32_t lds_dst, int key0, int lane, int u_lo, const uint32_t* loff,
+                                      bool nt) {
   constexpr int CPR = D / 8;
   constexpr int RPL = 64 / CPR;
   constexpr int NOFF = IS_V ? 1 : (D == 128 ? 4 : 2);
@@ -283,7 +296,10 @@ __device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int u = u_lo + i;
-      dma16_s(rowp, loff[u % NOFF], lds_dst + u * 1024);
+      if (nt)
+        dma16_s<true>(rowp, loff[u % NOFF], lds_dst + u * 1024);
+      else
+        dma16_s<false>(rowp, loff[u % NOFF], lds_dst + u * 1024);
       rowp += step;
     }
     return;
@@ -409,6 +425,7 @@ void split_kernel(const SplitArgs a) {
 
   // HBM -> LDS: this wave's share of one unit (keys key0 .. key0+31) into
   // stage st of its stream's ring.
+  const bool kv_nt = __builtin_amdgcn_readfirstlane(a.kv_nt) != 0;
   auto issue = [&](int st, int key0) {
     const uint32_t sb = sring_lds + st * SB;
     if (PAGED) {
@@ -421,9 +438,14 @@ void split_kernel(const SplitArgs a) {
       }
       const int64_t pid0 = clamp_page(a, raw0), pid1 = clamp_page(a, raw1);
       if (dma_v)
-        dma_half_paged<T, D, true, LPU>(vbase, a, pid0, pid1, pg0, sb + HALF, key0, lane, dma_u0, loff);
+        dma_half_paged<T, D, true, LPU>(vbase, a, pid0, pid1, pg0, sb + HALF, key0, lane, dma_u0, loff, kv_nt);
       else
-        dma_half_paged<T, D, false, LPU>(kbase, a, pid0, pid1, pg0, sb, key0, lane, dma_u0, loff);
+        dma_half_paged<T, D, false, LPU>(kbase, a, pid0, pid1, pg0, sb, key0, lane, dma_u0, loff, kv_nt);
+    } else if (kv_nt) {
+      if (dma_v)
+        dma_half<T, D, true, LPU, false, true>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
+      else
+        dma_half<T, D, false, LPU, false, true>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
     } else if (dma_v) {
       dma_half<T, D, true, LPU>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
     } else {
@@ -1785,6 +1807,10 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   sa.vt_max = p.vt_max;
   sa.ws_o = workspace;
   sa.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
+  // Non-temporal K/V loads when little L2 reuse is at stake (TSFA_KV_NT=0/1
+  // forces them off/on).
+  const int kv_nt = env_int("TSFA_KV_NT", -1);
+  sa.kv_nt = kv_nt >= 0 ? (kv_nt != 0) : (p.n_chunks <= 2);
 
   CombineArgs ca;
   ca.o = o;

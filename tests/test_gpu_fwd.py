@@ -110,10 +110,12 @@ def test_cases(case):
     assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
 
 
-# The planner's other kernels, forced through its environment switches: the
-# wide kernel (one wave per SIMD, 64 rows per wave, 256-row chunks) and the
-# 8-wave kernel with one key stream.
-KERNELS = {"wide": {"TSFA_WIDE": "2"}, "one-stream": {"TSFA_WIDE": "0", "TSFA_STREAMS": "1"}}
+# The planner's other kernels and load flavours, forced through its
+# environment switches: the wide kernel (one wave per SIMD, 64 rows per wave,
+# 256-row chunks), the 8-wave kernel with one key stream, and the K/V loads
+# with and without the non-temporal hint (chosen by the row-chunk count).
+KERNELS = {"wide": {"TSFA_WIDE": "2"}, "one-stream": {"TSFA_WIDE": "0", "TSFA_STREAMS": "1"},
+           "kv-nt": {"TSFA_KV_NT": "1"}, "kv-temporal": {"TSFA_KV_NT": "0"}}
 
 
 @pytest.mark.parametrize("kernel", sorted(KERNELS))
