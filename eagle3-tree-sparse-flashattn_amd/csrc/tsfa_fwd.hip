@@ -819,13 +819,23 @@ void split_kernel(const SplitArgs a) {
     const float inv = L > 0.f ? 1.f / L : 0.f;  // empty partial: O = 0, weight 0 in the combine
     const int r = rg * 32 + ln;
     typedef T T4 __attribute__((ext_vector_type(4)));
+    // stream 1's O^T, read before any staging write (the staging rows share
+    // the ring, so interleaved reads and writes would serialise on LDS)
+    f32x4 xo[DT][4];
+    if (S == 2) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          xo[dt][q] = *reinterpret_cast<const f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16);
+    }
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         T4 v4;
         if (S == 2) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16);
+          const f32x4 x = xo[dt][q];
 #pragma unroll
           for (int i = 0; i < 4; ++i) v4[i] = (T)((w0 * o[dt][4 * q + i] + w1 * x[i]) * inv);
         } else {
@@ -837,12 +847,22 @@ void split_kernel(const SplitArgs a) {
     if (lh == 0 && r < rows_chunk) a.ws_ml[part_row0 + r] = make_float2(M, L);
   }
   sync_lds();
+  // Whole rows out, 1 KB per wave instruction; the LDS reads go first so they
+  // overlap instead of each waiting on its own round trip.
   constexpr int CPR = D / 8;
+  constexpr int NIT = ROWS * CPR / (kWaves * 64);
+  static_assert(NIT * kWaves * 64 == ROWS * CPR, "staging loop");
   T* dst = static_cast<T*>(a.ws_o) + part_row0 * D;
-  for (int idx = tid; idx < rows_chunk * CPR; idx += kWaves * 64) {
-    const int r = idx / CPR, c = idx % CPR;
-    *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) =
-        *reinterpret_cast<const i16x8*>(stg + r * ROWB + ((c ^ swz_k<D>(r)) << 4));
+  i16x8 rowv[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int idx = tid + it * kWaves * 64, r = idx / CPR, c = idx % CPR;
+    rowv[it] = *reinterpret_cast<const i16x8*>(stg + r * ROWB + ((c ^ swz_k<D>(r)) << 4));
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int idx = tid + it * kWaves * 64, r = idx / CPR, c = idx % CPR;
+    if (r < rows_chunk) *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) = rowv[it];
   }
 }
 
