@@ -145,7 +145,12 @@ int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o, float* ls
  * Every other argument as in tsfa_fwd; workspace of
  * tsfa_bwd_workspace_bytes(..., n_trees) bytes, n_trees = batch when
  * meta_seq_stride is non-zero (one tree per sequence), else 1.  Three or
- * four kernel launches on `stream`, no host synchronisation.  Supported: the
+ * four kernel launches, no host synchronisation: the dQ kernel runs on a
+ * library-owned side stream forked from `stream` after the first launch and
+ * joined back before the call returns its last launch (one side stream and
+ * two events per device and caller stream, kept for the process; inside a
+ * graph capture the fork and join are captured too; TSFA_BWD_CONCURRENT=0
+ * keeps every launch on `stream`).  Supported: the
  * shapes tsfa_fwd supports with q_len * gqa_group_size < 2^22; the tree's
  * block-state table of one 32-row tile must fit 8192 entries (otherwise
  * TSFA_ERR_UNSUPPORTED, as tsfa_bwd_workspace_bytes returning 0 signals). */
