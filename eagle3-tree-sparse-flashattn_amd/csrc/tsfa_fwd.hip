@@ -101,6 +101,7 @@ struct SplitArgs {
   int n_indices;              // entries of kv_indices (< 2^31)
   int page_shift, n_pages;
   int kv_nt;  // K/V loads non-temporal (each unit read by at most two row chunks)
+  int item_order;  // within an XCD: 0 natural, 1 prefix runs first, 2 tree items first
 };
 
 
@@ -332,6 +333,29 @@ template <int D> constexpr size_t lds_bytes_for() {
   return (size_t)kRingBytes + kMaskWords * 4 + (kMaxTreeUnits + kMiscInts) * 4;
 }
 
+// Work item of this workgroup.  XCD x (block id % 8) owns the items
+// [x*ipx, (x+1)*ipx) of the natural order item = chunk + n_chunks * (slot +
+// n_slots * bk) (so the row chunks sharing K/V units share the XCD's L2).
+// With item_order 1 the workgroups of an XCD take its prefix runs first and
+// its tree items last (2: the reverse): with few rounds, like items then
+// run side by side and the rounds pack (the 16-sequence decode shape, 3
+// rounds: 86.6 -> 78.6 us per call); with many rounds the natural order,
+// which spreads the tree items over the rounds, measured ~1 % faster.
+// Returns -1 for the padding blocks of the last XCD.
+__device__ inline int work_item(const SplitArgs& a) {
+  const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int lo = x * a.items_per_xcd, hi = min(lo + a.items_per_xcd, a.n_items);
+  if (lo + j >= hi) return -1;
+  if (a.n_slots < 2 || a.item_order == 0) return lo + j;
+  const int P = a.n_chunks * a.n_slots, Nt = a.n_chunks, Np = P - Nt;
+  auto before = [&](int i) { return (i / P) * Np + min(i % P, Np); };  // prefix items before item i
+  auto kth_prefix = [&](int k) { return (k / Np) * P + k % Np; };
+  auto kth_tree = [&](int k) { return (k / Nt) * P + Np + k % Nt; };
+  const int plo = before(lo), np = before(hi) - plo, nt = hi - lo - np;
+  if (a.item_order == 2) return j < nt ? kth_tree(lo - plo + j) : kth_prefix(plo + j - nt);
+  return j < np ? kth_prefix(plo + j) : kth_tree(lo - plo + j - np);
+}
+
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.
 template <typename T, int D, int S, bool PAGED>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -369,11 +393,8 @@ void split_kernel(const SplitArgs a) {
   const int rg = wave % RG, ks = wave / RG;  // with S = 2, SIMD rg%4 holds one wave of each stream
   const int ln = lane & 31, lh = lane >> 5;
 
-  // XCD-aware item order: consecutive block ids go to different XCDs, so each
-  // XCD gets a contiguous range of items; items are ordered chunk-fastest, so
-  // the chunks that read the same K/V units share an XCD's L2.
-  const int item = (blockIdx.x & 7) * a.items_per_xcd + (blockIdx.x >> 3);
-  if (item >= a.n_items) return;
+  const int item = work_item(a);
+  if (item < 0) return;
   const int chunk = item % a.n_chunks;
   int rest = item / a.n_chunks;
   const int slot = rest % a.n_slots;
@@ -916,8 +937,8 @@ void wide_kernel(const SplitArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, lh = lane >> 5;
 
-  const int item = (blockIdx.x & 7) * a.items_per_xcd + (blockIdx.x >> 3);
-  if (item >= a.n_items) return;
+  const int item = work_item(a);
+  if (item < 0) return;
   const int chunk = item % a.n_chunks;
   int rest = item / a.n_chunks;
   const int slot = rest % a.n_slots;
@@ -1831,6 +1852,12 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   // forces them off/on).
   const int kv_nt = env_int("TSFA_KV_NT", -1);
   sa.kv_nt = kv_nt >= 0 ? (kv_nt != 0) : (p.n_chunks <= 2);
+  // Prefix runs first when the grid has at most 4 rounds (TSFA_ITEM_ORDER=0/1/2
+  // forces natural / prefix first / tree first).
+  int cus = 256;
+  if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
+  const int order = env_int("TSFA_ITEM_ORDER", -1);
+  sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
 
   CombineArgs ca;
   ca.o = o;

@@ -112,10 +112,12 @@ def test_cases(case):
 
 # The planner's other kernels and load flavours, forced through its
 # environment switches: the wide kernel (one wave per SIMD, 64 rows per wave,
-# 256-row chunks), the 8-wave kernel with one key stream, and the K/V loads
-# with and without the non-temporal hint (chosen by the row-chunk count).
+# 256-row chunks), the 8-wave kernel with one key stream, the K/V loads
+# with and without the non-temporal hint (chosen by the row-chunk count), and
+# the three dispatch orders of the work items.
 KERNELS = {"wide": {"TSFA_WIDE": "2"}, "one-stream": {"TSFA_WIDE": "0", "TSFA_STREAMS": "1"},
-           "kv-nt": {"TSFA_KV_NT": "1"}, "kv-temporal": {"TSFA_KV_NT": "0"}}
+           "kv-nt": {"TSFA_KV_NT": "1"}, "kv-temporal": {"TSFA_KV_NT": "0"},
+           "items-natural": {"TSFA_ITEM_ORDER": "0"}, "items-tree-first": {"TSFA_ITEM_ORDER": "2"}}
 
 
 @pytest.mark.parametrize("kernel", sorted(KERNELS))
