@@ -102,6 +102,7 @@ struct SplitArgs {
   int page_shift, n_pages;
   int kv_nt;  // K/V loads non-temporal (each unit read by at most two row chunks)
   int item_order;  // within an XCD: 0 natural, 1 prefix runs first, 2 tree items first
+  int fold_tree;   // no tree items: the last prefix split of each chunk also runs the tree units
 };
 
 
@@ -400,7 +401,10 @@ void split_kernel(const SplitArgs a) {
   const int slot = rest % a.n_slots;
   const int bk = rest / a.n_slots;
   const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
-  const bool is_tree = slot == a.n_slots - 1;
+  // roles: a prefix run (slots below n_slots - 1), the tree units (the last
+  // slot), or with fold_tree both in the last slot
+  const bool is_tree = !a.fold_tree && slot == a.n_slots - 1;
+  const bool do_tree = slot == a.n_slots - 1;
 
   const int G = a.group;
   const int TG = a.q_len * G;
@@ -718,8 +722,12 @@ void split_kernel(const SplitArgs a) {
     run_units(
         n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; });
-  } else {
-    load_q();
+  }
+  if (do_tree) {
+    // after a prefix run: its ring reads and loads done (the block states
+    // reuse the ring), Q already in registers
+    if (is_tree) load_q();
+    else sync_all();
     const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
     const int tok_hi = (row0 + rows_chunk - 1) / G;  // tokens tok_lo .. tok_hi
     const int ntok = tok_hi - tok_lo + 1;
@@ -1492,7 +1500,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
 // ------------------------------------------------------------------- plan
 struct Plan {
   int wide, streams, rows_per_chunk;
-  int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages;
+  int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages, fold_tree;
   int vt_max, tree_key_limit;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
 };
@@ -1565,7 +1573,21 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   }
   p->units_per_split = ups;
   p->n_splits = ups > 0 ? ceil_div(p->n_pu, ups) : 0;
-  p->n_slots = p->n_splits + 1;
+  // A separate tree item per chunk costs a round when it does not fit beside
+  // the prefix runs; then, if the tree is short next to a run (at most a
+  // quarter of its units, or 2), the last run of each chunk takes the tree
+  // units too (the 16-sequence decode shape: 3 rounds -> 2).  TSFA_FOLD_TREE
+  // =0/1 forces it off/on (on only where there is a prefix run).
+  p->fold_tree = 0;
+  if (!p->wide && p->n_splits >= 1) {
+    const int64_t tree_units = ceil_div(std::max(0, kv_len - prefix_len), kUnitKeys);
+    const int64_t rounds_sep = (groups * (p->n_splits + 1) + cus - 1) / cus;
+    const int64_t rounds_fold = (groups * p->n_splits + cus - 1) / cus;
+    const int force = env_int("TSFA_FOLD_TREE", -1);
+    p->fold_tree = force >= 0 ? (force != 0)
+                              : (rounds_fold < rounds_sep && tree_units <= std::max(2, ups / 4) ? 1 : 0);
+  }
+  p->n_slots = p->n_splits + (p->fold_tree ? 0 : 1);
   const int64_t items = groups * p->n_slots;
   if (items > (int64_t)INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
   p->n_items = (int)items;
@@ -1858,6 +1880,8 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
   const int order = env_int("TSFA_ITEM_ORDER", -1);
   sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
+  sa.fold_tree = p.fold_tree;
+  if (p.fold_tree) sa.item_order = 0;  // no tree items to order
 
   CombineArgs ca;
   ca.o = o;

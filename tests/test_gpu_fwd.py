@@ -113,11 +113,13 @@ def test_cases(case):
 # The planner's other kernels and load flavours, forced through its
 # environment switches: the wide kernel (one wave per SIMD, 64 rows per wave,
 # 256-row chunks), the 8-wave kernel with one key stream, the K/V loads
-# with and without the non-temporal hint (chosen by the row-chunk count), and
-# the three dispatch orders of the work items.
+# with and without the non-temporal hint (chosen by the row-chunk count), the
+# three dispatch orders of the work items, and the tree units run by their own
+# workgroup or by the last prefix run of each chunk.
 KERNELS = {"wide": {"TSFA_WIDE": "2"}, "one-stream": {"TSFA_WIDE": "0", "TSFA_STREAMS": "1"},
            "kv-nt": {"TSFA_KV_NT": "1"}, "kv-temporal": {"TSFA_KV_NT": "0"},
-           "items-natural": {"TSFA_ITEM_ORDER": "0"}, "items-tree-first": {"TSFA_ITEM_ORDER": "2"}}
+           "items-natural": {"TSFA_ITEM_ORDER": "0"}, "items-tree-first": {"TSFA_ITEM_ORDER": "2"},
+           "tree-folded": {"TSFA_FOLD_TREE": "1"}, "tree-separate": {"TSFA_FOLD_TREE": "0"}}
 
 
 @pytest.mark.parametrize("kernel", sorted(KERNELS))
@@ -148,8 +150,11 @@ def test_workload_other_kernels(kernel, monkeypatch):
     assert_close_to_oracle(out, oracle_out(q, k, v, mask, w.prefix_len), w.dtype)
 
 
+@pytest.mark.parametrize("fold", [None, "1"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_per_sequence_trees(dtype):
+def test_per_sequence_trees(dtype, fold, monkeypatch):
+    if fold is not None:  # the tree units run by the last prefix run of each chunk
+        monkeypatch.setenv("TSFA_FOLD_TREE", fold)
     b, hq, hkv, t, p, d = 3, 8, 2, 45, 70, 128
     rng = np.random.default_rng(3)
     masks = torch.from_numpy(np.stack([_tree("random", t, rng) for _ in range(b)]))
