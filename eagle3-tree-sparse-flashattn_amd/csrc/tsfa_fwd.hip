@@ -1881,7 +1881,9 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   const int order = env_int("TSFA_ITEM_ORDER", -1);
   sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
   sa.fold_tree = p.fold_tree;
-  if (p.fold_tree) sa.item_order = 0;  // no tree items to order
+  // folded: the last run of each chunk carries the tree units, the longest
+  // items, so those go first (longest first)
+  if (p.fold_tree && order < 0) sa.item_order = sa.item_order ? 2 : 0;
 
   CombineArgs ca;
   ca.o = o;
