@@ -1413,14 +1413,16 @@ void wide_kernel(const SplitArgs a) {
 // Merge of the n_slots partials of workspace row R of (batch, kv head) bk
 // into O (and the row's LSE when asked): kEpt outputs per thread, part
 // selects them.  16-byte loads and stores (measured 19.0 -> 12.8 us at B=16
-// against 8-byte accesses, no change at B=1); up to kBatch slots are loaded
+// against 8-byte accesses, no change at B=1); up to NB slots are loaded
 // together (one memory round trip for the usual slot counts) and folded in
-// branch-free (an empty partial has weight 0).
+// branch-free (an empty partial has weight 0).  NB is the smallest of 2, 4,
+// 8, 16 that covers n_slots (a batch past n_slots repeats the last slot's
+// loads: 16-slot batches on the 2-slot plan of the 16-sequence decode shape
+// cost 17.0 us per combine against 7.0).
 constexpr int kEpt = 8;
-constexpr int kBatch = 16;
 constexpr int kCombineThreads = 128;
 
-template <typename T, int D>
+template <typename T, int D, int NB>
 __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int part) {
   const int64_t TG = (int64_t)a.q_len * a.group;
   const int t = R / a.group, g = R - t * a.group;
@@ -1439,19 +1441,19 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
   float acc[kEpt];
 #pragma unroll
   for (int e = 0; e < kEpt; ++e) acc[e] = 0.f;
-  for (int s0 = 0; s0 < a.n_slots; s0 += kBatch) {
-    const int nb = min(kBatch, a.n_slots - s0);
-    float2 v[kBatch];
-    TV x[kBatch];
+  for (int s0 = 0; s0 < a.n_slots; s0 += NB) {
+    const int nb = min(NB, a.n_slots - s0);
+    float2 v[NB];
+    TV x[NB];
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int s = s0 + min(i, nb - 1);  // duplicates of the last slot get weight 0 below
       v[i] = ml[s * TG];
       x[i] = *reinterpret_cast<const TV*>(src + s * slot_stride);
     }
     float bm = mx;
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) bm = (i < nb) ? fmaxf(bm, v[i].x) : bm;
+    for (int i = 0; i < NB; ++i) bm = (i < nb) ? fmaxf(bm, v[i].x) : bm;
     if (bm != -INFINITY && bm != mx) {  // re-base the running sums on the new max
       const float alpha = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mx - bm) * a.scale_log2);
       l *= alpha;
@@ -1460,7 +1462,7 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
       mx = bm;
     }
 #pragma unroll
-    for (int i = 0; i < kBatch; ++i) {
+    for (int i = 0; i < NB; ++i) {
       // weight of partial s: l_s * 2^((m_s - M) * scale); 0 for an empty partial
       const float w = (i >= nb || v[i].x == -INFINITY) ? 0.f
                                                       : v[i].y * __builtin_amdgcn_exp2f((v[i].x - mx) * a.scale_log2);
@@ -1485,7 +1487,7 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
 
 // Merge the n_slots partials of every row and write O.  Threads walk the
 // workspace rows in order (coalesced partial loads).
-template <typename T, int D>
+template <typename T, int D, int NB>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineArgs a) {
   constexpr int TPR = D / kEpt;
   constexpr int RPB = kCombineThreads / TPR;  // rows per block
@@ -1494,7 +1496,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
   const int64_t row = a.xcd_row[x] + (int64_t)(blockIdx.x >> 3) * RPB + threadIdx.x / TPR;  // over B*Hkv*TG
   if (row >= a.xcd_row[x + 1]) return;
   const int64_t bk = row / TG;
-  merge_row<T, D>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR));
+  merge_row<T, D, NB>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR));
 }
 
 // ------------------------------------------------------------------- plan
@@ -1681,7 +1683,15 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   c.xcd_row[8] = (int64_t)ca.batch * ca.num_kv_heads * TG;
   const unsigned blocks = (unsigned)(8 * most);
   if (blocks == 0) return TSFA_OK;
-  hipLaunchKernelGGL((combine_kernel<T, D>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
+  const int ns = ca.n_slots;
+  if (ns <= 2)
+    hipLaunchKernelGGL((combine_kernel<T, D, 2>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
+  else if (ns <= 4)
+    hipLaunchKernelGGL((combine_kernel<T, D, 4>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
+  else if (ns <= 8)
+    hipLaunchKernelGGL((combine_kernel<T, D, 8>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
+  else
+    hipLaunchKernelGGL((combine_kernel<T, D, 16>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
