@@ -14,7 +14,12 @@
 //
 // Two launches per call: `classify` (one workgroup per block and sequence)
 // packs words and counts bits; `compact` (one workgroup per sequence) scans
-// the block classes and scatters the CSR arrays and MIXED payload.
+// the block classes and scatters the CSR arrays and MIXED payload.  A tree
+// whose packed words fit in LDS (at most kSmallBlocks blocks and
+// kSmallWords words: every EAGLE draft tree) takes one launch instead:
+// `build_small` packs, classifies and compacts a sequence in one workgroup.
+
+#include <stdlib.h>
 
 #include "tsfa_internal.h"
 
@@ -31,29 +36,47 @@ struct MetaGeom {
   int64_t cap;                                   // nqb * ntb
 };
 
+constexpr int kSmallBlocks = 256;
+constexpr int kSmallWords = 8192;  // 32 KB of packed words in LDS
+
+// Bits [32*wi, 32*wi + 32) of block (qb, tb) of the sequence whose mask
+// starts at m0, zero-padded past the block's clipped h x w extent (:44-64).
+__device__ inline uint32_t block_word(const uint8_t* m0, int64_t row_stride, const MetaGeom& g, int qb, int tb,
+                                      int wi) {
+  const int q0 = qb * g.block_m, k0 = tb * g.block_n;
+  const int h = min(g.block_m, g.q_len - q0);
+  const int w = min(g.block_n, g.q_len - k0);
+  const uint8_t* m = m0 + (int64_t)q0 * row_stride + k0;
+  const int64_t n_flat = (int64_t)g.block_m * g.block_n;
+  int64_t flat = (int64_t)wi * 32;
+  int r = (int)(flat / g.block_n);
+  int c = (int)(flat - (int64_t)r * g.block_n);
+  uint32_t word = 0;
+  for (int i = 0; i < 32 && flat + i < n_flat; ++i) {
+    if (r < h && c < w && m[(int64_t)r * row_stride + c] != 0) word |= 1u << i;
+    if (++c == g.block_n) { c = 0; ++r; }
+  }
+  return word;
+}
+
+// ZERO / FULL / MIXED from the set-bit count of a block (:113-124).
+__device__ inline int8_t block_class(const MetaGeom& g, int qb, int tb, int ones) {
+  const int h = min(g.block_m, g.q_len - qb * g.block_m);
+  const int w = min(g.block_n, g.q_len - tb * g.block_n);
+  return ones == 0 ? kZero : (ones == h * w ? kFull : kMixed);
+}
+
 __global__ __launch_bounds__(kMetaThreads) void classify_kernel(
     const uint8_t* __restrict__ mask, int64_t seq_stride, int64_t row_stride, MetaGeom g,
     int8_t* __restrict__ cls, int32_t* __restrict__ words) {
   const int blk = blockIdx.x;  // qb * ntb + tb
   const int seq = blockIdx.y;
   const int qb = blk / g.ntb, tb = blk - qb * g.ntb;
-  const int q0 = qb * g.block_m, k0 = tb * g.block_n;
-  const int h = min(g.block_m, g.q_len - q0);
-  const int w = min(g.block_n, g.q_len - k0);
-  const uint8_t* m = mask + seq * seq_stride + (int64_t)q0 * row_stride + k0;
   int32_t* out = words + ((int64_t)seq * g.cap + blk) * g.words;
-  const int64_t n_flat = (int64_t)g.block_m * g.block_n;
 
   int ones = 0;
   for (int wi = threadIdx.x; wi < g.words; wi += kMetaThreads) {
-    int64_t flat = (int64_t)wi * 32;
-    int r = (int)(flat / g.block_n);
-    int c = (int)(flat - (int64_t)r * g.block_n);
-    uint32_t word = 0;
-    for (int i = 0; i < 32 && flat + i < n_flat; ++i) {
-      if (r < h && c < w && m[(int64_t)r * row_stride + c] != 0) word |= 1u << i;
-      if (++c == g.block_n) { c = 0; ++r; }
-    }
+    const uint32_t word = block_word(mask + seq * seq_stride, row_stride, g, qb, tb, wi);
     out[wi] = (int32_t)word;
     ones += __popc(word);
   }
@@ -65,9 +88,7 @@ __global__ __launch_bounds__(kMetaThreads) void classify_kernel(
   if (threadIdx.x == 0) {
     int total = 0;
     for (int i = 0; i < kMetaThreads / 64; ++i) total += red[i];
-    int8_t c = kZero;
-    if (total > 0) c = (total == h * w) ? kFull : kMixed;
-    cls[(int64_t)seq * g.cap + blk] = c;
+    cls[(int64_t)seq * g.cap + blk] = block_class(g, qb, tb, total);
   }
 }
 
@@ -93,14 +114,13 @@ __device__ inline void scan2(int a, int b, int* ex_a, int* ex_b, int* tot_a, int
   __syncthreads();
 }
 
-__global__ __launch_bounds__(kMetaThreads) void compact_kernel(
-    MetaGeom g, const int8_t* __restrict__ cls, const int32_t* __restrict__ words,
-    int32_t* __restrict__ src_of_rank, int32_t* __restrict__ row_ptr, int32_t* __restrict__ col_idx,
-    int8_t* __restrict__ blk_type, int32_t* __restrict__ payload, int32_t* __restrict__ offset,
-    int32_t* __restrict__ counts) {
-  const int seq = blockIdx.x;
+// CSR scatter of sequence seq from its block classes c[], packed words
+// wsrc[] and rank scratch sr[] (global memory, or LDS for build_small).
+__device__ inline void compact_seq(const MetaGeom& g, int seq, const int8_t* c, const int32_t* wsrc, int32_t* sr,
+                                   int32_t* __restrict__ row_ptr, int32_t* __restrict__ col_idx,
+                                   int8_t* __restrict__ blk_type, int32_t* __restrict__ payload,
+                                   int32_t* __restrict__ offset, int32_t* __restrict__ counts) {
   const int64_t nb = g.cap;
-  const int8_t* c = cls + seq * nb;
   const int per = (int)((nb + kMetaThreads - 1) / kMetaThreads);
   const int64_t i0 = min((int64_t)threadIdx.x * per, nb);
   const int64_t i1 = min(i0 + per, nb);
@@ -117,7 +137,6 @@ __global__ __launch_bounds__(kMetaThreads) void compact_kernel(
   int32_t* ci = col_idx + seq * nb;
   int8_t* bt = blk_type + seq * nb;
   int32_t* of = offset + seq * nb;
-  int32_t* sr = src_of_rank + seq * nb;
   for (int64_t i = i0; i < i1; ++i) {
     const int qb = (int)(i / g.ntb), tb = (int)(i - (int64_t)qb * g.ntb);
     if (tb == 0) rp[qb] = nz_base;
@@ -142,12 +161,53 @@ __global__ __launch_bounds__(kMetaThreads) void compact_kernel(
   __syncthreads();  // src_of_rank complete (workgroup-scope fence + barrier)
 
   const int64_t total = (int64_t)n_mixed * g.words;
-  const int32_t* wsrc = words + seq * nb * g.words;
   int32_t* pl = payload + seq * nb * g.words;
   for (int64_t e = threadIdx.x; e < total; e += kMetaThreads) {
     const int64_t r = e / g.words, wi = e - r * g.words;
     pl[e] = wsrc[(int64_t)sr[r] * g.words + wi];
   }
+}
+
+__global__ __launch_bounds__(kMetaThreads) void compact_kernel(
+    MetaGeom g, const int8_t* __restrict__ cls, const int32_t* __restrict__ words,
+    int32_t* __restrict__ src_of_rank, int32_t* __restrict__ row_ptr, int32_t* __restrict__ col_idx,
+    int8_t* __restrict__ blk_type, int32_t* __restrict__ payload, int32_t* __restrict__ offset,
+    int32_t* __restrict__ counts) {
+  const int seq = blockIdx.x;
+  const int64_t nb = g.cap;
+  compact_seq(g, seq, cls + seq * nb, words + seq * nb * g.words, src_of_rank + seq * nb, row_ptr, col_idx,
+              blk_type, payload, offset, counts);
+}
+
+// One workgroup per sequence: packed words and block bit counts in LDS,
+// classes, then the same scatter as compact_kernel.
+__global__ __launch_bounds__(kMetaThreads) void build_small_kernel(
+    const uint8_t* __restrict__ mask, int64_t seq_stride, int64_t row_stride, MetaGeom g,
+    int32_t* __restrict__ row_ptr, int32_t* __restrict__ col_idx, int8_t* __restrict__ blk_type,
+    int32_t* __restrict__ payload, int32_t* __restrict__ offset, int32_t* __restrict__ counts) {
+  __shared__ int32_t s_words[kSmallWords];
+  __shared__ int s_ones[kSmallBlocks];
+  __shared__ int32_t s_rank[kSmallBlocks];
+  __shared__ int8_t s_cls[kSmallBlocks];
+  const int seq = blockIdx.x;
+  const int nb = (int)g.cap;
+  for (int i = threadIdx.x; i < nb; i += kMetaThreads) s_ones[i] = 0;
+  __syncthreads();
+  const uint8_t* m0 = mask + seq * seq_stride;
+  for (int e = threadIdx.x; e < nb * g.words; e += kMetaThreads) {
+    const int blk = e / g.words, wi = e - blk * g.words;
+    const int qb = blk / g.ntb, tb = blk - qb * g.ntb;
+    const uint32_t word = block_word(m0, row_stride, g, qb, tb, wi);
+    s_words[e] = (int32_t)word;
+    if (word != 0) atomicAdd(&s_ones[blk], __popc(word));
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nb; i += kMetaThreads) {
+    const int qb = i / g.ntb;
+    s_cls[i] = block_class(g, qb, i - qb * g.ntb, s_ones[i]);
+  }
+  __syncthreads();
+  compact_seq(g, seq, s_cls, s_words, s_rank, row_ptr, col_idx, blk_type, payload, offset, counts);
 }
 
 __global__ void pack_bits_kernel(const uint8_t* __restrict__ bits, int64_t n_bits, int32_t* __restrict__ words,
@@ -221,6 +281,14 @@ extern "C" int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int
   int32_t* words = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb));
   int32_t* src_of_rank =
       reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb) + align256(nb * g.words * 4));
+  const char* small_env = getenv("TSFA_META_SMALL");  // "0": always two launches
+  const bool small = g.cap > 0 && g.cap <= kSmallBlocks && g.cap * g.words <= kSmallWords &&
+                     !(small_env != nullptr && small_env[0] == '0');
+  if (small) {
+    hipLaunchKernelGGL(build_small_kernel, dim3((unsigned)n_seq), dim3(kMetaThreads), 0, stream, mask,
+                       mask_seq_stride, mask_row_stride, g, row_ptr, col_idx, blk_type, payload, offset, counts);
+    return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+  }
   if (g.cap > 0) {
     if (g.cap > INT32_MAX) return TSFA_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(classify_kernel, dim3((unsigned)g.cap, (unsigned)n_seq), dim3(kMetaThreads), 0, stream,

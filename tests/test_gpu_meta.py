@@ -46,8 +46,13 @@ def _sweep_cases():
     return cases
 
 
+# "auto": trees whose packed words fit in LDS take the one-launch builder;
+# "two-launch" forces classify + compact for every shape
+@pytest.mark.parametrize("path", ["auto", "two-launch"])
 @pytest.mark.parametrize("q_len,bm,bn,kind,seed", _sweep_cases())
-def test_sweep(q_len, bm, bn, kind, seed):
+def test_sweep(q_len, bm, bn, kind, seed, path, monkeypatch):
+    if path == "two-launch":
+        monkeypatch.setenv("TSFA_META_SMALL", "0")
     rng = np.random.default_rng(seed)
     if kind == "random":
         m = rng.random((q_len, q_len)) < rng.random()
@@ -78,7 +83,10 @@ def test_validation_errors():
         tsf.prepare_tree_sparse_metadata(torch.ones(4, 4, device="cuda"), 0, 0, 16)
 
 
-def test_batched_matches_per_sequence():
+@pytest.mark.parametrize("path", ["auto", "two-launch"])
+def test_batched_matches_per_sequence(path, monkeypatch):
+    if path == "two-launch":
+        monkeypatch.setenv("TSFA_META_SMALL", "0")
     w = configs.WORKLOADS["batched-decode-b16-p2048"]
     masks = configs.make_tree_mask(w).cuda()
     bm = tsf.prepare_tree_sparse_metadata_batched(masks, w.prefix_len, w.block_m, w.block_n)
