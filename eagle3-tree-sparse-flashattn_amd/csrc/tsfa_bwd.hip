@@ -846,6 +846,8 @@ int make_bwd_plan(int batch, int num_kv_heads, int q_len, int kv_len, int prefix
 // per CU on 256 CUs at the Llama-3-8B shape).  Default priority; the side
 // stream does not synchronise with the null stream.  A call captured into a
 // graph forks and joins inside the capture.
+constexpr int kMaxSideStreams = 64;
+
 struct SideStream {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
@@ -860,11 +862,15 @@ const SideStream* side_stream(hipStream_t stream) {
   const auto key = std::make_pair(dev, reinterpret_cast<uintptr_t>(stream));
   auto it = sides.find(key);
   if (it != sides.end()) return &it->second;
+  // at most kMaxSideStreams per device; callers past that run on one stream
+  static int per_dev[64] = {};
+  if (dev < 0 || dev >= 64 || per_dev[dev] >= kMaxSideStreams) return nullptr;
   SideStream ss;
   if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
   if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
     return nullptr;
+  ++per_dev[dev];
   return &sides.emplace(key, ss).first->second;
 }
 

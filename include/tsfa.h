@@ -148,7 +148,8 @@ int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o, float* ls
  * four kernel launches, no host synchronisation: the dQ kernel runs on a
  * library-owned side stream forked from `stream` after the first launch and
  * joined back before the call returns its last launch (one side stream and
- * two events per device and caller stream, kept for the process; inside a
+ * two events per device and caller stream, kept for the process, at most
+ * 64 per device, beyond which calls stay on `stream`; inside a
  * graph capture the fork and join are captured too; TSFA_BWD_CONCURRENT=0
  * keeps every launch on `stream`).  Supported: the
  * shapes tsfa_fwd supports with q_len * gqa_group_size < 2^22; the tree's

@@ -215,3 +215,33 @@ def test_bwd_graph_capture_replays():
         # dK / dV have a fixed summation order; dQ sums fp32 atomics of the key splits
         assert torch.equal(dk, eager[1]) and torch.equal(dv, eager[2]), f"replay {i}"
         torch.testing.assert_close(dq, eager[0], rtol=1e-2, atol=1e-3)
+
+
+def test_bwd_two_streams_at_once(monkeypatch):
+    # each caller stream gets its own side stream for the dQ kernel: two
+    # backward calls in flight on two streams give the single-stream results
+    b, hq, hkv, t, p, d = 1, 32, 8, 64, 1024, 128
+    mask = torch.from_numpy(_tree("eagle", t, np.random.default_rng(5)))
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, 16, 64)
+    ins = []
+    for seed in (31, 32):
+        q, k, v, do = (x.cuda() for x in _inputs(b, hq, hkv, t, p, d, BF, seed=seed))
+        o, lse = tsf.tree_sparse_attention_fwd(q, k, v, meta, return_lse=True)
+        ins.append((q, k, v, o, lse, do))
+    with monkeypatch.context() as m:
+        m.setenv("TSFA_BWD_CONCURRENT", "0")
+        refs = [tsf.tree_sparse_attention_bwd(*x, meta) for x in ins]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = [[], []]
+    for _ in range(8):
+        for j in (0, 1):
+            with torch.cuda.stream(streams[j]):
+                outs[j].append(tsf.tree_sparse_attention_bwd(*ins[j], meta))
+    torch.cuda.synchronize()
+    for j in (0, 1):
+        for dq, dk, dv in outs[j]:
+            assert torch.equal(dk, refs[j][1]) and torch.equal(dv, refs[j][2])
+            torch.testing.assert_close(dq, refs[j][0], rtol=1e-2, atol=1e-3)
