@@ -1523,16 +1523,21 @@ int64_t chunk_qblocks(int rows, int group, int block_m) { return (chunk_tokens(r
 // the grid.  The 8-wave kernel with two streams of 128-row chunks by default
 // (TSFA_STREAMS=1: one stream, 256-row chunks).  TSFA_WIDE=2 selects the wide
 // kernel (256-row chunks, one wave per SIMD), TSFA_WIDE=1 selects it above
-// 128 rows per (batch, kv head).  On the 8B decode shape the 8-wave kernel
-// measured faster: the short per-workgroup runs (4-8 units of 32 keys) leave
-// the wide kernel's longer Q staging and deeper pipeline unamortised.
+// 128 rows per (batch, kv head), TSFA_WIDE=0 never.  By default the wide
+// kernel runs long prefixes (>= 8192 keys) under a small tree (<= 256 keys)
+// with >= 1024 rows per (batch, kv head): the 70B shape, 1376.7 -> 1345.6 us
+// per call.  With a large tree (the 1024-token wide tree: 337 -> 395 us) or
+// short runs (the 8B decode shape: its 4-8 units of 32 keys leave the wide
+// kernel's longer Q staging and deeper pipeline unamortised) the 8-wave
+// kernel is faster.
 int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
-              Plan* p) {
+              Plan* p, bool paged = false) {
   const int G = num_heads / num_kv_heads;
   const int64_t TG = (int64_t)q_len * G;
   if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
-  const int wide = env_int("TSFA_WIDE", 0);
-  p->wide = wide == 2 || (wide == 1 && TG > kMaxRows / 2);
+  const int wide = env_int("TSFA_WIDE", -1);
+  p->wide = wide == 2 || (wide == 1 && TG > kMaxRows / 2) ||
+            (wide < 0 && !paged && TG >= 1024 && prefix_len >= 8192 && kv_len - prefix_len <= 256);
   p->streams = p->wide ? 1 : (env_int("TSFA_STREAMS", 2) == 1 ? 1 : 2);
   p->rows_per_chunk = kMaxRows / p->streams;
   p->n_chunks = (int)((TG + p->rows_per_chunk - 1) / p->rows_per_chunk);
@@ -1725,9 +1730,12 @@ extern "C" int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, i
 extern "C" size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                            int prefix_len, int head_dim) {
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
-  Plan p;
-  if (make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p) != TSFA_OK) return 0;
-  return p.ws_acc_bytes + p.ws_ml_bytes;
+  // enough for both the contiguous and the paged plan of the shape
+  Plan p, pp;
+  if (make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p) != TSFA_OK ||
+      make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &pp, true) != TSFA_OK)
+    return 0;
+  return std::max(p.ws_acc_bytes + p.ws_ml_bytes, pp.ws_acc_bytes + pp.ws_ml_bytes);
 }
 
 extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
@@ -1810,7 +1818,7 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
     if (meta_seq_stride[i] < 0) return TSFA_ERR_INVALID_ARGUMENT;
 
   Plan p;
-  st = make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p);
+  st = make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p, kv.paged());
   if (st != TSFA_OK) return st;
   p.tree_key_limit = (int)std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
   if (workspace == nullptr || workspace_bytes < p.ws_acc_bytes + p.ws_ml_bytes) return TSFA_ERR_WORKSPACE;
