@@ -249,7 +249,7 @@ def backward_timing(w, mask, qd, ks, vs, meta, steps: int, fwd_flops: float, cpu
     res = {"us_per_call": round(us, 3), "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
            "achieved_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4),
            "achieved_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "cpu_baseline": None,
-           "kernels": "prep and tree visibility (one launch) + key-parallel dK/dV + row-parallel dQ (+ dQ convert when the key range is split)"}
+           "kernels": "prep and tree visibility (one launch) + key-parallel dK/dV beside row-parallel dQ on a side stream (+ dQ convert when the key range is split)"}
     if cpu_seconds > 0:
         # the fp32 gradient oracle (closed forms, oracle/attn_grad_oracle.py) on the host cores
         from oracle.attn_grad_oracle import attention_grads
