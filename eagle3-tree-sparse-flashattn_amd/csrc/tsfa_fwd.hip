@@ -13,10 +13,15 @@
 //     a workgroup owns a chunk of 128 consecutive rows;
 //   * keys move in units of 32.  The prefix units are cut into runs (split-KV:
 //     a small tree still spreads the prefix over all 256 CUs) and one more
-//     workgroup per chunk runs the tree units: it expands the CSR rows of the
-//     chunk's q-blocks into per-token 32-bit visibility words for every tree
-//     unit that holds a visible key, and skips the rest (ZERO blocks are never
-//     loaded);
+//     workgroup per chunk runs the tree units (or, when that would add a
+//     round of workgroups and the tree is short, the chunk's last run does):
+//     it expands the CSR rows of the chunk's q-blocks into per-token 32-bit
+//     visibility words for every tree unit that holds a visible key, and
+//     skips the rest (ZERO blocks are never loaded);
+//   * work items map to XCDs in contiguous ranges, so the row chunks that read
+//     the same K/V units share an XCD's L2 (K/V loads carry the non-temporal
+//     hint when at most two chunks share a unit); plans of a few rounds
+//     dispatch each XCD's long items first;
 //   * a workgroup is 8 waves, two per SIMD: two key streams x four row groups
 //     of 32 rows.  Stream s takes every other unit of the workgroup's run
 //     through its own LDS ring, filled by global_load_lds (HBM -> LDS, 16 B
@@ -34,9 +39,11 @@
 //     unit;
 //   * at the end the two streams' (m, l, O) merge in LDS and the workgroup writes
 //     one partial per row (O/l in the input dtype, fp32 (m, l)); a second
-//     kernel merges the partials (log-sum-exp) and writes O.
-//   * wide_kernel (opt-in) runs the same work items with one wave per SIMD and
-//     64 rows per wave (AGPR accumulators), halving LDS operand bytes per MFMA.
+//     kernel merges the partials (log-sum-exp) and writes O, each XCD merging
+//     the chunks its split workgroups wrote (the partials come from its L2).
+//   * wide_kernel runs the same work items with one wave per SIMD and 64 rows
+//     per wave (AGPR accumulators), halving LDS operand bytes per MFMA; the
+//     planner picks it for long prefixes under small trees.
 
 #include <math.h>
 #include <stdlib.h>
