@@ -959,7 +959,8 @@ void wide_kernel(const SplitArgs a) {
   const int slot = rest % a.n_slots;
   const int bk = rest / a.n_slots;
   const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
-  const bool is_tree = slot == a.n_slots - 1;
+  const bool is_tree = !a.fold_tree && slot == a.n_slots - 1;  // as in split_kernel
+  const bool do_tree = slot == a.n_slots - 1;
 
   const int G = a.group;
   const int TG = a.q_len * G;
@@ -1297,8 +1298,10 @@ void wide_kernel(const SplitArgs a) {
     run_units(
         n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
         [&](int i, int) { return (1u << (P - key0_of(i))) - 1u; });
-  } else {
-    load_q();
+  }
+  if (do_tree) {
+    if (is_tree) load_q();
+    else sync_all();  // the prefix run's ring reads and loads done; Q stays in registers
     const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
     const int tok_hi = (row0 + rows_chunk - 1) / G;
     const int ntok = tok_hi - tok_lo + 1;
@@ -1588,18 +1591,21 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   p->units_per_split = ups;
   p->n_splits = ups > 0 ? ceil_div(p->n_pu, ups) : 0;
   // A separate tree item per chunk costs a round when it does not fit beside
-  // the prefix runs; then, if the tree is short next to a run (at most a
-  // quarter of its units, or 2), the last run of each chunk takes the tree
-  // units too (the 16-sequence decode shape: 3 rounds -> 2).  TSFA_FOLD_TREE
-  // =0/1 forces it off/on (on only where there is a prefix run).
+  // the prefix runs; on a plan of at most 4 rounds, if the tree is short next
+  // to a run (at most a quarter of its units, or 2), the last run of each
+  // chunk takes the tree units too (the 16-sequence decode shape: 3 rounds ->
+  // 2, 73.6 -> 66.0 us per call; on the 70B shape, 16 rounds -> 15, folding
+  // measured 0.6 % slower).  TSFA_FOLD_TREE=0/1 forces it off/on (on only
+  // where there is a prefix run).
   p->fold_tree = 0;
-  if (!p->wide && p->n_splits >= 1) {
+  if (p->n_splits >= 1) {
     const int64_t tree_units = ceil_div(std::max(0, kv_len - prefix_len), kUnitKeys);
     const int64_t rounds_sep = (groups * (p->n_splits + 1) + cus - 1) / cus;
     const int64_t rounds_fold = (groups * p->n_splits + cus - 1) / cus;
     const int force = env_int("TSFA_FOLD_TREE", -1);
     p->fold_tree = force >= 0 ? (force != 0)
-                              : (rounds_fold < rounds_sep && tree_units <= std::max(2, ups / 4) ? 1 : 0);
+                              : (rounds_fold < rounds_sep && rounds_sep <= 4 && tree_units <= std::max(2, ups / 4)
+                                     ? 1 : 0);
   }
   p->n_slots = p->n_splits + (p->fold_tree ? 0 : 1);
   const int64_t items = groups * p->n_slots;

@@ -119,7 +119,8 @@ def test_cases(case):
 KERNELS = {"wide": {"TSFA_WIDE": "2"}, "one-stream": {"TSFA_WIDE": "0", "TSFA_STREAMS": "1"},
            "kv-nt": {"TSFA_KV_NT": "1"}, "kv-temporal": {"TSFA_KV_NT": "0"},
            "items-natural": {"TSFA_ITEM_ORDER": "0"}, "items-tree-first": {"TSFA_ITEM_ORDER": "2"},
-           "tree-folded": {"TSFA_FOLD_TREE": "1"}, "tree-separate": {"TSFA_FOLD_TREE": "0"}}
+           "tree-folded": {"TSFA_FOLD_TREE": "1"}, "tree-separate": {"TSFA_FOLD_TREE": "0"},
+           "wide-tree-folded": {"TSFA_WIDE": "2", "TSFA_FOLD_TREE": "1"}}
 
 
 @pytest.mark.parametrize("kernel", sorted(KERNELS))
