@@ -108,6 +108,8 @@ struct SplitArgs {
   int n_indices;              // entries of kv_indices (< 2^31)
   int page_shift, n_pages;
   int kv_nt;  // K/V loads non-temporal (each unit read by at most two row chunks)
+  int cache32;                // paged cache below 4 GB (selects the 32-bit-offset kernel)
+  uint32_t cps_b32, crs_b32;  // its page and row strides in bytes
   int item_order;  // within an XCD: 0 natural, 1 prefix runs first, 2 tree items first
   int fold_tree;   // no tree items: the last prefix split of each chunk also runs the tree units
 };
@@ -288,7 +290,7 @@ __device__ inline int64_t clamp_page(const SplitArgs& a, int raw) { return (int6
 // its RPL rows sit in one page below kv_len and per-lane clamped addresses
 // when it straddles a page boundary or reaches past kv_len (those keys are
 // masked).
-template <typename T, int D, bool IS_V, int NL>
+template <typename T, int D, bool IS_V, int NL, bool C32>
 __device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_t pid0, int64_t pid1, int pg0,
                                       uint32_t lds_dst, int key0, int lane, int u_lo, const uint32_t* loff,
                                       bool nt) {
@@ -300,8 +302,17 @@ __device__ inline void dma_half_paged(const T* hbase, const SplitArgs& a, int64_
   const int kw = key0 + u_lo * RPL;  // first key of the wave's share
   auto row_ptr = [&](int64_t pid, int key) { return hbase + pid * a.cps + (int64_t)(key & pmask) * a.crs; };
   if (kw + NL * RPL <= kv_len && (kw & pmask) + NL * RPL <= pmask + 1) {
-    const char* rowp = reinterpret_cast<const char*>(row_ptr(pid0, kw));
-    const int64_t step = (int64_t)RPL * a.crs * 2;
+    // C32 (a cache below 4 GB): 32-bit byte offsets from the head's base,
+    // fewer scalar products and live 64-bit values in the issue path
+    const char* rowp;
+    int64_t step;
+    if constexpr (C32) {
+      rowp = reinterpret_cast<const char*>(hbase) + ((uint32_t)pid0 * a.cps_b32 + (uint32_t)(kw & pmask) * a.crs_b32);
+      step = (int64_t)(RPL * a.crs_b32);
+    } else {
+      rowp = reinterpret_cast<const char*>(row_ptr(pid0, kw));
+      step = (int64_t)RPL * a.crs * 2;
+    }
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int u = u_lo + i;
@@ -365,7 +376,7 @@ __device__ inline int work_item(const SplitArgs& a) {
 }
 
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.
-template <typename T, int D, int S, bool PAGED>
+template <typename T, int D, int S, bool PAGED, bool C32 = false>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
@@ -470,9 +481,9 @@ void split_kernel(const SplitArgs a) {
       }
       const int64_t pid0 = clamp_page(a, raw0), pid1 = clamp_page(a, raw1);
       if (dma_v)
-        dma_half_paged<T, D, true, LPU>(vbase, a, pid0, pid1, pg0, sb + HALF, key0, lane, dma_u0, loff, kv_nt);
+        dma_half_paged<T, D, true, LPU, C32>(vbase, a, pid0, pid1, pg0, sb + HALF, key0, lane, dma_u0, loff, kv_nt);
       else
-        dma_half_paged<T, D, false, LPU>(kbase, a, pid0, pid1, pg0, sb, key0, lane, dma_u0, loff, kv_nt);
+        dma_half_paged<T, D, false, LPU, C32>(kbase, a, pid0, pid1, pg0, sb, key0, lane, dma_u0, loff, kv_nt);
     } else if (kv_nt) {
       if (dma_v)
         dma_half<T, D, true, LPU, false, true>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
@@ -1626,7 +1637,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   return TSFA_OK;
 }
 
-template <typename T, int D, int S, bool PAGED>
+template <typename T, int D, int S, bool PAGED, bool C32 = false>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -1635,12 +1646,12 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
+  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -1668,9 +1679,15 @@ thread_local int g_kernel_mask = 3;
 template <typename T, int D, bool PAGED>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
-    const int st = (p.wide && !PAGED) ? launch_wide<T, D>(sa, p, stream)
-                   : p.streams == 2   ? launch_split<T, D, 2, PAGED>(sa, p, stream)
-                                      : launch_split<T, D, 1, PAGED>(sa, p, stream);
+    int st;
+    if constexpr (PAGED)
+      st = (sa.cache32 && p.streams == 2) ? launch_split<T, D, 2, true, true>(sa, p, stream)
+           : p.streams == 2               ? launch_split<T, D, 2, true>(sa, p, stream)
+                                          : launch_split<T, D, 1, true>(sa, p, stream);
+    else
+      st = p.wide             ? launch_wide<T, D>(sa, p, stream)
+           : p.streams == 2   ? launch_split<T, D, 2, false>(sa, p, stream)
+                              : launch_split<T, D, 1, false>(sa, p, stream);
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;
@@ -1866,6 +1883,13 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
     int shift = 0;
     while ((1 << shift) < kv.page_size) ++shift;
     sa.page_shift = shift;
+    // byte offsets from a head's base stay inside the cache: 32 bits suffice
+    // below 4 GB (TSFA_PAGED32=0 keeps the 64-bit kernel)
+    const uint64_t cache_bytes = (uint64_t)kv.n_pages * (uint64_t)kv.cache_strides[0] * 2;
+    sa.cache32 = (kv.cache_strides[0] > 0 && cache_bytes < ((uint64_t)1 << 32) && env_int("TSFA_PAGED32", 1) != 0)
+                     ? 1 : 0;
+    sa.cps_b32 = (uint32_t)(kv.cache_strides[0] * 2);
+    sa.crs_b32 = (uint32_t)(kv.cache_strides[2] * 2);
   } else {
     sa.k = kv.k;
     sa.v = kv.v;

@@ -88,6 +88,14 @@ def test_paged_one_stream_kernel(case, monkeypatch):
     test_paged_cases(case)
 
 
+@pytest.mark.parametrize("case", [CASES[i] for i in (0, 2, 4, 5, 7)], ids=["p0", "p2", "p4", "p5", "p7"])
+def test_paged_64bit_offsets(case, monkeypatch):
+    # caches below 4 GB take the 32-bit-offset kernel by default; this runs
+    # the 64-bit one on the same cases
+    monkeypatch.setenv("TSFA_PAGED32", "0")
+    test_paged_cases(case)
+
+
 def test_paged_ignores_wide_switch(monkeypatch):
     # the paged forward always runs the 8-wave kernel, whatever the planner picks
     monkeypatch.setenv("TSFA_WIDE", "2")
