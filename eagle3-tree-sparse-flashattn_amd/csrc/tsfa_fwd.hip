@@ -66,6 +66,20 @@ constexpr int kMaxTreeUnits = 1024;  // tree keys <= 32768
 constexpr int kMiscInts = 320;       // LDS scalars: visible-unit count, row_ptr window
 constexpr float kRescaleLog2 = 8.0f;
 
+// Per-workgroup timestamps for timeline measurements: compiled in only with
+// -DTSFA_STAMPS (a separate measurement build); TSFA_STAMP is empty otherwise.
+#ifdef TSFA_STAMPS
+__device__ unsigned long long g_stamps[4096 * 64];
+#define TSFA_STAMP(k)                                                                      \
+  do {                                                                                     \
+    if (threadIdx.x == 0) g_stamps[(size_t)blockIdx.x * 64 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define TSFA_STAMP(k) \
+  do {            \
+  } while (0)
+#endif
+
 struct CombineArgs {
   void* o;
   int64_t sob, soh, som;
@@ -153,6 +167,50 @@ __device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_ba
                  : "v"(voff), "s"(sbase), "s"(lds_base)
                  : "memory", "m0");
 }
+// N loads of 1 KB (N = 4, 2 or 1) with one scalar base and one M0: load i goes
+// to LDS m0v + i KB and reads global sbase + off[i] + i KB -- the
+// instruction's immediate offset applies to the LDS address as well as the
+// global one (checked on gfx950), so consecutive LDS KBs need no M0 update.
+template <int N, bool NT>
+__device__ inline void dma_rows(const void* sbase, const uint32_t (&off)[N], uint32_t m0v) {
+  static_assert(N == 4 || N == 2 || N == 1, "loads per wave and unit");
+  if constexpr (N == 1 && NT)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2 nt"
+                 :
+                 : "v"(off[0]), "s"(m0v), "s"(sbase)
+                 : "memory", "m0");
+  else if constexpr (N == 1)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2"
+                 :
+                 : "v"(off[0]), "s"(m0v), "s"(sbase)
+                 : "memory", "m0");
+  else if constexpr (N == 4 && NT)
+    asm volatile("s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, %5 nt\n\tglobal_load_lds_dwordx4 %1, %5 offset:1024 nt\n\t"
+                 "global_load_lds_dwordx4 %2, %5 offset:2048 nt\n\tglobal_load_lds_dwordx4 %3, %5 offset:3072 nt"
+                 :
+                 : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(m0v), "s"(sbase)
+                 : "memory", "m0");
+  else if constexpr (N == 4)
+    asm volatile("s_mov_b32 m0, %4\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, %5\n\tglobal_load_lds_dwordx4 %1, %5 offset:1024\n\t"
+                 "global_load_lds_dwordx4 %2, %5 offset:2048\n\tglobal_load_lds_dwordx4 %3, %5 offset:3072"
+                 :
+                 : "v"(off[0]), "v"(off[1]), "v"(off[2]), "v"(off[3]), "s"(m0v), "s"(sbase)
+                 : "memory", "m0");
+  else if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, %3 nt\n\tglobal_load_lds_dwordx4 %1, %3 offset:1024 nt"
+                 :
+                 : "v"(off[0]), "v"(off[1]), "s"(m0v), "s"(sbase)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\t"
+                 "global_load_lds_dwordx4 %0, %3\n\tglobal_load_lds_dwordx4 %1, %3 offset:1024"
+                 :
+                 : "v"(off[0]), "v"(off[1]), "s"(m0v), "s"(sbase)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 template <int N> __device__ inline void vm_wait() {
@@ -179,6 +237,11 @@ __device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barr
 __device__ inline void sync_all() { asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ inline uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const TSFA_LDS void*)p; }
+// LDS reads at a 32-bit LDS byte address (no generic-pointer base arithmetic).
+template <typename V> __device__ inline V lds_ld(uint32_t addr) { return *(const TSFA_LDS V*)(uintptr_t)addr; }
+__device__ inline i16x4 lds_tr(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(uintptr_t)addr);
+}
 
 template <typename V, typename U> __device__ inline V bit_cast(U u) { return __builtin_bit_cast(V, u); }
 
@@ -229,12 +292,17 @@ __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst,
     }
   } else if (OFF32) {
     // scalar base at row key0; a lane's row is at most 31 rows further and
-    // row strides stay below 2^26 elements, so its byte offset fits 32 bits
+    // row strides stay below 2^26 elements, so its byte offset fits 32 bits.
+    // The lane index goes through an empty asm: this path runs once per run,
+    // and its lane terms hoisted out of the unit loop would hold registers
+    // (spilled) for the whole loop.
+    int ln_ = lane;
+    asm volatile("" : "+v"(ln_));
     const char* rowp = reinterpret_cast<const char*>(base + (int64_t)key0 * stride);
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int u = u_lo + i;
-      const int row = u * RPL + lane / CPR, pos = lane % CPR;
+      const int row = u * RPL + ln_ / CPR, pos = ln_ % CPR;
       const uint32_t rel = (uint32_t)(min(key0 + row, kv_len - 1) - key0);
       const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
       dma16_s(rowp, rel * (uint32_t)stride * 2u + (uint32_t)((pos ^ sw) << 4), lds_dst + u * 1024);
@@ -248,6 +316,31 @@ __device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst,
       const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
       dma16(base + (int64_t)key * stride + ((pos ^ sw) << 3), lds_dst + u * 1024);
     }
+  }
+}
+
+// Loads [u_lo, u_lo + NL) of one half of a unit whose rows may reach past
+// kv_len, or whose row stride is below D: per-lane rows clamped to kv_len - 1
+// (those keys are masked) from a scalar base at key0 with 32-bit lane
+// offsets (a lane's row is at most 31 rows further and row strides stay below
+// 2^26 elements).  The lane index passes through an empty asm: this runs at
+// most once per run, and lane terms hoisted out of the unit loop would hold
+// registers for the whole loop.
+template <typename T, int D, bool IS_V, int NL>
+__device__ inline void dma_tail(const T* base, int64_t stride, uint32_t lds_dst, int key0, int kv_len, int lane,
+                                int u_lo) {
+  constexpr int CPR = D / 8;
+  constexpr int RPL = 64 / CPR;
+  int ln_ = lane;
+  asm volatile("" : "+v"(ln_));
+  const char* rowp = reinterpret_cast<const char*>(base + (int64_t)key0 * stride);
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int u = u_lo + i;
+    const int row = u * RPL + ln_ / CPR, pos = ln_ % CPR;
+    const uint32_t rel = (uint32_t)(min(key0 + row, kv_len - 1) - key0);
+    const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
+    dma16_s(rowp, rel * (uint32_t)stride * 2u + (uint32_t)((pos ^ sw) << 4), lds_dst + u * 1024);
   }
 }
 
@@ -375,8 +468,9 @@ __device__ inline int work_item(const SplitArgs& a) {
   return j < np ? kth_prefix(plo + j) : kth_tree(lo - plo + j - np);
 }
 
-// S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.
-template <typename T, int D, int S, bool PAGED, bool C32 = false>
+// S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  PIPE
+// selects the software-pipelined unit loop (run_units_pipe).
+template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
@@ -400,7 +494,7 @@ void split_kernel(const SplitArgs a) {
   static_assert(QS >= 1 && QS < NS && QROWS * ROWB == QS * SB, "Q staging");
   static_assert(S == 1 || kWaves * DT * 64 * 64 / 2 + ROWS * ROWB <= kRingBytes, "merge buffer");
 
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  extern __shared__ __attribute__((aligned(256))) unsigned char smem[];  // stage bases keep bits 0-7 clear
   unsigned char* ring = smem;
   uint32_t* masks = reinterpret_cast<uint32_t*>(smem + kRingBytes);
   int* vis = reinterpret_cast<int*>(masks + kMaskWords);
@@ -414,6 +508,10 @@ void split_kernel(const SplitArgs a) {
 
   const int item = work_item(a);
   if (item < 0) return;
+  TSFA_STAMP(0);
+#ifdef TSFA_STAMPS
+  if (threadIdx.x == 0) g_stamps[(size_t)blockIdx.x * 64 + 63] = (unsigned long long)item;
+#endif
   const int chunk = item % a.n_chunks;
   int rest = item / a.n_chunks;
   const int slot = rest % a.n_slots;
@@ -441,15 +539,49 @@ void split_kernel(const SplitArgs a) {
   if (PAGED) pt_base = a.kv_indptr ? ld_uniform(a.kv_indptr, b) : b * a.pt_stride;
   unsigned char* sring = ring + ks * RB;
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+  // One-shot prefix runs (pipelined loop, contiguous K/V, two streams): unit i
+  // of a run of at most NOS units sits in stage i of the ring followed by the
+  // mask area (a prefix run does not use it), Q in the last two stages; every
+  // unit is requested up front (the two behind Q once Q is read) and the loop
+  // only waits.  Latency under load is ~2.5 us, so a ring that requests a
+  // unit two steps ahead stalls every step on short runs.
+  constexpr int NOS = (kRingBytes + kMaskWords * 4) / SB;
+  static_assert(S == 1 || QS == 1, "one-shot Q staging: one stage per stream");
+  static_assert(NOS <= 32 && (NOS - S) * LPU < 64, "one-shot geometry");
+  // LDS address of the stage of the stream's unit j: ring stage j % NS, or
+  // stage ks + S*j of the one-shot layout
+  bool oneshot = false;
+  uint32_t st_base = sring_lds, st_step = SB;
+  int st_mask = NS - 1;
+  auto stage = [&](int j) { return st_base + (uint32_t)((j & st_mask) * st_step); };
 
   // The stream's RG waves move equal shares of each unit: the first half of
   // them K, the second half V.
   const bool dma_v = rg >= RG / 2;
   const int dma_u0 = (rg % (RG / 2)) * LPU;
-  uint32_t loff[D == 128 ? 4 : 2];
+  uint32_t loff[D == 128 ? 4 : 2];  // paged: lane offsets of the loads (by load index mod NOFF)
+  if constexpr (PAGED) {
 #pragma unroll
-  for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
-    loff[u] = dma_v ? dma_lane_off<D, true>(u, vstride, lane) : dma_lane_off<D, false>(u, kstride, lane);
+    for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
+      loff[u] = dma_v ? dma_lane_off<D, true>(u, vstride, lane) : dma_lane_off<D, false>(u, kstride, lane);
+  }
+  // Contiguous K/V: this wave's half (K or V), its row stride and LDS offset,
+  // chosen once.  With a row stride of at least D a unit's LPU loads take one
+  // scalar row base and one M0 (dma_rows): load i reads i KB past the base by
+  // its immediate offset plus the rest of its global step (RPL rows) by its
+  // lane offset doff[i]; smaller strides take the clamped per-lane path.
+  constexpr int DRPL = 64 / (D / 8);  // key rows per 1 KB load
+  const T* dbase = dma_v ? vbase : kbase;
+  const int64_t dstride = dma_v ? vstride : kstride;
+  const uint32_t dlds = dma_v ? (uint32_t)HALF : 0u;
+  const bool rows_fast = __builtin_amdgcn_readfirstlane(dstride >= D ? 1 : 0) != 0;
+  uint32_t doff[LPU];
+#pragma unroll
+  for (int i = 0; i < LPU; ++i)
+    doff[i] = (dma_v ? dma_lane_off<D, true>(dma_u0 + i, dstride, lane)
+                     : dma_lane_off<D, false>(dma_u0 + i, dstride, lane)) +
+              (uint32_t)((int64_t)i * (DRPL * dstride * 2 - 1024));
 
   // Paged: the raw page-table entries of the next unit this wave issues,
   // read one step early (prefetch) so their scalar loads land behind the
@@ -469,8 +601,7 @@ void split_kernel(const SplitArgs a) {
   // HBM -> LDS: this wave's share of one unit (keys key0 .. key0+31) into
   // stage st of its stream's ring.
   const bool kv_nt = __builtin_amdgcn_readfirstlane(a.kv_nt) != 0;
-  auto issue = [&](int st, int key0) {
-    const uint32_t sb = sring_lds + st * SB;
+  auto issue_at = [&](uint32_t sb, int key0) {
     if (PAGED) {
       int pg0, pg1;
       share_pages<D, LPU>(a, key0, dma_u0, pg0, pg1);
@@ -484,17 +615,18 @@ void split_kernel(const SplitArgs a) {
         dma_half_paged<T, D, true, LPU, C32>(vbase, a, pid0, pid1, pg0, sb + HALF, key0, lane, dma_u0, loff, kv_nt);
       else
         dma_half_paged<T, D, false, LPU, C32>(kbase, a, pid0, pid1, pg0, sb, key0, lane, dma_u0, loff, kv_nt);
-    } else if (kv_nt) {
-      if (dma_v)
-        dma_half<T, D, true, LPU, false, true>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
-      else
-        dma_half<T, D, false, LPU, false, true>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
+    } else if (rows_fast && key0 + kUnitKeys <= a.kv_len) {
+      const char* rowp = reinterpret_cast<const char*>(dbase + (int64_t)(key0 + dma_u0 * DRPL) * dstride);
+      const uint32_t m0v = sb + dlds + dma_u0 * 1024;
+      if (kv_nt) dma_rows<LPU, true>(rowp, doff, m0v);
+      else dma_rows<LPU, false>(rowp, doff, m0v);
     } else if (dma_v) {
-      dma_half<T, D, true, LPU>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
+      dma_tail<T, D, true, LPU>(dbase, dstride, sb + HALF, key0, a.kv_len, lane, dma_u0);
     } else {
-      dma_half<T, D, false, LPU>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
+      dma_tail<T, D, false, LPU>(dbase, dstride, sb, key0, a.kv_len, lane, dma_u0);
     }
   };
+  auto issue = [&](int st, int key0) { issue_at(sring_lds + st * SB, key0); };
 
   // Q^T operand fragments of the wave's row tile: row r = row0 + rg*32 + ln,
   // d = kk*16 + lh*8 + [0, 8); Q is negated for a negative scale.
@@ -525,7 +657,10 @@ void split_kernel(const SplitArgs a) {
   // stream), as global_load_lds issued ahead of the first K/V units, so the
   // prologue need not wait for Q before filling the ring.  Rows past the end
   // repeat the last row (their outputs are never stored).
-  auto issue_q = [&]() {
+  // Q stage of the stream holding chunk rows [s*QROWS, (s+1)*QROWS): the last
+  // QS stages of its ring, or stage NOS - S + s in one-shot runs.
+  auto q_stage = [&](int s, bool os) { return os ? ring + (NOS - S + s) * SB : ring + s * RB + (NS - QS) * SB; };
+  auto issue_q = [&](bool os) {
     constexpr int RPL = 1024 / ROWB, CPR = D / 8;
     constexpr int QL = ROWS / RPL / kWaves;  // 1 KB loads per wave
 #pragma unroll
@@ -537,12 +672,11 @@ void split_kernel(const SplitArgs a) {
       const int g = R - t * G;
       const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
                      ((pos ^ swz_k<D>(tr)) << 3);
-      dma16(src, __builtin_amdgcn_readfirstlane(
-                     lds_addr(ring + (l0 / QROWS) * RB + (NS - QS) * SB + (l0 % QROWS) * ROWB)));
+      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(q_stage(l0 / QROWS, os) + (l0 % QROWS) * ROWB)));
     }
   };
-  auto read_q = [&]() {
-    const unsigned char* qs = ring + (rg * 32 / QROWS) * RB + (NS - QS) * SB + ((rg * 32) % QROWS) * ROWB;
+  auto read_q = [&](bool os) {
+    const unsigned char* qs = q_stage(rg * 32 / QROWS, os) + ((rg * 32) % QROWS) * ROWB;
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
       qf[kk] = *reinterpret_cast<const i16x8*>(qs + ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4)) ^ qsgn;
@@ -558,28 +692,27 @@ void split_kernel(const SplitArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
 
-  // LDS byte offsets of this lane's operand reads (the chunk XOR does not
-  // commute with the d offset, so one per d-tile / k-step; loop invariant).
+  // LDS byte offsets of this lane's operand reads within a stage.
   // V^T: 16-lane group x = (h, d-half); lane i of the group reads 8 bytes of
   // key row 4*h + i/4 (+16*s2 + 8*jj, which keeps the swizzle) at d = dt*32 +
   // 16*(x&1) + 4*(i%4); the transpose read hands lane i keys +[0,4) of d = i.
   // K: lane (ln, lh) reads 16 bytes of key row ln at d = kk*16 + 8*lh.
+  // The chunk XOR swizzles only move offset bits 5-7 (K, per k-step) and 6-7
+  // (V^T, per d-tile), so k-step kk reads at k_off0 ^ (kk << 5) and d-tile dt
+  // at v_off0 ^ (dt << 6); stage bases are multiples of 4 KB, so the XOR
+  // commutes with adding them (one base register per operand instead of one
+  // per k-step / d-tile).
   const int vx = lane >> 4, vi = lane & 15;
   const int vkey = 4 * (vx >> 1) + (vi >> 2);
-  int v_off[DT], k_off[KSTEPS];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
-    v_off[dt] = vkey * ROWB + (((d >> 3) ^ swz_v<D>(vkey)) << 4) + ((d & 7) << 1);
-  }
-#pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) k_off[kk] = ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4);
+  const int v_off0 = vkey * ROWB + ((((16 * (vx & 1) + 4 * (vi & 3)) >> 3) ^ swz_v<D>(vkey)) << 4) + ((4 * (vi & 3) & 7) << 1);
+  const int k_off0 = ln * ROWB + ((lh ^ swz_k<D>(ln)) << 4);
 
   // S^T of one 32-key unit for the wave's 32 rows: MFMA row m = key, column =
   // query row; lane (ln, lh) holds keys 8*(i/4) + 4*lh + i%4 of row ln.
   auto read_k = [&](const unsigned char* sk, i16x8 (&kf)[KSTEPS]) {
+    const int base = (int)(sk - smem) + k_off0;
 #pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) kf[kk] = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
+    for (int kk = 0; kk < KSTEPS; ++kk) kf[kk] = *reinterpret_cast<const i16x8*>(smem + (base ^ (kk << 5)));
   };
   auto qk = [&](const i16x8 (&kf)[KSTEPS]) {
     f32x16 s;
@@ -593,14 +726,15 @@ void split_kernel(const SplitArgs a) {
   // V^T fragments of one unit (stage base sv): lane i of 16-lane group x gets
   // keys 16*s2 + 8*jj + 4*(x>>1) + [0,4) of d = dt*32 + 16*(x&1) + i.
   auto read_v = [&](const unsigned char* sv, i16x4 (&vh)[DT][2][2]) {
+    const int base = (int)(sv - smem) + v_off0;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
-          vh[dt][s2][jj] =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(sv + v_off[dt] + (16 * s2 + 8 * jj) * ROWB));
+          vh[dt][s2][jj] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (TSFA_LDS i16x4*)(smem + (base ^ (dt << 6)) + (16 * s2 + 8 * jj) * ROWB));
   };
   // Online softmax of one unit's S^T (VALU only): masks the unit's invisible
   // keys, re-bases (m, l, O) when the running max grows past the lazy
@@ -719,6 +853,195 @@ void split_kernel(const SplitArgs a) {
       }
     }
   };
+  // ---- software-pipelined unit loop (PIPE) ----
+  // Iteration j of a wave: the mask and row statistics of unit j (whose S^T
+  // the previous iteration computed), then group 1 -- the S^T MFMAs of unit
+  // j+1 with the exponentials and rounded P of unit j between them -- then
+  // the rare O re-base, then group 2 -- O^T += V^T P^T of unit j with the row
+  // sum of unit j between them.  A wave keeps its own matrix core busy while
+  // its softmax runs, and every VALU read of an MFMA result (S^T by the mask
+  // and statistics, O^T by the re-base) happens an MFMA group and a barrier
+  // after the MFMAs that wrote it.  The running max moves without a branch
+  // (a re-based row takes the unit's row max and scales l at once).  The ring
+  // is used as by run_units: iteration j reads K of unit j+1 and V of unit j
+  // after barrier j.
+  auto apply_mask = [&](f32x16& s, uint32_t mask) {
+    const uint32_t w = mask >> (4 * lh);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (!((w >> (8 * (i >> 2) + (i & 3))) & 1u)) s[i] = -INFINITY;
+  };
+  // Row statistics of one unit's S^T (tree_sparse_flashattn.py:272-276,
+  // :320-324): returns whether the row re-based; alpha scales O and l.
+  auto stats = [&](const f32x16& s, float& alpha) {
+    const float mx = max3f(max3f(max3f(s[0], s[1], s[2]), max3f(s[3], s[4], s[5]), max3f(s[6], s[7], s[8])),
+                           max3f(max3f(s[9], s[10], s[11]), max3f(s[12], s[13], s[14]), s[15]), -INFINITY);
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    const float rmax = max3f(__uint_as_float(sw[0]), __uint_as_float(sw[1]), -INFINITY);
+    // rmax > m_lim >= m_run, so a re-based row takes rmax; false while both are -inf
+    const bool need = rmax > m_lim;
+    const float m_new = need ? rmax : m_run;
+    // m_run = -inf gives alpha = 0 (O and l are still 0) (tree_sparse_flashattn.py:276, :324)
+    alpha = need ? __builtin_amdgcn_exp2f((m_run - m_new) * sl2) : 1.f;
+    m_run = m_new;
+    mb = (m_new == -INFINITY) ? 0.f : m_new * sl2;
+    m_lim = m_new + thr_raw;
+    l_run *= alpha;
+    return need;
+  };
+  // Unit j of the stream (u: its index in the run; s_in: its S^T; s_out:
+  // S^T of unit j+1 when NEXT): mask and statistics, group 1 when NEXT (the
+  // S^T MFMAs of unit j+1 with the exponentials and rounded P of unit j
+  // between them), the O re-base, group 2 (O^T += V^T P^T of unit j, V^T read
+  // two MFMAs ahead, the row sum between them).
+  auto pipe_iter = [&](int j, int u, auto next_c, f32x16& s_in, f32x16& s_out, auto masked_of, auto mask_of) {
+    constexpr bool NEXT = decltype(next_c)::value;
+    constexpr int NPV = 2 * DT;  // P V MFMAs
+    i16x4 vh[DT][2][2];
+    float p[16];
+    V8 pb[2];
+    const uint32_t vb = stage(j) + (uint32_t)(HALF + v_off0);
+    auto rv = [&](int idx) {  // V^T fragment idx = (dt, s2, jj); P V MFMA g reads 2g and 2g+1
+      const int dt = idx >> 2, s2 = (idx >> 1) & 1, jj = idx & 1;
+      vh[dt][s2][jj] = lds_tr((vb ^ (uint32_t)(dt << 6)) + (uint32_t)((16 * s2 + 8 * jj) * ROWB));
+    };
+    if (masked_of(u)) {
+      asm volatile("" ::: "memory");
+      apply_mask(s_in, mask_of(u));
+    }
+    float alpha;
+    const bool need = stats(s_in, alpha);
+    // exponential, rounding and register pin of the pair (e, e+1) of unit j
+    auto expo2 = [&](int e) {
+      p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_in[e], sl2, -mb));
+      p[e + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(s_in[e + 1], sl2, -mb));
+      pb[e >> 3][e & 7] = (T)p[e];
+      pb[e >> 3][(e & 7) + 1] = (T)p[e + 1];
+    };
+    if constexpr (NEXT) {
+      // group 1 in explicit order: K of unit j+1 read two k-steps ahead of
+      // its MFMAs; the statistics above and then the exponentials and
+      // rounded P of unit j between the MFMAs; V^T of the first two P V
+      // MFMAs at the end
+      const uint32_t kb = stage(j + 1) + (uint32_t)k_off0;
+      auto rk = [&](int kk) { return lds_ld<i16x8>(kb ^ (uint32_t)(kk << 5)); };
+      i16x8 kf[KSTEPS];
+      kf[0] = rk(0);
+      kf[1] = rk(1);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_out[i] = 0.f;
+      constexpr int K0 = KSTEPS / 4;  // steps that carry the statistics; the 8 exponential pairs spread over the rest
+#pragma unroll
+      for (int kk = 0; kk < KSTEPS; ++kk) {
+        if (kk + 2 < KSTEPS) kf[kk + 2] = rk(kk + 2);
+        s_out = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[kk]), s_out);
+        if (kk >= K0) {
+#pragma unroll
+          for (int pr = (kk - K0) * 8 / (KSTEPS - K0); pr < (kk - K0 + 1) * 8 / (KSTEPS - K0); ++pr) expo2(2 * pr);
+        }
+        if (kk == KSTEPS - 1)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rv(r);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // P exists here: the exponentials and conversions stay in group 1 (its
+      // block ends at the mask branch) instead of sinking into group 2
+      asm volatile("" : "+v"(pb[0]), "+v"(pb[1]));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rv(r);
+#pragma unroll
+      for (int pr = 0; pr < 8; ++pr) expo2(2 * pr);
+    }
+    // O re-base for unit j: after P V of unit j-1 (issued an iteration ago),
+    // before that of unit j
+    if (__ballot(need) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+    // group 2 in explicit order: MFMA g with V^T of MFMA g+2 read behind it
+    // and a share of the row sum of unit j
+#pragma unroll
+    for (int g = 0; g < NPV; ++g) {
+      if (2 * (g + 2) < 4 * DT) {
+        rv(2 * (g + 2));
+        rv(2 * (g + 2) + 1);
+      }
+      const int dt = g >> 1, s2 = g & 1;
+      const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
+      o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
+      // tree sum of p: 8 + 4 + 2 + 1 adds spread over the MFMAs
+      if (g == 0)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = p[i] + p[i + 8];
+      if (g == 1)
+#pragma unroll
+        for (int i = 4; i < 8; ++i) p[i] = p[i] + p[i + 8];
+      if (g == 2)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = p[i] + p[i + 4];
+      if (g == 3) {
+        p[0] = p[0] + p[2];
+        p[1] = p[1] + p[3];
+        l_run += p[0] + p[1];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
+    const int mine = n > ks ? (n - ks + S - 1) / S : 0;
+    const int steps = (n + S - 1) / S;
+    if (oneshot) {
+      // units [0, pre) requested with Q; the rest go into Q's stages once
+      // every wave has read Q (the barrier below)
+      if (mine > 0) wait_units<LPU, NOS - S>(pre - 1);  // unit 0 landed
+      sync_lds();
+      for (int j = pre; j < mine; ++j) issue_at(stage(j), key0_of(ks + S * j));
+    } else {
+      for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + S * j));
+      if (PAGED && NS - 1 < mine) prefetch(key0_of(ks + S * (NS - 1)));
+      if (mine > 0) wait_units<LPU, NS - 2>(min(mine - 1, NS - 2));  // unit 0 landed
+      sync_lds();
+    }
+    TSFA_STAMP(2);
+    f32x16 s_cur, s_next;  // S^T of unit j and of unit j+1
+    if (mine > 0 && active) {
+      i16x8 kf[KSTEPS];
+      read_k(ring + (stage(0) - ring_lds), kf);
+      s_cur = qk(kf);
+    }
+    // unit j+1 landed for every wave of the stream; ring stage (j-1)%NS is free
+    auto ring_step = [&](int j) {
+      if (j + 1 < mine) {
+        if (oneshot) wait_units<LPU, NOS - S>(mine - 2 - j);
+        else wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      sync_lds();
+      __builtin_amdgcn_sched_barrier(0);
+      if (j < 40) TSFA_STAMP(3 + j);
+      if (!oneshot && j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+      if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // (unrolling by two to alternate the S^T registers instead of copying
+    // them made the allocator shuffle the O accumulators: 281 copies)
+    for (int j = 0; j < steps; ++j) {
+      ring_step(j);
+      if (j + 1 < mine && active) {
+        pipe_iter(j, ks + S * j, std::true_type{}, s_cur, s_next, masked_of, mask_of);
+        s_cur = s_next;
+      }
+    }
+    // The stream's last unit: its V^T stage landed before barrier mine-2 and
+    // no later load targets it (a load into it would be of unit >= mine).
+    if (mine > 0 && active) pipe_iter(mine - 1, ks + S * (mine - 1), std::false_type{}, s_cur, s_cur, masked_of, mask_of);
+  };
+  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
+    if constexpr (PIPE) run_units_pipe(n, pre, key0_of, masked_of, mask_of);
+    else run_units(n, pre, key0_of, masked_of, mask_of);
+  };
+
   if (!is_tree) {
     // Prefix run: units [u_lo, u_lo + n) of keys [0, prefix_len); the last
     // unit of the prefix may be partial.
@@ -730,16 +1053,39 @@ void split_kernel(const SplitArgs a) {
     // only (loads complete in order), then every wave reads its fragments.
     // With QS > 1 the ring prologue reuses Q stages: one more barrier first.
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
-    const int pre = min(mine, NS - QS);
-    issue_q();
-    for (int j = 0; j < pre; ++j) issue(j, key0_of(ks + S * j));
-    wait_units<LPU, NS - QS>(pre);
-    sync_lds();
-    read_q();
-    if (QS > 1) sync_lds();
-    run_units(
+    int pre;
+    if (PIPE && !PAGED && n <= NOS) {
+      // one-shot: Q in the last S stages, run units below NOS - S with it
+      oneshot = true;
+      st_base = ring_lds + ks * SB;
+      st_step = S * SB;
+      st_mask = 31;
+      const int early = min(n, NOS - S);
+      pre = early > ks ? (early - ks + S - 1) / S : 0;
+      issue_q(true);
+      for (int j = 0; j < pre; ++j) issue_at(stage(j), key0_of(ks + S * j));
+      wait_units<LPU, NOS - S>(pre);
+      sync_lds();
+      TSFA_STAMP(1);
+      read_q(true);
+    } else {
+      pre = min(mine, NS - QS);
+      issue_q(false);
+      for (int j = 0; j < pre; ++j) issue(j, key0_of(ks + S * j));
+      wait_units<LPU, NS - QS>(pre);
+      sync_lds();
+      TSFA_STAMP(1);
+      read_q(false);
+      if (QS > 1) sync_lds();
+    }
+    units(
         n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; });
+    // a folded tree phase runs on the rings
+    oneshot = false;
+    st_base = sring_lds;
+    st_step = SB;
+    st_mask = NS - 1;
   }
   if (do_tree) {
     // after a prefix run: its ring reads and loads done (the block states
@@ -826,7 +1172,7 @@ void split_kernel(const SplitArgs a) {
         reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
       }
       sync_lds();
-      run_units(
+      units(
           nb, 0, [&](int i) { return P + vis[vb0 + i] * kUnitKeys; }, [&](int) { return true; },
           [&](int i) { return masks[row_tt * a.vt_max + i]; });
       sync_all();  // ring and masks free for the next batch
@@ -838,6 +1184,7 @@ void split_kernel(const SplitArgs a) {
   // owner normalises and stages the row in the input dtype; then all waves
   // store whole rows (1 KB per instruction).
   sync_all();
+  TSFA_STAMP(50);
   float2* mls = reinterpret_cast<float2*>(masks);                   // [row group][32]
   unsigned char* stg = ring + (S == 2 ? kRingBytes - ROWS * ROWB : 0);  // [ROWS][D], chunks swizzled
   if (S == 2 && ks == 1) {
@@ -911,6 +1258,7 @@ void split_kernel(const SplitArgs a) {
     const int idx = tid + it * kWaves * 64, r = idx / CPR, c = idx % CPR;
     if (r < rows_chunk) *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) = rowv[it];
   }
+  TSFA_STAMP(51);
 }
 
 // ------------------------------------------------------------- wide kernel
@@ -1637,7 +1985,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   return TSFA_OK;
 }
 
-template <typename T, int D, int S, bool PAGED, bool C32 = false>
+template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -1646,12 +1994,13 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32, PIPE>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream, args);
+  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32, PIPE>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream,
+                     args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -1680,13 +2029,17 @@ template <typename T, int D, bool PAGED>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
     int st;
+    const bool pipe = env_int("TSFA_PIPE", 1) != 0;
     if constexpr (PAGED)
-      st = (sa.cache32 && p.streams == 2) ? launch_split<T, D, 2, true, true>(sa, p, stream)
-           : p.streams == 2               ? launch_split<T, D, 2, true>(sa, p, stream)
-                                          : launch_split<T, D, 1, true>(sa, p, stream);
+      st = (sa.cache32 && p.streams == 2) ? (pipe ? launch_split<T, D, 2, true, true, true>(sa, p, stream)
+                                                  : launch_split<T, D, 2, true, true>(sa, p, stream))
+           : p.streams == 2 ? (pipe ? launch_split<T, D, 2, true, false, true>(sa, p, stream)
+                                    : launch_split<T, D, 2, true>(sa, p, stream))
+                            : launch_split<T, D, 1, true>(sa, p, stream);
     else
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
-           : p.streams == 2   ? launch_split<T, D, 2, false>(sa, p, stream)
+           : p.streams == 2   ? (pipe ? launch_split<T, D, 2, false, false, true>(sa, p, stream)
+                                      : launch_split<T, D, 2, false>(sa, p, stream))
                               : launch_split<T, D, 1, false>(sa, p, stream);
     if (st != TSFA_OK) return st;
   }
@@ -2036,3 +2389,9 @@ extern "C" int tsfa_fwd_set_kernel_mask(int mask) {
   g_kernel_mask = mask;
   return TSFA_OK;
 }
+
+#ifdef TSFA_STAMPS
+extern "C" int tsfa_stamps_copy(void* dst, size_t bytes) {
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 4;
+}
+#endif
