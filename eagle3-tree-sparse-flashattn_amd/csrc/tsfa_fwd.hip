@@ -74,9 +74,31 @@ __device__ unsigned long long g_stamps[4096 * 64];
   do {                                                                                     \
     if (threadIdx.x == 0) g_stamps[(size_t)blockIdx.x * 64 + (k)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
+// Per-wave cycle sums of loop phases (s_memtime deltas; each reading waits
+// for the wave's outstanding LDS/scalar loads, so this build perturbs the loop).
+__device__ unsigned long long g_cyc[4096 * 32];
+#define TSFA_CYC_DECL unsigned long long cyc_prev = __builtin_amdgcn_s_memtime(), cyc_acc[4] = {0, 0, 0, 0};
+#define TSFA_CYC(k)                                              \
+  do {                                                           \
+    const unsigned long long cyc_now = __builtin_amdgcn_s_memtime(); \
+    cyc_acc[k] += cyc_now - cyc_prev;                            \
+    cyc_prev = cyc_now;                                          \
+  } while (0)
+#define TSFA_CYC_STORE                                                                         \
+  do {                                                                                         \
+    if ((threadIdx.x & 63) == 0)                                                               \
+      for (int k_ = 0; k_ < 4; ++k_) g_cyc[(size_t)blockIdx.x * 32 + (threadIdx.x >> 6) * 4 + k_] = cyc_acc[k_]; \
+  } while (0)
 #else
 #define TSFA_STAMP(k) \
   do {            \
+  } while (0)
+#define TSFA_CYC_DECL
+#define TSFA_CYC(k) \
+  do {          \
+  } while (0)
+#define TSFA_CYC_STORE \
+  do {             \
   } while (0)
 #endif
 
@@ -109,6 +131,8 @@ struct SplitArgs {
   int neg_q;         // sm_scale < 0: Q enters negated (scores keep their sign)
   int num_kv_heads, group, q_len, kv_len, prefix_len, block_m, block_n, n_tree_blocks;
   int n_chunks, units_per_split, n_pu, n_slots, n_items, items_per_xcd;
+  FastDiv fd_chunks, fd_slots, fd_kvh, fd_group;  // n_chunks, n_slots, num_kv_heads, group
+  FastDiv fd_P, fd_Np, fd_Nt;                     // item order: n_chunks*n_slots, its prefix and tree items
   int tree_key_limit;  // min(n_tree_blocks*BN, kv_len - prefix_len)
   int vt_max;          // tree units per mask batch
   void* ws_o;          // [B*Hkv][n_slots][q_len*G][D] partial O / l in the input dtype
@@ -126,6 +150,8 @@ struct SplitArgs {
   uint32_t cps_b32, crs_b32;  // its page and row strides in bytes
   int item_order;  // within an XCD: 0 natural, 1 prefix runs first, 2 tree items first
   int fold_tree;   // no tree items: the last prefix split of each chunk also runs the tree units
+  int os_first;    // one-shot prefix runs: run units requested with Q (the rest once Q landed)
+  int rot_step;    // prefix run of chunk c starts at its unit (c * rot_step) mod n and wraps
 };
 
 
@@ -148,14 +174,26 @@ template <int D> __device__ inline int swz_v(int key) { return D == 128 ? ((key 
 // the L2).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; the clobber documents the write
-__device__ inline void dma16(const void* src, uint32_t lds_base) {
+__device__ inline void dma16(const void* src, uint32_t lds_in) {
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_in);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
                : "v"(src), "s"(lds_base)
                : "memory", "m0");
 }
+// A wave-uniform pointer stated as such to the compiler: the "s" operand of
+// the loads below must be an SGPR pair, and a base it cannot prove uniform
+// would otherwise be handed over in VGPRs (rejected by the assembler).
+__device__ inline const void* uniform_ptr(const void* p) {
+  const uint64_t u = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
 template <bool NT = false>
-__device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+__device__ inline void dma16_s(const void* sbase_in, uint32_t voff, uint32_t lds_in) {
+  const void* sbase = uniform_ptr(sbase_in);
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_in);
   if constexpr (NT)
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt"
                  :
@@ -172,8 +210,10 @@ __device__ inline void dma16_s(const void* sbase, uint32_t voff, uint32_t lds_ba
 // instruction's immediate offset applies to the LDS address as well as the
 // global one (checked on gfx950), so consecutive LDS KBs need no M0 update.
 template <int N, bool NT>
-__device__ inline void dma_rows(const void* sbase, const uint32_t (&off)[N], uint32_t m0v) {
+__device__ inline void dma_rows(const void* sbase_in, const uint32_t (&off)[N], uint32_t m0v_in) {
   static_assert(N == 4 || N == 2 || N == 1, "loads per wave and unit");
+  const void* sbase = uniform_ptr(sbase_in);
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(m0v_in);
   if constexpr (N == 1 && NT)
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %2 nt"
                  :
@@ -460,9 +500,9 @@ __device__ inline int work_item(const SplitArgs& a) {
   if (lo + j >= hi) return -1;
   if (a.n_slots < 2 || a.item_order == 0) return lo + j;
   const int P = a.n_chunks * a.n_slots, Nt = a.n_chunks, Np = P - Nt;
-  auto before = [&](int i) { return (i / P) * Np + min(i % P, Np); };  // prefix items before item i
-  auto kth_prefix = [&](int k) { return (k / Np) * P + k % Np; };
-  auto kth_tree = [&](int k) { return (k / Nt) * P + Np + k % Nt; };
+  auto before = [&](int i) { return (int)fdiv(i, a.fd_P) * Np + min((int)frem(i, a.fd_P), Np); };  // prefix items before item i
+  auto kth_prefix = [&](int k) { return (int)fdiv(k, a.fd_Np) * P + (int)frem(k, a.fd_Np); };
+  auto kth_tree = [&](int k) { return (int)fdiv(k, a.fd_Nt) * P + Np + (int)frem(k, a.fd_Nt); };
   const int plo = before(lo), np = before(hi) - plo, nt = hi - lo - np;
   if (a.item_order == 2) return j < nt ? kth_tree(lo - plo + j) : kth_prefix(plo + j - nt);
   return j < np ? kth_prefix(plo + j) : kth_tree(lo - plo + j - np);
@@ -512,11 +552,12 @@ void split_kernel(const SplitArgs a) {
 #ifdef TSFA_STAMPS
   if (threadIdx.x == 0) g_stamps[(size_t)blockIdx.x * 64 + 63] = (unsigned long long)item;
 #endif
-  const int chunk = item % a.n_chunks;
-  int rest = item / a.n_chunks;
-  const int slot = rest % a.n_slots;
-  const int bk = rest / a.n_slots;
-  const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
+  const int rest = fdiv(item, a.fd_chunks);
+  const int chunk = item - rest * a.n_chunks;
+  const int bk = fdiv(rest, a.fd_slots);
+  const int slot = rest - bk * a.n_slots;
+  const int b = fdiv(bk, a.fd_kvh);
+  const int kvh = bk - b * a.num_kv_heads;
   // roles: a prefix run (slots below n_slots - 1), the tree units (the last
   // slot), or with fold_tree both in the last slot
   const bool is_tree = !a.fold_tree && slot == a.n_slots - 1;
@@ -527,7 +568,7 @@ void split_kernel(const SplitArgs a) {
   const int row0 = chunk * ROWS;
   const int rows_chunk = min(ROWS, TG - row0);
   const bool active = rg * 32 < rows_chunk;
-  const int tok_lo = row0 / G;
+  const int tok_lo = (int)fdiv(row0, a.fd_group);
   const float sl2 = a.scale_log2;
   const float thr_raw = kRescaleLog2 / sl2;  // re-base the running max past 2^8 growth
 
@@ -555,6 +596,7 @@ void split_kernel(const SplitArgs a) {
   uint32_t st_base = sring_lds, st_step = SB;
   int st_mask = NS - 1;
   auto stage = [&](int j) { return st_base + (uint32_t)((j & st_mask) * st_step); };
+  TSFA_CYC_DECL
 
   // The stream's RG waves move equal shares of each unit: the first half of
   // them K, the second half V.
@@ -632,14 +674,14 @@ void split_kernel(const SplitArgs a) {
   // d = kk*16 + lh*8 + [0, 8); Q is negated for a negative scale.
   i16x8 qf[KSTEPS];
   const int qrow = row0 + rg * 32 + ln;
-  const int row_tt = qrow < TG ? qrow / G - tok_lo : 0;  // token of the lane's row, chunk-relative
+  const int row_tt = qrow < TG ? (int)fdiv(qrow, a.fd_group) - tok_lo : 0;  // token of the lane's row, chunk-relative
   const short qsgn = a.neg_q ? (short)0x8000 : (short)0;
   // Q straight into registers (rows past the end load zeros).
   auto load_q = [&]() {
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk) qf[kk] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     if (qrow < TG) {
-      const int t = qrow / G;
+      const int t = (int)fdiv(qrow, a.fd_group);
       const int g = qrow - t * G;
       const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
                     lh * 8;
@@ -668,7 +710,7 @@ void split_kernel(const SplitArgs a) {
       const int l0 = (wave * QL + i) * RPL;  // first chunk row of the load
       const int row = l0 + lane / CPR, pos = lane % CPR, tr = row % QROWS;
       const int R = min(row0 + row, TG - 1);
-      const int t = R / G;
+      const int t = (int)fdiv(R, a.fd_group);
       const int g = R - t * G;
       const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
                      ((pos ^ swz_k<D>(tr)) << 3);
@@ -947,6 +989,7 @@ void split_kernel(const SplitArgs a) {
       // P exists here: the exponentials and conversions stay in group 1 (its
       // block ends at the mask branch) instead of sinking into group 2
       asm volatile("" : "+v"(pb[0]), "+v"(pb[1]));
+      TSFA_CYC(0);
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) rv(r);
@@ -959,6 +1002,7 @@ void split_kernel(const SplitArgs a) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
+    if constexpr (NEXT) TSFA_CYC(3);
     // group 2 in explicit order: MFMA g with V^T of MFMA g+2 read behind it
     // and a share of the row sum of unit j
 #pragma unroll
@@ -987,6 +1031,7 @@ void split_kernel(const SplitArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (NEXT) TSFA_CYC(1);
   };
   auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
@@ -1020,6 +1065,7 @@ void split_kernel(const SplitArgs a) {
       sync_lds();
       __builtin_amdgcn_sched_barrier(0);
       if (j < 40) TSFA_STAMP(3 + j);
+      TSFA_CYC(2);
       if (!oneshot && j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
       if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
       __builtin_amdgcn_sched_barrier(0);
@@ -1048,23 +1094,31 @@ void split_kernel(const SplitArgs a) {
     const int P = a.prefix_len;
     const int u_lo = slot * a.units_per_split;
     const int n = min(a.units_per_split, a.n_pu - u_lo);
-    auto key0_of = [&](int i) { return (u_lo + i) * kUnitKeys; };
+    // The row chunks of one split read its units in rotated orders, so that
+    // they do not all request the same K/V lines at the same time.
+    const int rot = n > 0 ? (int)((uint32_t)(chunk * a.rot_step) % (uint32_t)n) : 0;
+    auto key0_of = [&](int i) {
+      const int r = i + rot;
+      return (u_lo + (r >= n ? r - n : r)) * kUnitKeys;
+    };
     // Q and the first NS-QS units of each stream leave together; wait for Q
     // only (loads complete in order), then every wave reads its fragments.
     // With QS > 1 the ring prologue reuses Q stages: one more barrier first.
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     int pre;
-    if (PIPE && !PAGED && n <= NOS) {
+    if (PIPE && !PAGED && S == 2 && n <= NOS) {
       // one-shot: Q in the last S stages, run units below NOS - S with it
       oneshot = true;
       st_base = ring_lds + ks * SB;
       st_step = S * SB;
       st_mask = 31;
-      const int early = min(n, NOS - S);
+      const int early = min(n, NOS - S), first = min(early, max(a.os_first, S));
       pre = early > ks ? (early - ks + S - 1) / S : 0;
+      const int pre1 = first > ks ? (first - ks + S - 1) / S : 0;
       issue_q(true);
-      for (int j = 0; j < pre; ++j) issue_at(stage(j), key0_of(ks + S * j));
-      wait_units<LPU, NOS - S>(pre);
+      for (int j = 0; j < pre1; ++j) issue_at(stage(j), key0_of(ks + S * j));
+      wait_units<LPU, NOS - S>(pre1);
+      for (int j = pre1; j < pre; ++j) issue_at(stage(j), key0_of(ks + S * j));
       sync_lds();
       TSFA_STAMP(1);
       read_q(true);
@@ -1093,7 +1147,7 @@ void split_kernel(const SplitArgs a) {
     if (is_tree) load_q();
     else sync_all();
     const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-    const int tok_hi = (row0 + rows_chunk - 1) / G;  // tokens tok_lo .. tok_hi
+    const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
     const int ntok = tok_hi - tok_lo + 1;
     const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
     const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
@@ -1259,6 +1313,7 @@ void split_kernel(const SplitArgs a) {
     if (r < rows_chunk) *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) = rowv[it];
   }
   TSFA_STAMP(51);
+  TSFA_CYC_STORE;
 }
 
 // ------------------------------------------------------------- wide kernel
@@ -1313,11 +1368,12 @@ void wide_kernel(const SplitArgs a) {
 
   const int item = work_item(a);
   if (item < 0) return;
-  const int chunk = item % a.n_chunks;
-  int rest = item / a.n_chunks;
-  const int slot = rest % a.n_slots;
-  const int bk = rest / a.n_slots;
-  const int kvh = bk % a.num_kv_heads, b = bk / a.num_kv_heads;
+  const int rest = fdiv(item, a.fd_chunks);
+  const int chunk = item - rest * a.n_chunks;
+  const int bk = fdiv(rest, a.fd_slots);
+  const int slot = rest - bk * a.n_slots;
+  const int b = fdiv(bk, a.fd_kvh);
+  const int kvh = bk - b * a.num_kv_heads;
   const bool is_tree = !a.fold_tree && slot == a.n_slots - 1;  // as in split_kernel
   const bool do_tree = slot == a.n_slots - 1;
 
@@ -1325,7 +1381,7 @@ void wide_kernel(const SplitArgs a) {
   const int TG = a.q_len * G;
   const int row0 = chunk * ROWS;
   const int rows_chunk = min(ROWS, TG - row0);
-  const int tok_lo = row0 / G;
+  const int tok_lo = (int)fdiv(row0, a.fd_group);
   const float sl2 = a.scale_log2;
   const float thr_raw = kRescaleLog2 / sl2;
 
@@ -1356,7 +1412,7 @@ void wide_kernel(const SplitArgs a) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int qrow = row0 + wave * 64 + t * 32 + ln;
-    row_tt[t] = qrow < TG ? qrow / G - tok_lo : 0;
+    row_tt[t] = qrow < TG ? (int)fdiv(qrow, a.fd_group) - tok_lo : 0;
   }
   auto load_q = [&]() {  // straight into registers (rows past the end load zeros)
 #pragma unroll
@@ -1365,7 +1421,7 @@ void wide_kernel(const SplitArgs a) {
       for (int kk = 0; kk < KSTEPS; ++kk) qf[t][kk] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
       const int qrow = row0 + wave * 64 + t * 32 + ln;
       if (qrow < TG) {
-        const int tq = qrow / G;
+        const int tq = (int)fdiv(qrow, a.fd_group);
         const int g = qrow - tq * G;
         const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh +
                       (int64_t)tq * a.sqm + lh * 8;
@@ -1390,7 +1446,7 @@ void wide_kernel(const SplitArgs a) {
       const int l0 = (wave * QL + i) * RPL;
       const int row = l0 + lane / CPR, pos = lane % CPR;
       const int R = min(row0 + row, TG - 1);
-      const int tq = R / G;
+      const int tq = (int)fdiv(R, a.fd_group);
       const int g = R - tq * G;
       const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)tq * a.sqm +
                      ((pos ^ swz_k<D>(row)) << 3);
@@ -1662,7 +1718,7 @@ void wide_kernel(const SplitArgs a) {
     if (is_tree) load_q();
     else sync_all();  // the prefix run's ring reads and loads done; Q stays in registers
     const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-    const int tok_hi = (row0 + rows_chunk - 1) / G;
+    const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);
     const int ntok = tok_hi - tok_lo + 1;
     const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
     const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
@@ -1889,25 +1945,24 @@ int64_t chunk_tokens(int rows, int group) { return (int64_t)(rows - 1) / group +
 int64_t chunk_qblocks(int rows, int group, int block_m) { return (chunk_tokens(rows, group) - 1) / block_m + 2; }
 
 // Kernel, key streams per workgroup, prefix run length (units per split) and
-// the grid.  The 8-wave kernel with two streams of 128-row chunks by default
-// (TSFA_STREAMS=1: one stream, 256-row chunks).  TSFA_WIDE=2 selects the wide
-// kernel (256-row chunks, one wave per SIMD), TSFA_WIDE=1 selects it above
-// 128 rows per (batch, kv head), TSFA_WIDE=0 never.  By default the wide
-// kernel runs long prefixes (>= 8192 keys) under a small tree (<= 256 keys)
-// with >= 1024 rows per (batch, kv head): the 70B shape, 1376.7 -> 1345.6 us
-// per call.  With a large tree (the 1024-token wide tree: 337 -> 395 us) or
-// short runs (the 8B decode shape: its 4-8 units of 32 keys leave the wide
-// kernel's longer Q staging and deeper pipeline unamortised) the 8-wave
-// kernel is faster.
+// the grid.  The 8-wave kernel: two key streams of 128-row chunks below 1024
+// rows per (batch, kv head), one stream of 256-row chunks from 1024 rows on
+// (TSFA_STREAMS=1/2 forces one or two).  One stream loads each K/V unit once
+// for 256 rows, halving the loads per MFMA and leaving six units in flight
+// instead of two per stream: the 1024-token wide tree 391 -> 377 us, the 70B
+// shape 1463 (wide kernel) -> 1355 us per call.  Two streams fill the grid
+// where rows are few (the 8B decode shape: 22.9 -> 19.3 us; 16 sequences:
+// 75.1 -> 70.3 us).  TSFA_WIDE=2 selects the wide kernel (256-row chunks, one
+// wave per SIMD), TSFA_WIDE=1 selects it above 128 rows per (batch, kv head).
 int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
               Plan* p, bool paged = false) {
   const int G = num_heads / num_kv_heads;
   const int64_t TG = (int64_t)q_len * G;
   if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
   const int wide = env_int("TSFA_WIDE", -1);
-  p->wide = wide == 2 || (wide == 1 && TG > kMaxRows / 2) ||
-            (wide < 0 && !paged && TG >= 1024 && prefix_len >= 8192 && kv_len - prefix_len <= 256);
-  p->streams = p->wide ? 1 : (env_int("TSFA_STREAMS", 2) == 1 ? 1 : 2);
+  p->wide = wide == 2 || (wide == 1 && TG > kMaxRows / 2);  // paged calls run its plan on the 8-wave kernel
+  const int streams = env_int("TSFA_STREAMS", 0);
+  p->streams = p->wide || streams == 1 || (streams != 2 && TG >= 1024) ? 1 : 2;
   p->rows_per_chunk = kMaxRows / p->streams;
   p->n_chunks = (int)((TG + p->rows_per_chunk - 1) / p->rows_per_chunk);
   p->n_pu = ceil_div(prefix_len, kUnitKeys);
@@ -2035,12 +2090,14 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
                                                   : launch_split<T, D, 2, true, true>(sa, p, stream))
            : p.streams == 2 ? (pipe ? launch_split<T, D, 2, true, false, true>(sa, p, stream)
                                     : launch_split<T, D, 2, true>(sa, p, stream))
-                            : launch_split<T, D, 1, true>(sa, p, stream);
+                            : (pipe ? launch_split<T, D, 1, true, false, true>(sa, p, stream)
+                                    : launch_split<T, D, 1, true>(sa, p, stream));
     else
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
            : p.streams == 2   ? (pipe ? launch_split<T, D, 2, false, false, true>(sa, p, stream)
                                       : launch_split<T, D, 2, false>(sa, p, stream))
-                              : launch_split<T, D, 1, false>(sa, p, stream);
+                              : (pipe ? launch_split<T, D, 1, false, false, true>(sa, p, stream)
+                                      : launch_split<T, D, 1, false>(sa, p, stream));
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;
@@ -2274,6 +2331,13 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   sa.n_slots = p.n_slots;
   sa.n_items = p.n_items;
   sa.items_per_xcd = p.items_per_xcd;
+  sa.fd_chunks = make_fastdiv(p.n_chunks);
+  sa.fd_slots = make_fastdiv(p.n_slots);
+  sa.fd_kvh = make_fastdiv(num_kv_heads);
+  sa.fd_group = make_fastdiv(gqa_group_size);
+  sa.fd_P = make_fastdiv(p.n_chunks * p.n_slots);
+  sa.fd_Np = make_fastdiv(std::max(1, p.n_chunks * (p.n_slots - 1)));
+  sa.fd_Nt = make_fastdiv(p.n_chunks);
   sa.tree_key_limit = p.tree_key_limit;
   sa.vt_max = p.vt_max;
   sa.ws_o = workspace;
@@ -2289,6 +2353,8 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   const int order = env_int("TSFA_ITEM_ORDER", -1);
   sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
   sa.fold_tree = p.fold_tree;
+  sa.os_first = env_int("TSFA_OS_FIRST", 64);
+  sa.rot_step = env_int("TSFA_ROT", 0);
   // folded: the last run of each chunk carries the tree units, the longest
   // items, so those go first (longest first)
   if (p.fold_tree && order < 0) sa.item_order = sa.item_order ? 2 : 0;
@@ -2393,5 +2459,8 @@ extern "C" int tsfa_fwd_set_kernel_mask(int mask) {
 #ifdef TSFA_STAMPS
 extern "C" int tsfa_stamps_copy(void* dst, size_t bytes) {
   return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_stamps), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 4;
+}
+extern "C" int tsfa_cyc_copy(void* dst, size_t bytes) {
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_cyc), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 4;
 }
 #endif

@@ -250,9 +250,27 @@ def prepare_tree_sparse_metadata_batched(
         block_n=BLOCK_N, prefix_len=prefix_len)
 
 
+def _workspace(workspace: Optional[torch.Tensor], nbytes: int, dev: torch.device) -> torch.Tensor:
+    """The caller's workspace (a uint8 device tensor of at least ``nbytes``) or a new one."""
+    if workspace is None:
+        return torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=dev)
+    if workspace.device != dev or workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous uint8 tensor on {dev}")
+    if workspace.numel() < nbytes:
+        raise ValueError(f"workspace holds {workspace.numel()} bytes, the call needs {nbytes}")
+    return workspace
+
+
+def fwd_workspace_bytes(q: torch.Tensor, k: torch.Tensor, meta) -> int:
+    """Bytes of the split-KV workspace tree_sparse_attention_fwd(q, k, v, meta) uses."""
+    bsz, n_heads, q_len, head_dim = q.shape
+    return int(_lib.load().tsfa_fwd_workspace_bytes(bsz, n_heads, k.shape[1], q_len, k.shape[2], meta.prefix_len,
+                                                    head_dim))
+
+
 def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_strides, strides, sm_scale,
                 batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks,
-                gqa_group_size, block_m, block_n, head_dim, lse=None):
+                gqa_group_size, block_m, block_n, head_dim, lse=None, workspace=None):
     lib = _lib.load()
     for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
         if not t.is_cuda:
@@ -270,7 +288,7 @@ def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_st
     _lib.check("block_sparse_tree_fwd_kernel", lib.tsfa_fwd_check_args(*args))
     ws_bytes = lib.tsfa_fwd_workspace_bytes(batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
                                             head_dim)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    ws = _workspace(workspace, ws_bytes, dev)
     with torch.cuda.device(dev):
         if lse is None:
             st = lib.tsfa_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(o), _lib.ptr(row_ptr),
@@ -322,6 +340,30 @@ class _BlockSparseTreeFwdKernel:
 block_sparse_tree_fwd_kernel = _BlockSparseTreeFwdKernel()
 
 
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor], **same_as_q) -> None:
+    """Shape checks the C-ABI cannot make (it sees strides only): q [B,Hq,T,D],
+    k and v [B,Hkv,L,D] with Hq a multiple of Hkv, and each keyword tensor
+    (out, dq, ...) of q's shape; ``dk``/``dv`` keywords must have k's shape.
+    Raised before any launch (eagle_tree_sparse_bridge.py:84-87 asserts the
+    same of its inputs)."""
+    if q.dim() != 4 or k.dim() != 4:
+        raise ValueError(f"q and k must be 4-D [B, H, L, D], got {tuple(q.shape)} and {tuple(k.shape)}")
+    if v is not None and tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"v shape {tuple(v.shape)} != k shape {tuple(k.shape)}")
+    if k.shape[0] != q.shape[0]:
+        raise ValueError(f"k batch {k.shape[0]} != q batch {q.shape[0]}")
+    if k.shape[3] != q.shape[3]:
+        raise ValueError(f"k head_dim {k.shape[3]} != q head_dim {q.shape[3]}")
+    if k.shape[1] < 1 or q.shape[1] % k.shape[1]:
+        raise ValueError(f"num_heads {q.shape[1]} must be a multiple of num_kv_heads {k.shape[1]}")
+    for name, t in same_as_q.items():
+        if t is None:
+            continue
+        want = k.shape if name in ("dk", "dv") else q.shape
+        if tuple(t.shape) != tuple(want):
+            raise ValueError(f"{name} shape {tuple(t.shape)} != {tuple(want)}")
+
+
 def _row_contig(t: torch.Tensor) -> torch.Tensor:
     if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
         return t.contiguous()
@@ -341,7 +383,7 @@ def _meta_arrays(meta, bsz: int):
 
 def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta, *,
                               sm_scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                              return_lse: bool = False):
+                              return_lse: bool = False, workspace: Optional[torch.Tensor] = None):
     """O = tree-sparse attention of q [B,Hq,T,D] over k/v [B,Hkv,P+T,D].
 
     ``meta`` is a TreeSparseMetadata (one tree for the whole batch) or a
@@ -349,8 +391,10 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     sequence), already on q's device.  With ``return_lse`` the result is
     ``(O, lse)``: lse [B, Hq, T] fp32 is the natural-log log-sum-exp of each
     row's visible scaled scores (-inf for a row with no visible key), what
-    tree_sparse_attention_bwd needs.
+    tree_sparse_attention_bwd needs.  ``workspace`` optionally supplies the
+    split-KV partials buffer (uint8, ``fwd_workspace_bytes`` of the shape).
     """
+    _check_qkv(q, k, v, out=out)
     q, k, v = _row_contig(q), _row_contig(k), _row_contig(v)
     bsz, n_heads, q_len, head_dim = q.shape
     _, n_kv_heads, kv_len, _ = k.shape
@@ -363,7 +407,7 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lse = torch.empty((bsz, n_heads, q_len), dtype=torch.float32, device=q.device) if return_lse else None
     _launch_fwd(q, k, v, out, *tensors, meta_strides, strides, sm_scale, bsz, n_heads, n_kv_heads, q_len,
                 kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, n_heads // n_kv_heads,
-                meta.block_m, meta.block_n, head_dim, lse=lse)
+                meta.block_m, meta.block_n, head_dim, lse=lse, workspace=workspace)
     return (out, lse) if return_lse else out
 
 
@@ -379,6 +423,7 @@ def tree_sparse_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     contribute nothing and get dQ = 0.  No counterpart in the reference, which
     has no backward (README.md:198).
     """
+    _check_qkv(q, k, v, o=o, dout=dout, dq=dq, dk=dk, dv=dv)
     q, k, v, o, dout = (_row_contig(t) for t in (q, k, v, o, dout))
     bsz, n_heads, q_len, head_dim = q.shape
     _, n_kv_heads, kv_len, _ = k.shape
@@ -478,6 +523,10 @@ def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_
     With ``return_lse`` the result is ``(O, lse)`` as in
     tree_sparse_attention_fwd.
     """
+    if q.dim() != 4:
+        raise ValueError(f"q must be 4-D [B, Hq, T, D], got {tuple(q.shape)}")
+    if out is not None and tuple(out.shape) != tuple(q.shape):
+        raise ValueError(f"out shape {tuple(out.shape)} != q shape {tuple(q.shape)}")
     q = _row_contig(q)
     bsz, n_heads, q_len, head_dim = q.shape
     if kv_cache.dim() != 5 or kv_cache.shape[1] != 2:

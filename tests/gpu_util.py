@@ -11,11 +11,15 @@ from oracle.attn_oracle import dense_mask_attention
 # max_abs_err bars against the fp32 oracle (the named workloads use these alone).
 TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3}
 # Edge cases with few visible keys have |O| up to ~4, where rounding O once to
-# the output dtype already costs up to 2^-9*|O| (bf16) -- 7.8e-3 at |O| = 3.3,
+# the output dtype already costs up to 2^-9*|O| (bf16) -- 7.8e-3 at |O| = 4,
 # and the reference's own numerics (P rounded to the input dtype before PV,
-# tree_sparse_flashattn.py:278) add as much again.  Those tests allow
-# TOL + REL * |ref| with REL = 4 ulp of the output dtype.
-REL = {torch.bfloat16: 2.0 ** -7, torch.float16: 2.0 ** -9}
+# tree_sparse_flashattn.py:278) add about as much again.  Those tests allow
+# TOL + REL * |ref|.  Measured over the 83 such cases of the GPU suite: bf16
+# max_abs_err 1.37e-2 in 13 of 48 cases above the absolute bar, needing at
+# most 2.81e-3*|ref| beyond it (REL = 2^-8 = 3.91e-3, 2 ulp); fp16 max_abs_err
+# 1.18e-3, never above its absolute bar (REL = 0).  Every relaxed comparison
+# prints its max_abs_err and the relative share it needed.
+REL = {torch.bfloat16: 2.0 ** -8, torch.float16: 0.0}
 
 
 def assert_meta_equal(meta, ref: mo.OracleMetadata):
@@ -55,8 +59,14 @@ def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None, relative=Fals
     diff[nan_ref] = 0
     err = float(diff.max()) if diff.numel() else 0.0
     if relative:
-        bound = tol + REL[dtype] * ref.abs().nan_to_num(0.0)
+        mag = ref.abs().nan_to_num(0.0)
+        bound = tol + REL[dtype] * mag
         excess = float((diff - bound).max()) if diff.numel() else 0.0
+        # the relative share the worst element needed beyond the absolute bar
+        over = (diff - tol).clamp(min=0) / mag.clamp(min=1e-30)
+        need = float(over.max()) if diff.numel() else 0.0
+        print(f"[err] relative bar: max_abs_err {err:.3e} (absolute bar {tol:.0e}); relative part needed "
+              f"{need:.2e} of |ref|, allowed {REL[dtype]:.2e}", flush=True)
         assert excess <= 0, f"max_abs_err {err:.3e} exceeds {tol:.1e} + {REL[dtype]:.1e}*|ref|"
     else:
         assert err <= tol, f"max_abs_err {err:.3e} > {tol:.1e}"

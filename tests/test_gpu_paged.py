@@ -97,9 +97,25 @@ def test_paged_64bit_offsets(case, monkeypatch):
 
 
 def test_paged_ignores_wide_switch(monkeypatch):
-    # the paged forward always runs the 8-wave kernel, whatever the planner picks
+    # the paged forward always runs the 8-wave kernel: under TSFA_WIDE=2 it
+    # takes the wide plan's 256-row chunks on the one-stream 8-wave kernel,
+    # bit for bit the contiguous forward on that kernel
+    b, hq, hkv, t, p, d, dtype, bm, bn, kind, ps, layout, table = CASES[1]
+    rng = np.random.default_rng(t * 31 + p)
+    mask = torch.from_numpy(_tree(kind, t, rng))
+    q, k, v = (x.cuda() for x in _qkv(b, hq, hkv, t, p, d, dtype, seed=t + p))
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, bm, bn)
+    cache, indptr, indices = configs.make_paged_kv(k, v, ps, layout=layout, seed=t, spare_pages=3)
+    monkeypatch.setenv("TSFA_WIDE", "0")
+    monkeypatch.setenv("TSFA_STREAMS", "1")
+    out_c = tsf.tree_sparse_attention_fwd(q, k, v, meta)
     monkeypatch.setenv("TSFA_WIDE", "2")
-    test_paged_cases(CASES[1])
+    monkeypatch.delenv("TSFA_STREAMS")
+    out_p = tsf.tree_sparse_attention_fwd_paged(q, cache, indices, meta, kv_len=k.shape[2], kv_indptr=indptr,
+                                                kv_layout=layout)
+    torch.cuda.synchronize()
+    assert torch.equal(out_p.nan_to_num(0.0), out_c.nan_to_num(0.0))
+    assert_close_to_oracle(out_p, oracle_out(q.cpu(), k.cpu(), v.cpu(), mask, p), dtype, relative=p < 256)
 
 
 @pytest.mark.parametrize("page_size", [16, 64])

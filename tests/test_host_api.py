@@ -85,3 +85,55 @@ def test_run_requires_device_tensors():
     k = torch.zeros(1, 2, 8, 64)
     with pytest.raises(AssertionError):
         bridge.run_tree_sparse_kernel(q, k, k, torch.eye(4, dtype=torch.bool), block_m=16, block_n=16)
+
+
+def _cpu_meta(t=4, p=4):
+    z = torch.zeros(1, dtype=torch.int32)
+    return tsf.TreeSparseMetadata(z, z, z.to(torch.int8), z, z, 1, 1, 16, 16, p)
+
+
+@pytest.mark.parametrize("bad", ["k_batch", "k_dim", "v_shape", "out_shape", "gqa"])
+def test_fwd_rejects_mismatched_shapes(bad):
+    # raised on the host before any launch (CPU tensors: nothing reaches a device)
+    q, k, v, out = torch.zeros(2, 4, 4, 64), torch.zeros(2, 2, 8, 64), torch.zeros(2, 2, 8, 64), None
+    if bad == "k_batch":
+        k = v = torch.zeros(1, 2, 8, 64)
+    elif bad == "k_dim":
+        k = v = torch.zeros(2, 2, 8, 128)
+    elif bad == "v_shape":
+        v = torch.zeros(2, 2, 9, 64)
+    elif bad == "out_shape":
+        out = torch.zeros(2, 4, 5, 64)
+    else:
+        k = v = torch.zeros(2, 3, 8, 64)
+    with pytest.raises(ValueError):
+        tsf.tree_sparse_attention_fwd(q, k, v, _cpu_meta(), out=out)
+
+
+@pytest.mark.parametrize("bad", ["dq", "dk", "dv", "o", "dout", "k_batch"])
+def test_bwd_rejects_mismatched_shapes(bad):
+    q, k = torch.zeros(2, 4, 4, 64), torch.zeros(2, 2, 8, 64)
+    v, o, dout, lse = k.clone(), q.clone(), q.clone(), torch.zeros(2, 4, 4)
+    kw = {}
+    if bad in ("dq", "o", "dout"):
+        wrong = torch.zeros(2, 4, 3, 64)
+        if bad == "dq":
+            kw["dq"] = wrong
+        elif bad == "o":
+            o = wrong
+        else:
+            dout = wrong
+    elif bad in ("dk", "dv"):
+        kw[bad] = torch.zeros(2, 2, 7, 64)
+    else:
+        k = v = torch.zeros(3, 2, 8, 64)
+    with pytest.raises(ValueError):
+        tsf.tree_sparse_attention_bwd(q, k, v, o, lse, dout, _cpu_meta(), **kw)
+
+
+def test_paged_rejects_out_shape():
+    q = torch.zeros(1, 4, 4, 64)
+    cache = torch.zeros(2, 2, 16, 2, 64)
+    with pytest.raises(ValueError):
+        tsf.tree_sparse_attention_fwd_paged(q, cache, torch.zeros(1, 1, dtype=torch.int32), _cpu_meta(), kv_len=8,
+                                            out=torch.zeros(1, 4, 4, 32))
