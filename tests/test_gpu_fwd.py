@@ -263,4 +263,4 @@ def test_unsupported_dtype_raises(dtype):
 
 def test_tolerances_declared():
     assert TOL[torch.bfloat16] == 8e-3 and TOL[torch.float16] == 2e-3
-    assert REL[torch.bfloat16] == 2.0 ** -7 and REL[torch.float16] == 2.0 ** -9
+    assert REL[torch.bfloat16] == 2.0 ** -8 and REL[torch.float16] == 0.0
