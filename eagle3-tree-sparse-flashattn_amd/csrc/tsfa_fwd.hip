@@ -50,6 +50,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "tsfa_internal.h"
@@ -2403,6 +2404,74 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
                   meta_seq_stride, strides, strides ? strides + 12 : nullptr, sm_scale, batch, num_heads, num_kv_heads, q_len,
                   kv_len, prefix_len, n_q_blocks, n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype,
                   workspace, workspace_bytes, stream_);
+}
+
+// ------------------------------------------------- allocation-free forward
+// The split-KV partials of tsfa_fwd_noalloc live in this file-scope device
+// array: each GPU the library runs on holds its own copy (kNoAllocBytes) until
+// the process ends.  Its address on a device comes from hipGetSymbolAddress,
+// taken once per device with that device current; host code passes that
+// address, never the array's name, to kernels.  The split kernel writes every
+// partial the combine reads, so nothing needs clearing between calls.  All
+// calls on one GPU share the array: calls that overlap in time on one GPU
+// (different streams, or host threads) race on it.
+constexpr size_t kNoAllocBytes = TSFA_FWD_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device of `stream` (the current device for the null stream) and the
+// scratch array's address there.
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (stream != nullptr) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return TSFA_ERR_DEVICE;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return TSFA_ERR_DEVICE;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return TSFA_ERR_DEVICE;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int cur = -1;
+      if (hipGetDevice(&cur) != hipSuccess) return TSFA_ERR_DEVICE;
+      if (cur != dev && hipSetDevice(dev) != hipSuccess) return TSFA_ERR_DEVICE;
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (cur != dev) (void)hipSetDevice(cur);
+      if (e != hipSuccess || p == nullptr) return TSFA_ERR_DEVICE;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return TSFA_OK;
+}
+}  // namespace
+
+extern "C" int tsfa_fwd_noalloc(const void* q, const void* k, const void* v, void* o, const int32_t* row_ptr,
+                                const int32_t* col_idx, const int8_t* blk_type, const int32_t* mixed_mask_payload,
+                                const int32_t* mixed_mask_offset, const int64_t* meta_seq_stride,
+                                const int64_t* strides, float sm_scale, int batch, int num_heads, int num_kv_heads,
+                                int q_len, int kv_len, int prefix_len, int n_q_blocks, int n_tree_blocks,
+                                int gqa_group_size, int block_m, int block_n, int head_dim, int dtype,
+                                tsfa_stream_t stream_) {
+  // the same checks and kernels as tsfa_fwd; a call whose partials exceed
+  // the array is refused before anything runs
+  const int st = tsfa_fwd_check_args(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
+                                     n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype);
+  if (st != TSFA_OK) return st;
+  if (tsfa_fwd_workspace_bytes(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim) > kNoAllocBytes)
+    return TSFA_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int sst = noalloc_scratch(reinterpret_cast<hipStream_t>(stream_), &ws);
+  if (sst != TSFA_OK) return sst;
+  return tsfa_fwd(q, k, v, o, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset, meta_seq_stride,
+                  strides, sm_scale, batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
+                  n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype, ws, kNoAllocBytes, stream_);
 }
 
 extern "C" int tsfa_fwd_lse(const void* q, const void* k, const void* v, void* o, float* lse,

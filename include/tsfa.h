@@ -208,6 +208,24 @@ int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr
                    int block_m, int block_n, int head_dim, int dtype,
                    void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
 
+/* tsfa_fwd without the workspace argument, for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  No counterpart in the reference.  The split-KV
+ * partials go to a library-owned device array of TSFA_FWD_NOALLOC_MAX_BYTES,
+ * one per GPU, held until the process ends; its address is taken once per
+ * device (hipGetSymbolAddress) and the call allocates nothing.  Calls whose
+ * tsfa_fwd_workspace_bytes exceed the array return TSFA_ERR_WORKSPACE before
+ * launching.  All calls on one GPU share the array: calls that overlap in
+ * time on one GPU (other streams, other host threads) race on it. */
+#define TSFA_FWD_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int tsfa_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
+                     const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
+                     const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
+                     const int64_t* meta_seq_stride, const int64_t* strides, float sm_scale,
+                     int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
+                     int n_q_blocks, int n_tree_blocks, int gqa_group_size,
+                     int block_m, int block_n, int head_dim, int dtype, tsfa_stream_t stream);
+
 /* Work decomposition tsfa_fwd would use (for reports and tests):
  * out[0] = prefix splits per (batch, kv head, row chunk), out[1] = prefix
  * units (32 keys) per split, out[2] = query rows (token x head of a GQA
