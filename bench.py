@@ -46,6 +46,10 @@ import os
 import sys
 import time
 
+# this process times the split-KV kernel and the combine apart
+# (tsfa_fwd_set_kernel_mask), a hook the library keeps locked otherwise
+os.environ.setdefault("TSFA_BENCH_HOOKS", "1")
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "eagle3-tree-sparse-flashattn_amd")
 for _p in (ROOT, PKG):

@@ -60,9 +60,7 @@ namespace tsfa {
 namespace bwd {
 
 constexpr int kWaves = 8;                 // 4 key groups x 2 row groups
-constexpr int kBlockKeys = 128;           // keys per workgroup (32 per key group)
-constexpr int kTileRows = 32;             // query rows per tile
-constexpr int kMaxStateInts = 8192;       // block-state table of one tile (visibility words)
+// kBlockKeys, kTileRows, kMaxStateInts: tsfa_plan.h
 constexpr int kBufs = 2;                  // Q / dO tile buffers per row group: loads run one step ahead
 
 // 16-byte-chunk XOR swizzle of a row-major [rows][D] LDS tile (row period
@@ -810,36 +808,6 @@ __global__ __launch_bounds__(256) void bwd_prep_vis_kernel(const PrepArgs pa, co
 }
 
 // ------------------------------------------------------------------- host
-struct BwdPlan {
-  int n_tiles, n_pb, n_tb, n_tkeys, n_trees, nqbc_max;
-  size_t rowstat_bytes, dq_bytes, vis_bytes;
-};
-
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-int make_bwd_plan(int batch, int num_kv_heads, int q_len, int kv_len, int prefix_len, int gqa, int head_dim,
-                  int block_m, int n_tree_blocks, int n_trees, BwdPlan* p) {
-  const int64_t TG = (int64_t)q_len * gqa;
-  if (TG >= ((int64_t)1 << 22)) return TSFA_ERR_UNSUPPORTED;  // the kernel's row -> token division is exact below
-  p->n_tiles = (int)((TG + kTileRows - 1) / kTileRows);
-  p->n_pb = ceil_div(prefix_len, kBlockKeys);
-  p->n_tb = ceil_div(kv_len - prefix_len, kBlockKeys);
-  p->n_tkeys = p->n_tb * kBlockKeys;
-  p->n_trees = n_trees;
-  // q-blocks a 32-row tile spans: tokens t_lo .. t_lo + ceil(32/G)
-  const int toks = (kTileRows + gqa - 1) / gqa + 1;
-  p->nqbc_max = std::min(ceil_div(q_len, block_m), toks / block_m + 2);
-  if ((int64_t)p->nqbc_max * n_tree_blocks > kMaxStateInts || p->nqbc_max + 1 > 72) return TSFA_ERR_UNSUPPORTED;
-  const int64_t rows = (int64_t)batch * num_kv_heads;
-  p->rowstat_bytes = align256((size_t)rows * p->n_tiles * kTileRows * 8);
-  p->dq_bytes = align256((size_t)rows * p->n_tiles * kTileRows * head_dim * 4);
-  p->vis_bytes = align256((size_t)n_trees * p->n_tiles * p->n_tkeys * 4 + 16);
-  const int64_t items = rows * (p->n_pb + p->n_tb);
-  if (items > (int64_t)INT32_MAX / 2 || (int64_t)n_trees * p->n_tiles * p->n_tkeys > ((int64_t)1 << 28))
-    return TSFA_ERR_UNSUPPORTED;
-  return TSFA_OK;
-}
-
 // A side stream and fork/join events per (device, caller stream): the dQ
 // kernel runs beside the dK/dV kernel, so its workgroups fill the CUs that
 // the dK/dV grid leaves idle (a partial last round: 264 workgroups of one
@@ -867,9 +835,15 @@ const SideStream* side_stream(hipStream_t stream) {
   if (dev < 0 || dev >= 64 || per_dev[dev] >= kMaxSideStreams) return nullptr;
   SideStream ss;
   if (hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-  if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess)
+  if (hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess) {
+    (void)hipStreamDestroy(ss.s);
     return nullptr;
+  }
+  if (hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) {
+    (void)hipEventDestroy(ss.fork);
+    (void)hipStreamDestroy(ss.s);
+    return nullptr;
+  }
   ++per_dev[dev];
   return &sides.emplace(key, ss).first->second;
 }
@@ -899,8 +873,7 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
                      pa, va, (int)prep_blocks, std::max(1, vis_chunks));
   if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
   const unsigned grid = (unsigned)ba.items_per_xcd * 8;
-  const char* conc = getenv("TSFA_BWD_CONCURRENT");  // "0": one stream (measurements)
-  const bool concurrent = conc == nullptr || *conc == 0 || atoi(conc) != 0;
+  const bool concurrent = config().bwd_concurrent != 0;  // TSFA_BWD_CONCURRENT=0: one stream (measurements)
   const SideStream* side = (ba.q_items > 0 && concurrent) ? side_stream(stream) : nullptr;
   if (side != nullptr && (hipEventRecord(side->fork, stream) != hipSuccess ||
                           hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess))
@@ -927,19 +900,6 @@ int launch_bwd(const BwdArgs& ba, const PrepArgs& pa, const VisArgs& va, const D
 
 using namespace tsfa;
 using namespace tsfa::bwd;
-
-extern "C" size_t tsfa_bwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
-                                           int prefix_len, int block_m, int n_tree_blocks, int head_dim,
-                                           int n_trees) {
-  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || block_m <= 0 ||
-      kv_len < prefix_len || prefix_len < 0 || n_trees <= 0)
-    return 0;
-  BwdPlan p;
-  if (make_bwd_plan(batch, num_kv_heads, q_len, kv_len, prefix_len, num_heads / num_kv_heads, head_dim, block_m,
-                    n_tree_blocks, n_trees, &p) != TSFA_OK)
-    return 0;
-  return p.rowstat_bytes + p.dq_bytes + p.vis_bytes;
-}
 
 extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
                         const void* dout, void* dq, void* dk, void* dv, const int32_t* row_ptr,

@@ -1,5 +1,5 @@
-// Host-side utilities of libtsfa: version, status strings and a per-device
-// cache of the attributes the forward planner needs.
+// Per-device cache of the attributes the forward planner needs (compute
+// units, LDS per workgroup).
 
 #include <atomic>
 
@@ -38,17 +38,3 @@ int device_max_lds_per_block(int* out) {
 }
 
 }  // namespace tsfa
-
-extern "C" int tsfa_version(void) { return 1; }
-
-extern "C" const char* tsfa_status_string(int status) {
-  switch (status) {
-    case TSFA_OK: return "ok";
-    case TSFA_ERR_INVALID_ARGUMENT: return "invalid argument";
-    case TSFA_ERR_UNSUPPORTED: return "unsupported configuration";
-    case TSFA_ERR_WORKSPACE: return "workspace missing or too small";
-    case TSFA_ERR_LAUNCH: return "kernel launch failed";
-    case TSFA_ERR_DEVICE: return "no usable HIP device";
-    default: return "unknown status";
-  }
-}

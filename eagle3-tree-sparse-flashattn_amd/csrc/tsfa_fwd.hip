@@ -58,13 +58,8 @@
 namespace tsfa {
 namespace fwd {
 
-constexpr int kWaves = 8;                  // 32 query rows each
-constexpr int kMaxRows = 32 * kWaves;      // rows per chunk with one key stream
-constexpr int kUnitKeys = 32;
-constexpr int kRingBytes = 131072;   // K/V rings of the streams; the merge buffer at the end
-constexpr int kMaskWords = 4096;     // per-token 32-bit visibility words of tree units
-constexpr int kMaxTreeUnits = 1024;  // tree keys <= 32768
-constexpr int kMiscInts = 320;       // LDS scalars: visible-unit count, row_ptr window
+// kWaves, kMaxRows, kUnitKeys, kRingBytes, kMaskWords, kMaxTreeUnits and
+// kMiscInts come from tsfa_plan.h (the planner sizes the grid and LDS by them)
 constexpr float kRescaleLog2 = 8.0f;
 
 // Per-workgroup timestamps for timeline measurements: compiled in only with
@@ -482,9 +477,6 @@ template <int D, bool IS_V> __device__ inline uint32_t dma_lane_off(int u, int64
   return (uint32_t)(lr * stride * 2 + ((pos ^ sw) << 4));
 }
 
-template <int D> constexpr size_t lds_bytes_for() {
-  return (size_t)kRingBytes + kMaskWords * 4 + (kMaxTreeUnits + kMiscInts) * 4;
-}
 
 // Work item of this workgroup.  XCD x (block id % 8) owns the items
 // [x*ipx, (x+1)*ipx) of the natural order item = chunk + n_chunks * (slot +
@@ -1925,122 +1917,6 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
   merge_row<T, D, NB>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR));
 }
 
-// ------------------------------------------------------------------- plan
-struct Plan {
-  int wide, streams, rows_per_chunk;
-  int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages, fold_tree;
-  int vt_max, tree_key_limit;
-  size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
-};
-
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
-int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  if (s == nullptr || *s == 0) return dflt;
-  return atoi(s);
-}
-
-// Tokens a chunk of `rows` consecutive rows can touch, and q-blocks those span.
-int64_t chunk_tokens(int rows, int group) { return (int64_t)(rows - 1) / group + 2; }
-int64_t chunk_qblocks(int rows, int group, int block_m) { return (chunk_tokens(rows, group) - 1) / block_m + 2; }
-
-// Kernel, key streams per workgroup, prefix run length (units per split) and
-// the grid.  The 8-wave kernel: two key streams of 128-row chunks below 1024
-// rows per (batch, kv head), one stream of 256-row chunks from 1024 rows on
-// (TSFA_STREAMS=1/2 forces one or two).  One stream loads each K/V unit once
-// for 256 rows, halving the loads per MFMA and leaving six units in flight
-// instead of two per stream: the 1024-token wide tree 391 -> 377 us, the 70B
-// shape 1463 (wide kernel) -> 1355 us per call.  Two streams fill the grid
-// where rows are few (the 8B decode shape: 22.9 -> 19.3 us; 16 sequences:
-// 75.1 -> 70.3 us).  TSFA_WIDE=2 selects the wide kernel (256-row chunks, one
-// wave per SIMD), TSFA_WIDE=1 selects it above 128 rows per (batch, kv head).
-int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
-              Plan* p, bool paged = false) {
-  const int G = num_heads / num_kv_heads;
-  const int64_t TG = (int64_t)q_len * G;
-  if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
-  const int wide = env_int("TSFA_WIDE", -1);
-  p->wide = wide == 2 || (wide == 1 && TG > kMaxRows / 2);  // paged calls run its plan on the 8-wave kernel
-  const int streams = env_int("TSFA_STREAMS", 0);
-  p->streams = p->wide || streams == 1 || (streams != 2 && TG >= 1024) ? 1 : 2;
-  p->rows_per_chunk = kMaxRows / p->streams;
-  p->n_chunks = (int)((TG + p->rows_per_chunk - 1) / p->rows_per_chunk);
-  p->n_pu = ceil_div(prefix_len, kUnitKeys);
-  int cus = 256;
-  if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
-  const int64_t groups = (int64_t)batch * num_kv_heads * p->n_chunks;
-  int ups = 0;
-  if (p->n_pu > 0) {
-    ups = env_int("TSFA_PREFIX_UNITS_PER_SPLIT", 0);
-    if (ups <= 0) {
-      // Makespan model (microseconds): one workgroup per CU; a workgroup
-      // costs a fixed start/finish plus its longest stream; every slot of
-      // partials is written once and read once by the combine.
-      const double t_unit = (p->wide ? 0.6 : 0.5) * head_dim / 128.0, t_fixed = 1.5;
-      const double part_bytes = (double)batch * num_heads * q_len * (2.0 * head_dim + 8.0);
-      double best = 1e300;
-      for (int cand = 1; cand <= p->n_pu; ++cand) {
-        const int64_t splits = ceil_div(p->n_pu, cand);
-        if (cand > 1 && ceil_div(p->n_pu, cand - 1) == splits) continue;
-        const int64_t items = groups * (splits + 1);
-        const int64_t rounds = (items + cus - 1) / cus;
-        const double cost = (double)rounds * (t_fixed + ceil_div(cand, p->streams) * t_unit) +
-                            part_bytes * (double)(splits + 1) * 2.0 / 5.0e6;
-        if (cost < best * (1.0 - 1e-9)) {
-          best = cost;
-          ups = cand;
-        }
-      }
-      // Within one round, a plan with the same steps per stream that keeps
-      // more CUs busy is faster despite its extra partials (measured on the
-      // Llama-3-8B shape: 256 workgroups of 9 units beat 224 of 10 by ~1 %).
-      if (ups > 0 && groups * (ceil_div(p->n_pu, ups) + 1) <= cus) {
-        const int steps = ceil_div(ups, p->streams);
-        for (int cand = ups - 1; cand >= 1 && ceil_div(cand, p->streams) == steps; --cand)
-          if (groups * (ceil_div(p->n_pu, cand) + 1) <= cus) ups = cand;
-      }
-    }
-    ups = std::min(std::max(ups, 1), p->n_pu);
-  }
-  p->units_per_split = ups;
-  p->n_splits = ups > 0 ? ceil_div(p->n_pu, ups) : 0;
-  // A separate tree item per chunk costs a round when it does not fit beside
-  // the prefix runs; on a plan of at most 4 rounds, if the tree is short next
-  // to a run (at most a quarter of its units, or 2), the last run of each
-  // chunk takes the tree units too (the 16-sequence decode shape: 3 rounds ->
-  // 2, 73.6 -> 66.0 us per call; on the 70B shape, 16 rounds -> 15, folding
-  // measured 0.6 % slower).  TSFA_FOLD_TREE=0/1 forces it off/on (on only
-  // where there is a prefix run).
-  p->fold_tree = 0;
-  if (p->n_splits >= 1) {
-    const int64_t tree_units = ceil_div(std::max(0, kv_len - prefix_len), kUnitKeys);
-    const int64_t rounds_sep = (groups * (p->n_splits + 1) + cus - 1) / cus;
-    const int64_t rounds_fold = (groups * p->n_splits + cus - 1) / cus;
-    const int force = env_int("TSFA_FOLD_TREE", -1);
-    p->fold_tree = force >= 0 ? (force != 0)
-                              : (rounds_fold < rounds_sep && rounds_sep <= 4 && tree_units <= std::max(2, ups / 4)
-                                     ? 1 : 0);
-  }
-  p->n_slots = p->n_splits + (p->fold_tree ? 0 : 1);
-  const int64_t items = groups * p->n_slots;
-  if (items > (int64_t)INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
-  p->n_items = (int)items;
-  p->items_per_xcd = ceil_div(p->n_items, 8);
-  p->grid = p->items_per_xcd * 8;
-  int max_lds = 65536;
-  if (device_max_lds_per_block(&max_lds) != TSFA_OK) return TSFA_ERR_DEVICE;
-  p->lds_bytes = head_dim == 128 ? lds_bytes_for<128>() : lds_bytes_for<64>();
-  if (p->lds_bytes > (size_t)max_lds) return TSFA_ERR_UNSUPPORTED;
-  p->ring_stages = kRingBytes / p->streams / (2 * kUnitKeys * head_dim * 2);
-  p->vt_max = (int)(kMaskWords / chunk_tokens(p->rows_per_chunk, G));
-  p->tree_key_limit = kv_len - prefix_len;  // refined by the caller with n_tree_blocks*BN
-  const size_t rows = (size_t)batch * num_heads * q_len;
-  p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 2);
-  p->ws_ml_bytes = align256(rows * p->n_slots * 8);
-  return TSFA_OK;
-}
-
 template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
@@ -2085,7 +1961,7 @@ template <typename T, int D, bool PAGED>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
     int st;
-    const bool pipe = env_int("TSFA_PIPE", 1) != 0;
+    const bool pipe = config().pipe != 0;
     if constexpr (PAGED)
       st = (sa.cache32 && p.streams == 2) ? (pipe ? launch_split<T, D, 2, true, true, true>(sa, p, stream)
                                                   : launch_split<T, D, 2, true, true>(sa, p, stream))
@@ -2147,34 +2023,50 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
 using namespace tsfa;
 using namespace tsfa::fwd;
 
-extern "C" int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
-                                   int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size,
-                                   int block_m, int block_n, int head_dim, int dtype) {
-  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || q_len < 0) return TSFA_ERR_INVALID_ARGUMENT;
-  if (block_m <= 0 || block_n <= 0) return TSFA_ERR_INVALID_ARGUMENT;          // tree_sparse_flashattn.py:87-88
-  if (prefix_len < 0 || kv_len < prefix_len) return TSFA_ERR_INVALID_ARGUMENT;  // eagle_tree_sparse_bridge.py:91-93
-  if (gqa_group_size <= 0 || num_heads != gqa_group_size * num_kv_heads) return TSFA_ERR_INVALID_ARGUMENT;
-  if (n_q_blocks != ceil_div(q_len, block_m) || n_tree_blocks != ceil_div(q_len, block_n))
-    return TSFA_ERR_INVALID_ARGUMENT;
-  if (dtype != TSFA_DTYPE_FP16 && dtype != TSFA_DTYPE_BF16) return TSFA_ERR_UNSUPPORTED;
-  if (head_dim != 64 && head_dim != 128) return TSFA_ERR_UNSUPPORTED;
-  if (block_n % 16 != 0) return TSFA_ERR_UNSUPPORTED;
-  const int64_t tree_limit = std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
-  if (tree_limit > (int64_t)kMaxTreeUnits * kUnitKeys) return TSFA_ERR_UNSUPPORTED;
-  // the tree block-state table [q-blocks of a chunk][n_tree_blocks] lives in
-  // the LDS ring and the chunk's row_ptr window in the LDS scalars
-  const int64_t nqbc = chunk_qblocks(kMaxRows, gqa_group_size, block_m);
-  if (nqbc * n_tree_blocks * 4 > (int64_t)kRingBytes || nqbc + 1 > kMiscInts - 8) return TSFA_ERR_UNSUPPORTED;
-  return TSFA_OK;
+namespace {
+
+// The plan of a shape on the current device (its CU count and LDS limit),
+// memoised per host thread: a call's workspace query and its launch plan the
+// same shape once.
+int device_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
+                bool paged, Plan* p) {
+  int cus = 0, max_lds = 0;
+  if (device_cu_count(&cus) != TSFA_OK || device_max_lds_per_block(&max_lds) != TSFA_OK) return TSFA_ERR_DEVICE;
+  const Config& cfg = config();
+  struct Entry {
+    int key[12];
+    Plan plan;
+    int status;
+  };
+  constexpr int kEntries = 4;
+  thread_local Entry cache[kEntries];
+  thread_local int n_cached = 0, next = 0;
+  const int key[12] = {batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, paged ? 1 : 0, cus,
+                       max_lds, cfg.generation, 1};
+  for (int e = 0; e < n_cached; ++e)
+    if (std::equal(key, key + 12, cache[e].key)) {
+      *p = cache[e].plan;
+      return cache[e].status;
+    }
+  Entry& ent = cache[next];
+  next = (next + 1) % kEntries;
+  n_cached = std::min(n_cached + 1, kEntries);
+  std::copy(key, key + 12, ent.key);
+  ent.status = make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, paged, cus, max_lds,
+                         cfg, &ent.plan);
+  *p = ent.plan;
+  return ent.status;
 }
+
+}  // namespace
 
 extern "C" size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                            int prefix_len, int head_dim) {
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
   // enough for both the contiguous and the paged plan of the shape
   Plan p, pp;
-  if (make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p) != TSFA_OK ||
-      make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &pp, true) != TSFA_OK)
+  if (device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, false, &p) != TSFA_OK ||
+      device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, true, &pp) != TSFA_OK)
     return 0;
   return std::max(p.ws_acc_bytes + p.ws_ml_bytes, pp.ws_acc_bytes + pp.ws_ml_bytes);
 }
@@ -2184,7 +2076,7 @@ extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_l
   if (out6 == nullptr || batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return TSFA_ERR_INVALID_ARGUMENT;
   Plan p;
-  const int st = make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p);
+  const int st = device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, false, &p);
   if (st != TSFA_OK) return st;
   out6[0] = p.n_splits;
   out6[1] = p.units_per_split;
@@ -2224,42 +2116,19 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   if (batch == 0 || q_len == 0) return TSFA_OK;
   if (q_strides == nullptr || o_strides == nullptr || meta_seq_stride == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
   if (q == nullptr || o == nullptr || row_ptr == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
-  if (kv.paged() ? (kv.cache_strides == nullptr || kv.kv_indices == nullptr)
-                 : (kv.k == nullptr || kv.v == nullptr || kv.k_strides == nullptr || kv.v_strides == nullptr))
-    return TSFA_ERR_INVALID_ARGUMENT;
-  // contiguous head_dim, 16-byte aligned rows and bases
-  auto rows_ok = [](const int64_t* sd, int n) {
-    if (sd[n - 1] != 1) return false;
-    for (int j = 0; j < n - 1; ++j)
-      if (sd[j] % 8 != 0) return false;
-    return true;
-  };
-  auto aligned = [](const void* ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
-  if (!rows_ok(q_strides, 4) || !rows_ok(o_strides, 4) || !aligned(q) || !aligned(o)) return TSFA_ERR_UNSUPPORTED;
-  if (kv.paged()) {
-    if (!rows_ok(kv.cache_strides, 5) || !aligned(kv.cache)) return TSFA_ERR_UNSUPPORTED;
-    if (kv.cache_strides[2] >= ((int64_t)1 << 26)) return TSFA_ERR_UNSUPPORTED;  // 32-bit lane offsets
-    // pages of 16 keys or more, a power of two: a wave's 16-key DMA share
-    // then spans at most two pages
-    if (kv.page_size < 16 || (kv.page_size & (kv.page_size - 1)) != 0) return TSFA_ERR_UNSUPPORTED;
-    if (kv.pt_stride < 0 || kv.n_indices > INT32_MAX || kv.pt_stride > INT32_MAX ||
-        (kv_len > 0 && (kv.n_pages <= 0 || kv.n_indices <= 0)))
-      return TSFA_ERR_INVALID_ARGUMENT;
-    // a dense page table holds every sequence's ceil(kv_len / page_size) pages
-    if (kv.kv_indptr == nullptr && kv_len > 0 &&
-        (int64_t)(batch - 1) * kv.pt_stride + ceil_div(kv_len, kv.page_size) > kv.n_indices)
-      return TSFA_ERR_INVALID_ARGUMENT;
-  } else {
-    if (!rows_ok(kv.k_strides, 4) || !rows_ok(kv.v_strides, 4) || !aligned(kv.k) || !aligned(kv.v))
-      return TSFA_ERR_UNSUPPORTED;
-    // K/V row strides must keep a 32-bit lane offset of 8 rows
-    if (kv.k_strides[2] >= ((int64_t)1 << 26) || kv.v_strides[2] >= ((int64_t)1 << 26)) return TSFA_ERR_UNSUPPORTED;
-  }
+  if (kv.paged() && kv.kv_indices == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  if (kv.paged() && (kv.cache == nullptr || kv.cache_strides == nullptr)) return TSFA_ERR_INVALID_ARGUMENT;
+  st = check_strides(q, q_strides, o, o_strides);
+  if (st != TSFA_OK) return st;
+  st = kv.paged() ? check_paged(batch, kv_len, kv.cache, kv.cache_strides, kv.kv_indptr, kv.pt_stride, kv.n_indices,
+                                kv.n_pages, kv.page_size)
+                  : check_kv_strides(kv.k, kv.k_strides, kv.v, kv.v_strides);
+  if (st != TSFA_OK) return st;
   for (int i = 0; i < 5; ++i)
     if (meta_seq_stride[i] < 0) return TSFA_ERR_INVALID_ARGUMENT;
 
   Plan p;
-  st = make_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, &p, kv.paged());
+  st = device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, kv.paged(), &p);
   if (st != TSFA_OK) return st;
   p.tree_key_limit = (int)std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
   if (workspace == nullptr || workspace_bytes < p.ws_acc_bytes + p.ws_ml_bytes) return TSFA_ERR_WORKSPACE;
@@ -2294,10 +2163,10 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
     int shift = 0;
     while ((1 << shift) < kv.page_size) ++shift;
     sa.page_shift = shift;
-    // byte offsets from a head's base stay inside the cache: 32 bits suffice
-    // below 4 GB (TSFA_PAGED32=0 keeps the 64-bit kernel)
-    const uint64_t cache_bytes = (uint64_t)kv.n_pages * (uint64_t)kv.cache_strides[0] * 2;
-    sa.cache32 = (kv.cache_strides[0] > 0 && cache_bytes < ((uint64_t)1 << 32) && env_int("TSFA_PAGED32", 1) != 0)
+    // the 32-bit-offset kernel when every byte offset it forms from a kv
+    // head's base fits (TSFA_PAGED32=0 keeps the 64-bit kernel)
+    sa.cache32 = (config().paged32 != 0 && paged_offsets_fit_32(kv.n_pages, kv.cache_strides[0], kv.cache_strides[2],
+                                                                 kv.page_size, head_dim))
                      ? 1 : 0;
     sa.cps_b32 = (uint32_t)(kv.cache_strides[0] * 2);
     sa.crs_b32 = (uint32_t)(kv.cache_strides[2] * 2);
@@ -2345,17 +2214,17 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   sa.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
   // Non-temporal K/V loads when little L2 reuse is at stake (TSFA_KV_NT=0/1
   // forces them off/on).
-  const int kv_nt = env_int("TSFA_KV_NT", -1);
+  const int kv_nt = config().kv_nt;
   sa.kv_nt = kv_nt >= 0 ? (kv_nt != 0) : (p.n_chunks <= 2);
   // Prefix runs first when the grid has at most 4 rounds (TSFA_ITEM_ORDER=0/1/2
   // forces natural / prefix first / tree first).
   int cus = 256;
   if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
-  const int order = env_int("TSFA_ITEM_ORDER", -1);
+  const int order = config().item_order;
   sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
   sa.fold_tree = p.fold_tree;
-  sa.os_first = env_int("TSFA_OS_FIRST", 64);
-  sa.rot_step = env_int("TSFA_ROT", 0);
+  sa.os_first = config().os_first;
+  sa.rot_step = config().rot;
   // folded: the last run of each chunk carries the tree units, the longest
   // items, so those go first (longest first)
   if (p.fold_tree && order < 0) sa.item_order = sa.item_order ? 2 : 0;
@@ -2521,6 +2390,8 @@ extern "C" int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t
 
 extern "C" int tsfa_fwd_set_kernel_mask(int mask) {
   if (mask < 1 || mask > 3) return TSFA_ERR_INVALID_ARGUMENT;
+  // measurement builds of a process only: TSFA_BENCH_HOOKS=1 unlocks it
+  if (mask != 3 && config().bench_hooks == 0) return TSFA_ERR_UNSUPPORTED;
   g_kernel_mask = mask;
   return TSFA_OK;
 }

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/tsfa.h"
+#include "tsfa_plan.h"
 
 namespace tsfa {
 
@@ -35,30 +36,9 @@ template <> struct Mma<_Float16> {
   }
 };
 
-// Division by a runtime-invariant divisor d >= 1 for dividends 0 <= n < 2^31:
-// n / d == (umulhi(n, m) + n) >> s with s = ceil(log2 d) and
-// m = floor(2^32 (2^s - d) / d) + 1 (Granlund and Montgomery, "Division by
-// invariant integers using multiplication", 1994, Fig. 4.1; the sum cannot
-// wrap because umulhi(n, m) <= n < 2^31).  A kernel's per-wave scalar
-// divisions cost ~35 instructions each, on the scalar unit the CU's waves share.
-struct FastDiv {
-  uint32_t m, s, d;
-};
-inline FastDiv make_fastdiv(uint32_t d) {
-  uint32_t s = 0;
-  while ((1ull << s) < d) ++s;
-  const uint64_t m = ((1ull << 32) * ((1ull << s) - d)) / d + 1;
-  return FastDiv{(uint32_t)m, s, d};
-}
-__host__ __device__ inline uint32_t fdiv(uint32_t n, const FastDiv& f) {
-  return (uint32_t)((((uint64_t)n * f.m) >> 32) + n) >> f.s;
-}
-__host__ __device__ inline uint32_t frem(uint32_t n, const FastDiv& f) { return n - fdiv(n, f) * f.d; }
-
 // ---------------------------------------------------------- host utilities
 int device_cu_count(int* out);            // cached per device
 int device_max_lds_per_block(int* out);   // cached per device
 
-inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace tsfa

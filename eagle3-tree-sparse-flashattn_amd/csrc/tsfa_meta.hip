@@ -31,10 +31,8 @@ constexpr int kMetaThreads = 256;
 
 enum : int8_t { kZero = 0, kFull = 1, kMixed = 2 };
 
-struct MetaGeom {
-  int q_len, block_m, block_n, nqb, ntb, words;  // words = W per block
-  int64_t cap;                                   // nqb * ntb
-};
+using meta::MetaGeom;  // tsfa_plan.h
+using meta::meta_geom;
 
 constexpr int kSmallBlocks = 256;
 constexpr int kSmallWords = 8192;  // 32 KB of packed words in LDS
@@ -222,42 +220,10 @@ __global__ void pack_bits_kernel(const uint8_t* __restrict__ bits, int64_t n_bit
   words[wi] = (int32_t)word;
 }
 
-bool meta_geom(int q_len, int block_m, int block_n, MetaGeom* g) {
-  g->q_len = q_len;
-  g->block_m = block_m;
-  g->block_n = block_n;
-  g->nqb = ceil_div(q_len, block_m);
-  g->ntb = ceil_div(q_len, block_n);
-  const int64_t words = ((int64_t)block_m * block_n + 31) / 32;
-  g->cap = (int64_t)g->nqb * g->ntb;
-  if (words > INT32_MAX || g->cap * words > INT32_MAX) return false;  // int32 payload offsets
-  g->words = (int)words;
-  return true;
-}
-
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
 }  // namespace
 }  // namespace tsfa
 
 using namespace tsfa;
-
-extern "C" int tsfa_meta_check_args(int n_seq, int q_len, int block_m, int block_n) {
-  if (block_m <= 0 || block_n <= 0 || n_seq < 0 || q_len < 0) return TSFA_ERR_INVALID_ARGUMENT;
-  MetaGeom g;
-  if (!meta_geom(q_len, block_m, block_n, &g)) return TSFA_ERR_UNSUPPORTED;
-  if ((int64_t)n_seq * g.cap * g.words > ((int64_t)1 << 40)) return TSFA_ERR_UNSUPPORTED;
-  if (n_seq > 65535) return TSFA_ERR_UNSUPPORTED;  // grid.y
-  return TSFA_OK;
-}
-
-extern "C" size_t tsfa_meta_workspace_bytes(int n_seq, int q_len, int block_m, int block_n) {
-  if (tsfa_meta_check_args(n_seq, q_len, block_m, block_n) != TSFA_OK) return 0;
-  MetaGeom g;
-  meta_geom(q_len, block_m, block_n, &g);
-  const size_t nb = (size_t)n_seq * g.cap;
-  return align256(nb) + align256(nb * g.words * 4) + align256(nb * 4);
-}
 
 extern "C" int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int64_t mask_row_stride,
                                int n_seq, int q_len, int block_m, int block_n, int32_t* row_ptr,
@@ -281,9 +247,8 @@ extern "C" int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int
   int32_t* words = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb));
   int32_t* src_of_rank =
       reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb) + align256(nb * g.words * 4));
-  const char* small_env = getenv("TSFA_META_SMALL");  // "0": always two launches
   const bool small = g.cap > 0 && g.cap <= kSmallBlocks && g.cap * g.words <= kSmallWords &&
-                     !(small_env != nullptr && small_env[0] == '0');
+                     config().meta_small != 0;  // TSFA_META_SMALL=0: always two launches
   if (small) {
     hipLaunchKernelGGL(build_small_kernel, dim3((unsigned)n_seq), dim3(kMetaThreads), 0, stream, mask,
                        mask_seq_stride, mask_row_stride, g, row_ptr, col_idx, blk_type, payload, offset, counts);

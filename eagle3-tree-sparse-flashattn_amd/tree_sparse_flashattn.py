@@ -128,32 +128,32 @@ class BatchedTreeSparseMetadata:
         )
 
 
-def _hip_device(t: torch.Tensor) -> torch.device:
-    if t.is_cuda:
-        return t.device
-    if not torch.cuda.is_available():
-        raise RuntimeError("the tree-sparse metadata builder runs on a HIP device; none is available")
-    return torch.device("cuda", torch.cuda.current_device())
-
-
 def _pack_block_mask_to_int32(mask_2d: torch.Tensor) -> torch.Tensor:
     """Pack a bool [BLOCK_M, BLOCK_N] block row-major into int32 words.
 
     Bit i of word w is flat[32w + i] (tree_sparse_flashattn.py:44-64); the
-    result lives on the input's device.
+    result lives on the input's device: a CPU block is packed on the host
+    (tsfa_pack_bits_host), a device block on its device (tsfa_pack_bits).
     """
-    dev = _hip_device(mask_2d)
-    flat = mask_2d.reshape(-1).to(device=dev, dtype=torch.bool).contiguous().view(torch.uint8)
+    lib = _lib.load()
+    flat = mask_2d.reshape(-1)
+    if flat.dtype != torch.bool:
+        flat = flat != 0
+    flat = flat.contiguous().view(torch.uint8)
     n_bits = flat.numel()
-    out = torch.zeros(((n_bits + 31) // 32,), dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        _lib.check("tsfa_pack_bits", _lib.load().tsfa_pack_bits(_lib.ptr(flat), n_bits, _lib.ptr(out),
-                                                               _lib.stream_handle(dev)))
-    return out.to(mask_2d.device)
+    out = torch.zeros(((n_bits + 31) // 32,), dtype=torch.int32, device=flat.device)
+    if not flat.is_cuda:
+        _lib.check("_pack_block_mask_to_int32", lib.tsfa_pack_bits_host(_lib.ptr(flat), n_bits, _lib.ptr(out)))
+        return out
+    with torch.cuda.device(flat.device):
+        _lib.check("_pack_block_mask_to_int32", lib.tsfa_pack_bits(_lib.ptr(flat), n_bits, _lib.ptr(out),
+                                                                   _lib.stream_handle(flat.device)))
+    return out
 
 
 def _meta_build(masks_u8: torch.Tensor, block_m: int, block_n: int, dev: torch.device):
-    """Run tsfa_meta_build over [n_seq, q_len, q_len] uint8 masks on `dev`."""
+    """tsfa_meta_build over [n_seq, q_len, q_len] uint8 masks on `dev` (a HIP
+    device), or tsfa_meta_build_host when `dev` is the CPU."""
     lib = _lib.load()
     n_seq, q_len = masks_u8.shape[0], masks_u8.shape[1]
     _lib.check("prepare_tree_sparse_metadata", lib.tsfa_meta_check_args(n_seq, q_len, block_m, block_n))
@@ -168,6 +168,12 @@ def _meta_build(masks_u8: torch.Tensor, block_m: int, block_n: int, dev: torch.d
     payload = torch.empty((n_seq, cap * words), **i32)
     offset = torch.empty((n_seq, cap), **i32)
     counts = torch.empty((n_seq, 2), **i32)
+    if dev.type == "cpu":
+        st = lib.tsfa_meta_build_host(_lib.ptr(masks_u8), masks_u8.stride(0), masks_u8.stride(1), n_seq, q_len,
+                                      block_m, block_n, _lib.ptr(row_ptr), _lib.ptr(col_idx), _lib.ptr(blk_type),
+                                      _lib.ptr(payload), _lib.ptr(offset), _lib.ptr(counts))
+        _lib.check("prepare_tree_sparse_metadata", st)
+        return row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb
     ws_bytes = lib.tsfa_meta_workspace_bytes(n_seq, q_len, block_m, block_n)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
@@ -179,8 +185,8 @@ def _meta_build(masks_u8: torch.Tensor, block_m: int, block_n: int, dev: torch.d
     return row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb
 
 
-def _masks_u8(tree_masks: torch.Tensor, dev: torch.device) -> torch.Tensor:
-    m = tree_masks.to(device=dev)
+def _masks_u8(tree_masks: torch.Tensor) -> torch.Tensor:
+    m = tree_masks
     if m.dtype != torch.bool:
         m = m != 0  # nonzero -> visible, NaN included (tree_sparse_flashattn.py:90)
     if m.stride(-1) != 1:
@@ -199,25 +205,24 @@ def prepare_tree_sparse_metadata(
     Same contract as tree_sparse_flashattn.py:67-160: ``tree_mask`` is a
     [q_len, q_len] tensor of any dtype (nonzero = visible); ValueError for a
     non-square mask or non-positive block sizes.  The tensors come back on the
-    mask's device (a CPU mask is processed on the current HIP device and the
-    result copied back).
+    mask's device: a CPU mask is processed on the host (tsfa_meta_build_host,
+    no device needed, as the reference runs it), a device mask on its device.
     """
     if tree_mask.ndim != 2 or tree_mask.shape[0] != tree_mask.shape[1]:
         raise ValueError("tree_mask must be shape [q_len, q_len].")
     if BLOCK_M <= 0 or BLOCK_N <= 0:
         raise ValueError("BLOCK_M and BLOCK_N must be positive.")
-    dev = _hip_device(tree_mask)
-    masks = _masks_u8(tree_mask, dev).unsqueeze(0)
-    row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N, dev)
+    masks = _masks_u8(tree_mask).unsqueeze(0)
+    row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N,
+                                                                                tree_mask.device)
     nnz, n_mixed = (int(x) for x in counts[0].tolist())
     words = (BLOCK_M * BLOCK_N + 31) // 32
-    out_dev = tree_mask.device
     return TreeSparseMetadata(
-        row_ptr=row_ptr[0].to(out_dev),
-        col_idx=col_idx[0, :nnz].to(out_dev),
-        blk_type=blk_type[0, :nnz].to(out_dev),
-        mixed_mask_payload=payload[0, : n_mixed * words].to(out_dev),
-        mixed_mask_offset=(offset[0, :nnz] if n_mixed > 0 else offset[0, :0]).to(out_dev),
+        row_ptr=row_ptr[0],
+        col_idx=col_idx[0, :nnz],
+        blk_type=blk_type[0, :nnz],
+        mixed_mask_payload=payload[0, : n_mixed * words],
+        mixed_mask_offset=offset[0, :nnz] if n_mixed > 0 else offset[0, :0],
         n_q_blocks=nqb,
         n_tree_blocks=ntb,
         block_m=BLOCK_M,
@@ -234,16 +239,17 @@ def prepare_tree_sparse_metadata_batched(
 ) -> BatchedTreeSparseMetadata:
     """Metadata for [S, q_len, q_len] masks (one tree per sequence), or for one
     [q_len, q_len] mask shared by the whole batch (S = 1), in one launch and
-    without a host synchronisation (the record stays in capacity layout)."""
+    without a host synchronisation (the record stays in capacity layout).
+    CPU masks are processed on the host and give a CPU record."""
     if tree_masks.ndim == 2:
         tree_masks = tree_masks.unsqueeze(0)
     if tree_masks.ndim != 3 or tree_masks.shape[1] != tree_masks.shape[2]:
         raise ValueError("tree_masks must be shape [batch, q_len, q_len] or [q_len, q_len].")
     if BLOCK_M <= 0 or BLOCK_N <= 0:
         raise ValueError("BLOCK_M and BLOCK_N must be positive.")
-    dev = _hip_device(tree_masks)
-    masks = _masks_u8(tree_masks, dev)
-    row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N, dev)
+    masks = _masks_u8(tree_masks)
+    row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb = _meta_build(masks, BLOCK_M, BLOCK_N,
+                                                                                tree_masks.device)
     return BatchedTreeSparseMetadata(
         row_ptr=row_ptr, col_idx=col_idx, blk_type=blk_type, mixed_mask_payload=payload,
         mixed_mask_offset=offset, counts=counts, n_q_blocks=nqb, n_tree_blocks=ntb, block_m=BLOCK_M,

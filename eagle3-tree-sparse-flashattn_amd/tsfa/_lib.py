@@ -33,6 +33,11 @@ EXPORTS = (
     "tsfa_meta_workspace_bytes",
     "tsfa_meta_build",
     "tsfa_pack_bits",
+    "tsfa_meta_build_host",
+    "tsfa_pack_bits_host",
+    "tsfa_config_reload",
+    "tsfa_fwd_plan_for_device",
+    "tsfa_fwd_workspace_bytes_for_device",
     "tsfa_fwd_check_args",
     "tsfa_fwd_workspace_bytes",
     "tsfa_fwd",
@@ -55,6 +60,12 @@ _SIGNATURES = {
     "tsfa_meta_build": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                  _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "tsfa_pack_bits": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp]),
+    "tsfa_meta_build_host": (_c_int, [_c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                      _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp]),
+    "tsfa_pack_bits_host": (_c_int, [_c_vp, _c_i64, _c_vp]),
+    "tsfa_config_reload": (_c_int, []),
+    "tsfa_fwd_plan_for_device": (_c_int, [_c_int] * 10 + [ctypes.POINTER(ctypes.c_int32)]),
+    "tsfa_fwd_workspace_bytes_for_device": (_c_size, [_c_int] * 9),
     "tsfa_fwd_check_args": (_c_int, [_c_int] * 13),
     "tsfa_fwd_workspace_bytes": (_c_size, [_c_int] * 7),
     "tsfa_fwd": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -95,7 +106,12 @@ def load() -> ctypes.CDLL:
             "(the HIP path has no CPU fallback)"
         )
     lib = ctypes.CDLL(str(path))
+    # TSFA_HOST_ONLY=1: a build of the host-only part (tsfa_plan.cpp), as
+    # the sanitizer test loads it; its entry points are a subset
+    host_only = os.environ.get("TSFA_HOST_ONLY") == "1"
     for name, (res, args) in _SIGNATURES.items():
+        if host_only and not hasattr(lib, name):
+            continue
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args

@@ -1,7 +1,8 @@
 """Build libtsfa.so for gfx950 in-tree.
 
-Each ``csrc/*.hip`` file is compiled with ``hipcc -c`` and the objects are
-linked with the system C++ compiler against the HIP runtime that PyTorch
+Each ``csrc/*.hip`` file is compiled with ``hipcc -c``, each host-only
+``csrc/*.cpp`` file with the system C++ compiler, and the objects are linked
+with the system C++ compiler against the HIP runtime that PyTorch
 loads (torch/lib/libamdhip64.so when torch is importable), so the library and
 torch share one HIP runtime in the process and torch's stream handles are
 valid for libtsfa.
@@ -50,23 +51,28 @@ def hip_runtime_dir() -> Path:
     return ROCM / "lib"
 
 
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter"]
+
+
 def _compile(src: Path, obj: Path) -> None:
-    hipcc = str(ROCM / "bin" / "hipcc")
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cmd = [shutil.which("g++") or "c++", *CXX_FLAGS, "-c", str(src), "-o", str(obj)]
+    else:
+        cmd = [str(ROCM / "bin" / "hipcc"), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(
         line for line in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in line
     )
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{out}")
+        raise RuntimeError(f"compile failed for {src.name}:\n{out}")
     if out.strip():
         print(out, file=sys.stderr)
 
 
 def build(verbose: bool = True) -> Path:
-    """Compile every csrc/*.hip and link libtsfa.so (always rebuilds)."""
+    """Compile every csrc/*.hip and csrc/*.cpp and link libtsfa.so (always rebuilds)."""
     BUILD_DIR.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+    sources = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
     objs = [BUILD_DIR / (s.stem + ".o") for s in sources]
     with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         list(ex.map(_compile, sources, objs))

@@ -11,6 +11,7 @@
  * Reference interfaces replaced (LUOseu/eagle3-tree-sparse-flashattn):
  *   tsfa_meta_build   prepare_tree_sparse_metadata     tree_sparse_flashattn.py:67-160
  *   tsfa_pack_bits    _pack_block_mask_to_int32         tree_sparse_flashattn.py:44-64
+ *   tsfa_*_host       the same on a CPU mask (no device)
  *   tsfa_fwd          block_sparse_tree_fwd_kernel[grid] tree_sparse_flashattn.py:163-339
  *                     (argument list: tree_sparse_flashattn.py:164-203,
  *                      call sites eagle_tree_sparse_bridge.py:119-158,
@@ -77,6 +78,16 @@ int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int64_t mask_r
 /* Packs n_bits bools (uint8, nonzero = 1) row-major into ceil(n_bits/32)
  * int32 words, bit i of word w = bits[32w+i] (tree_sparse_flashattn.py:44-64). */
 int tsfa_pack_bits(const uint8_t* bits, int64_t n_bits, int32_t* words, tsfa_stream_t stream);
+
+/* The same two on the host (every pointer host memory, no device needed):
+ * prepare_tree_sparse_metadata and _pack_block_mask_to_int32 of a CPU mask,
+ * as the reference runs them (tree_sparse_flashattn.py:44-160, README.md
+ * quick start).  Output layout and errors as tsfa_meta_build / tsfa_pack_bits. */
+int tsfa_meta_build_host(const uint8_t* mask, int64_t mask_seq_stride, int64_t mask_row_stride,
+                         int n_seq, int q_len, int block_m, int block_n,
+                         int32_t* row_ptr, int32_t* col_idx, int8_t* blk_type,
+                         int32_t* payload, int32_t* offset, int32_t* counts);
+int tsfa_pack_bits_host(const uint8_t* bits, int64_t n_bits, int32_t* words);
 
 /* ----------------------------------------------------------------- forward
  * Tree-sparse attention forward: for every (b, h, t) row,
@@ -226,6 +237,22 @@ int tsfa_fwd_noalloc(const void* q, const void* k, const void* v, void* o,
                      int n_q_blocks, int n_tree_blocks, int gqa_group_size,
                      int block_m, int block_n, int head_dim, int dtype, tsfa_stream_t stream);
 
+/* tsfa_fwd_plan and tsfa_fwd_workspace_bytes for a device of `cus` compute
+ * units and `max_lds` bytes of LDS per workgroup instead of the current one
+ * (host-only: size a workspace, or test the planner, with no device).
+ * out8 = tsfa_fwd_plan's six values, then the partial slots per row chunk
+ * and whether the tree units ride on the last prefix run (1) or run as
+ * their own work items (0).  `paged` plans tsfa_fwd_paged.  No counterpart in
+ * the reference (its grid is fixed, tree_sparse_flashattn.py:358). */
+int tsfa_fwd_plan_for_device(int cus, int max_lds, int batch, int num_heads, int num_kv_heads, int q_len,
+                             int kv_len, int prefix_len, int head_dim, int paged, int32_t* out8);
+size_t tsfa_fwd_workspace_bytes_for_device(int cus, int max_lds, int batch, int num_heads, int num_kv_heads,
+                                           int q_len, int kv_len, int prefix_len, int head_dim);
+
+/* Re-read the TSFA_* environment switches (read once, at their first use).
+ * Not to be called while a forward or backward of this library runs. */
+int tsfa_config_reload(void);
+
 /* Work decomposition tsfa_fwd would use (for reports and tests):
  * out[0] = prefix splits per (batch, kv head, row chunk), out[1] = prefix
  * units (32 keys) per split, out[2] = query rows (token x head of a GQA
@@ -238,8 +265,9 @@ int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_
  * which kernels tsfa_fwd launches on this host thread -- bit 0 the split-KV
  * kernel, bit 1 the combine (3 = both, the default and the only setting that
  * computes O).  A benchmark times each kernel alone this way; any other mask
- * leaves O unwritten or computed from stale partials.  Invalid: mask outside
- * 1..3. */
+ * leaves O unwritten or computed from stale partials, so only a process that
+ * sets TSFA_BENCH_HOOKS=1 may select one (else TSFA_ERR_UNSUPPORTED; 3 is
+ * always accepted).  Invalid: mask outside 1..3. */
 int tsfa_fwd_set_kernel_mask(int mask);
 
 #ifdef __cplusplus

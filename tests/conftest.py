@@ -17,3 +17,46 @@ for p in (ROOT, PKG):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a HIP device (MI355X) and the built libtsfa.so")
+
+
+# The library reads its TSFA_* environment switches once; tests that switch
+# them through monkeypatch (setenv, delenv, and the restore at teardown) make
+# it read them again.
+import pytest  # noqa: E402
+
+_mp_setenv, _mp_delenv, _mp_undo = pytest.MonkeyPatch.setenv, pytest.MonkeyPatch.delenv, pytest.MonkeyPatch.undo
+
+
+def _reload_config():
+    try:
+        from tsfa import _lib
+        lib = _lib.load()
+    except Exception:  # library not built: nothing to reload
+        return
+    if hasattr(lib, "tsfa_config_reload"):
+        lib.tsfa_config_reload()
+
+
+def _setenv(self, name, value, prepend=None):
+    _mp_setenv(self, name, value, prepend)
+    if str(name).startswith("TSFA_"):
+        _reload_config()
+
+
+def _delenv(self, name, raising=True):
+    _mp_delenv(self, name, raising)
+    if str(name).startswith("TSFA_"):
+        _reload_config()
+
+
+def _undo(self):
+    touched = any(str(getattr(entry, "name", entry[1] if isinstance(entry, tuple) else "")).startswith("TSFA_")
+                  for entry in getattr(self, "_setitem", []))
+    _mp_undo(self)
+    if touched:
+        _reload_config()
+
+
+pytest.MonkeyPatch.setenv = _setenv
+pytest.MonkeyPatch.delenv = _delenv
+pytest.MonkeyPatch.undo = _undo

@@ -31,10 +31,15 @@ def test_prepare_rejects_blocks():
         tsf.prepare_tree_sparse_metadata(torch.ones(4, 4), 0, 16, -1)
 
 
-@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-device error path")
-def test_no_cpu_fallback():
-    with pytest.raises(RuntimeError):
-        tsf.prepare_tree_sparse_metadata(torch.ones(4, 4, dtype=torch.bool), 0, 16, 16)
+def test_forward_has_no_cpu_fallback():
+    # the metadata protocol runs on the host for a CPU mask; the forward
+    # itself refuses host tensors instead of computing on the CPU
+    q = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 8, 64, dtype=torch.bfloat16)
+    meta = tsf.prepare_tree_sparse_metadata(torch.ones(4, 4, dtype=torch.bool), 4, 16, 16)
+    assert meta.row_ptr.device.type == "cpu"
+    with pytest.raises(ValueError):
+        tsf.tree_sparse_attention_fwd(q, k, k, meta)
 
 
 def _hf_mask(q, kv, tree):
