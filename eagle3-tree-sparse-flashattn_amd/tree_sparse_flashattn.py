@@ -330,12 +330,32 @@ class _BlockSparseTreeFwdKernel:
                    num_stages=None, **_unused):
             if BLOCK_D != q_ptr.shape[-1]:
                 raise ValueError(f"BLOCK_D ({BLOCK_D}) must equal head_dim ({q_ptr.shape[-1]})")
-            strides = (stride_qb, stride_qh, stride_qm, stride_qd, stride_kb, stride_kh, stride_kn, stride_kd,
-                       stride_vb, stride_vh, stride_vn, stride_vd, stride_ob, stride_oh, stride_om, stride_od)
-            return _launch_fwd(q_ptr, k_ptr, v_ptr, o_ptr, row_ptr_ptr, col_idx_ptr, blk_type_ptr,
-                               mixed_mask_payload_ptr, mixed_mask_offset_ptr, (0, 0, 0, 0, 0), strides, sm_scale,
-                               batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
-                               n_tree_blocks, gqa_group_size, BLOCK_M, BLOCK_N, BLOCK_D)
+            # the reference addresses each operand by its base pointer and the
+            # strides given here (tree_sparse_flashattn.py:174-189): the same
+            # views of the tensors' storage
+            qv = _strided(q_ptr, (batch_size, num_heads, q_len, BLOCK_D), (stride_qb, stride_qh, stride_qm, stride_qd))
+            kv_shape = (batch_size, num_kv_heads, kv_len, BLOCK_D)
+            kv_ = _strided(k_ptr, kv_shape, (stride_kb, stride_kh, stride_kn, stride_kd))
+            vv = _strided(v_ptr, kv_shape, (stride_vb, stride_vh, stride_vn, stride_vd))
+            ov = _strided(o_ptr, (batch_size, num_heads, q_len, BLOCK_D), (stride_ob, stride_oh, stride_om, stride_od))
+            dp = _padded_dim(BLOCK_D)
+            direct = dp == BLOCK_D and all(_layout_ok(t) for t in (qv, kv_, vv, ov))
+            if direct:
+                qc, kc, vc, oc = qv, kv_, vv, ov
+            else:
+                # head_dim zero-padded to a kernel width (zeros add nothing to
+                # q.k and give zero columns of O) and layouts the kernel does
+                # not address (d stride != 1, unaligned rows) copied
+                qc, kc, vc = (_dense_padded(t, dp) for t in (qv, kv_, vv))
+                oc = torch.empty((batch_size, num_heads, q_len, dp), dtype=ov.dtype, device=ov.device)
+            strides = (*qc.stride(), *kc.stride(), *vc.stride(), *oc.stride())
+            _launch_fwd(qc, kc, vc, oc, row_ptr_ptr, col_idx_ptr, blk_type_ptr, mixed_mask_payload_ptr,
+                        mixed_mask_offset_ptr, (0, 0, 0, 0, 0), strides, sm_scale, batch_size, num_heads,
+                        num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks, gqa_group_size,
+                        BLOCK_M, BLOCK_N, dp)
+            if not direct:
+                ov.copy_(oc[..., :BLOCK_D])
+            return o_ptr
 
         return launch
 
@@ -370,6 +390,34 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor], **sa
             raise ValueError(f"{name} shape {tuple(t.shape)} != {tuple(want)}")
 
 
+# head_dim widths the kernels are built for; narrower dims are zero-padded
+_KERNEL_DIMS = (64, 128)
+
+
+def _padded_dim(d: int) -> int:
+    for w in _KERNEL_DIMS:
+        if d <= w:
+            return w
+    raise NotImplementedError(f"head_dim {d} is above this build's widest kernel ({_KERNEL_DIMS[-1]})")
+
+
+def _strided(t: torch.Tensor, size, stride) -> torch.Tensor:
+    return torch.as_strided(t, size, [int(x) for x in stride])
+
+
+def _layout_ok(t: torch.Tensor) -> bool:
+    # what the kernels address directly: d stride 1, 16-byte aligned rows
+    return t.stride(-1) == 1 and not any(st % 8 for st in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+
+
+def _dense_padded(t: torch.Tensor, width: int) -> torch.Tensor:
+    if t.shape[-1] == width:
+        return t.contiguous() if not _layout_ok(t) else t
+    out = torch.zeros((*t.shape[:-1], width), dtype=t.dtype, device=t.device)
+    out[..., : t.shape[-1]] = t
+    return out
+
+
 def _row_contig(t: torch.Tensor) -> torch.Tensor:
     if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
         return t.contiguous()
@@ -401,6 +449,27 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     split-KV partials buffer (uint8, ``fwd_workspace_bytes`` of the shape).
     """
     _check_qkv(q, k, v, out=out)
+    head_dim = q.shape[-1]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    if _padded_dim(head_dim) != head_dim:
+        # head_dim below a kernel width: zero-padded copies (no change to q.k)
+        dp = _padded_dim(head_dim)
+        res = tree_sparse_attention_fwd(_dense_padded(q, dp), _dense_padded(k, dp), _dense_padded(v, dp), meta,
+                                        sm_scale=sm_scale, return_lse=return_lse, workspace=workspace)
+        o = res[0] if return_lse else res
+        if out is None:
+            out = o[..., :head_dim].contiguous()
+        else:
+            out.copy_(o[..., :head_dim])
+        return (out, res[1]) if return_lse else out
+    if out is not None and not _layout_ok(out):
+        # an output the kernel cannot address (d stride != 1, unaligned rows)
+        # is written through a dense temporary
+        res = tree_sparse_attention_fwd(q, k, v, meta, sm_scale=sm_scale, return_lse=return_lse,
+                                        workspace=workspace)
+        out.copy_(res[0] if return_lse else res)
+        return (out, res[1]) if return_lse else out
     q, k, v = _row_contig(q), _row_contig(k), _row_contig(v)
     bsz, n_heads, q_len, head_dim = q.shape
     _, n_kv_heads, kv_len, _ = k.shape

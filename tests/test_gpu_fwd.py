@@ -244,6 +244,76 @@ def test_reference_grid_launch_and_strided_inputs():
     assert_close_to_oracle(o, oracle_out(q.cpu(), k.cpu(), v.cpu(), mask, P), torch.float16)
 
 
+def _grid_launch(q, k, v, o, meta, P, D, bm, bn):
+    B, H, Q = q.shape[0], q.shape[1], q.shape[2]
+    HKV = k.shape[1]
+    tsf.block_sparse_tree_fwd_kernel[(meta.n_q_blocks, B * H)](
+        q, k, v, o, meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset,
+        q.stride(0), q.stride(1), q.stride(2), q.stride(3), k.stride(0), k.stride(1), k.stride(2), k.stride(3),
+        v.stride(0), v.stride(1), v.stride(2), v.stride(3), o.stride(0), o.stride(1), o.stride(2), o.stride(3),
+        1.0 / math.sqrt(D), B, H, HKV, Q, k.shape[2], P, meta.n_q_blocks, meta.n_tree_blocks, H // HKV,
+        BLOCK_M=bm, BLOCK_N=bn, BLOCK_D=D)
+
+
+@pytest.mark.parametrize("layout", ["d-stride-2", "unaligned-rows", "o-d-stride-2"])
+def test_reference_grid_launch_layouts_the_kernel_does_not_address(layout):
+    # every d stride and row alignment the reference takes
+    # (tree_sparse_flashattn.py:174-189): copied to dense operands, O
+    # written back through a temporary
+    B, H, HKV, D, P, Q = 1, 8, 2, 64, 96, 40
+    g = torch.Generator().manual_seed(3)
+    rng = np.random.default_rng(3)
+    mask = torch.from_numpy(_tree("random", Q, rng))
+    if layout == "d-stride-2":
+        q = torch.randn(B, H, Q, 2 * D, generator=g).bfloat16().cuda()[..., ::2]
+        k = torch.randn(B, HKV, P + Q, 2 * D, generator=g).bfloat16().cuda()[..., ::2]
+        v = torch.randn(B, HKV, P + Q, 2 * D, generator=g).bfloat16().cuda()[..., ::2]
+    else:
+        q, k, v = (x.cuda() for x in _qkv(B, H, HKV, Q, P, D, torch.bfloat16, seed=3))
+    if layout == "unaligned-rows":
+        # rows of 65 elements, a base one element past an allocation's start
+        def shift(t):
+            buf = torch.zeros(t.numel() // D * 65 + 1, dtype=t.dtype, device=t.device)
+            view = buf[1:].as_strided(t.shape, (t.shape[1] * t.shape[2] * 65, t.shape[2] * 65, 65, 1))
+            view.copy_(t)
+            return view
+        q, k, v = shift(q), shift(k), shift(v)
+    if layout == "o-d-stride-2":
+        o = torch.full((B, H, Q, 2 * D), float("nan"), dtype=torch.bfloat16, device="cuda")[..., ::2]
+    else:
+        o = torch.full((B, H, Q, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), P, 16, 16)
+    _grid_launch(q, k, v, o, meta, P, D, 16, 16)
+    torch.cuda.synchronize()
+    err = assert_close_to_oracle(o, oracle_out(q.cpu(), k.cpu(), v.cpu(), mask, P), torch.bfloat16, relative=True)
+    print(f"[fwd] grid launch {layout} max_abs_err {err:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("d", [16, 32, 96])
+def test_head_dims_below_a_kernel_width(d):
+    # the reference takes any power-of-two BLOCK_D (README.md:190): head dims
+    # below 64 / 128 run zero-padded (zeros add nothing to q.k; O sliced)
+    B, H, HKV, P, Q = 2, 4, 2, 70, 33
+    rng = np.random.default_rng(d)
+    mask = torch.from_numpy(_tree("eagle", Q, rng))
+    q, k, v = (x.cuda() for x in _qkv(B, H, HKV, Q, P, d, torch.float16, seed=d))
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), P, 16, 16)
+    o = torch.full_like(q, float("nan"))
+    _grid_launch(q, k, v, o, meta, P, d, 16, 16)
+    out = tsf.tree_sparse_attention_fwd(q, k, v, meta)
+    torch.cuda.synchronize()
+    ref = oracle_out(q.cpu(), k.cpu(), v.cpu(), mask, P)
+    assert_close_to_oracle(o, ref, torch.float16, relative=True)
+    assert_close_to_oracle(out, ref, torch.float16, relative=True)
+    assert out.shape == q.shape
+
+
+def test_head_dim_above_the_widest_kernel_raises():
+    q, k, v = (x.cuda() for x in _qkv(1, 2, 2, 8, 8, 256, torch.bfloat16))
+    with pytest.raises(NotImplementedError):
+        _run(q, k, v, torch.eye(8, dtype=torch.bool), 16, 16)
+
+
 def test_repeat_calls_are_deterministic():
     w = configs.WORKLOADS["llama3-8b-eagle64-p4096"]
     q, k, v = (x.cuda() for x in configs.make_qkv(w))
