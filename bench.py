@@ -12,8 +12,10 @@ the reference kernel.  The calls cycle through enough independent K/V copies
 256 MB Infinity Cache.
 
 Timing: three regions, each K steps captured in one HIP graph (no host
-launch gaps) and bracketed by HIP events on the stream the graph replays on
-(tsfa_fwd_set_kernel_mask selects the kernels a call launches):
+launch gaps), replayed max(5, ceil(100/K)) times, each replay bracketed by a
+synchronisation and HIP events on the stream the graph replays on, the median
+replay reported (tsfa_fwd_set_kernel_mask selects the kernels a call
+launches):
   * full calls (split-KV + combine)  -> value;
   * the combine alone                -> its duration; full - combine = the
                                         split-KV kernel's duration inside real
@@ -29,7 +31,15 @@ roofline     = K/V bytes / split-KV kernel duration in real calls, against
 cpu_baseline = the fp32 dense+mask oracle (benchmark.py:8-35 restated) on the
                host cores, over a bounded sample of calls
 metadata     = the device metadata build (no host synchronisation), graph and
-               eager, beside the CPU oracle builder
+               eager, the library's host builder on a CPU mask, and the CPU
+               oracle builder
+eager        = the drop-in called eagerly as the reference's callers do:
+               run_tree_sparse_kernel(q, k, v, tree_mask) (metadata built per
+               call) and the forward with prebuilt metadata, host cost included
+workloads    = the other forward workloads (16-sequence decode, 1024-token
+               wide tree, 70B layout), each timed like the headline: us per
+               call, split-KV and combine, roofline fraction and bound
+cpu_baseline = also records the host CPU model and the oracle's dtype
 backward     = tree_sparse_attention_bwd (dQ, dK, dV) over the same cycled
                K/V, against the MFMA and HBM peaks
 paged        = the same forward reading FlashInfer's paged cache in place
@@ -103,9 +113,22 @@ def cpu_baseline(w, q, k, v, mask, seconds: float):
         "unit": "TB/s",
         "us_per_call": dt * 1e6,
         "cores": cores,
+        "cpu_model": _cpu_model(),
+        "dtype": "fp32",
         "kind": "port",
         "sample": f"{n} full calls of the fp32 dense+mask oracle on the same inputs (torch CPU, {cores} threads)",
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def metadata_timing(w, mask_dev, mask_cpu, reps: int = 200):
@@ -146,6 +169,14 @@ def metadata_timing(w, mask_dev, mask_cpu, reps: int = 200):
         b.record()
     torch.cuda.synchronize()
     graph_us = a.elapsed_time(b) * 1e3 / reps
+    build_host = (lambda: tsf.prepare_tree_sparse_metadata_batched(mask_cpu, w.prefix_len, w.block_m, w.block_n))
+    build_host()
+    n_host = 0
+    t0 = time.perf_counter()
+    while n_host < 5 or time.perf_counter() - t0 < 0.5:
+        build_host()
+        n_host += 1
+    host_us = (time.perf_counter() - t0) / n_host * 1e6
     masks = mask_cpu.numpy()
     build_cpu = ((lambda: [meta_oracle.build_metadata(m, w.prefix_len, w.block_m, w.block_n) for m in masks])
                  if masks.ndim == 3 else (lambda: meta_oracle.build_metadata(masks, w.prefix_len, w.block_m, w.block_n)))
@@ -157,8 +188,115 @@ def metadata_timing(w, mask_dev, mask_cpu, reps: int = 200):
         n += 1
     cpu_us = (time.perf_counter() - t0) / n * 1e6
     return {"hip_graph_us_per_build": round(graph_us, 3), "hip_eager_us_per_build": round(eager_us, 3),
-            "cpu_oracle_us_per_build": round(cpu_us, 1),
-            "sample": f"{reps} device builds per timing; {n} CPU oracle builds (numpy, 1 thread)"}
+            "host_builder_us_per_build": round(host_us, 1), "cpu_oracle_us_per_build": round(cpu_us, 1),
+            "sample": f"{reps} device builds per timing; {n_host} builds by the library's host builder "
+                      f"(tsfa_meta_build_host, CPU mask); {n} CPU oracle builds (numpy, 1 thread)"}
+
+
+def eager_call_timing(w, qd, ks, vs, mask_dev, meta, reps: int = 200):
+    """The drop-in as the reference's callers use it, eagerly (no graph): the
+    reference call form run_tree_sparse_kernel(q, k, v, tree_mask) -- metadata
+    built on every call, eagle_tree_sparse_bridge.py:95-106 -- and the forward
+    with metadata built once.  us_per_call: wall time per call over `reps`
+    calls with one synchronisation at the end (host cost and device time
+    overlap); host_us_per_call: time for the call to return (launch path)."""
+    import torch
+
+    import eagle_tree_sparse_bridge as bridge
+    import tree_sparse_flashattn as tsf
+
+    out = torch.empty_like(qd)
+    forms = {
+        "reference_call_form": lambda i: bridge.run_tree_sparse_kernel(qd, ks[i % len(ks)], vs[i % len(vs)], mask_dev,
+                                                                        block_m=w.block_m, block_n=w.block_n),
+        "forward_with_metadata": lambda i: tsf.tree_sparse_attention_fwd(qd, ks[i % len(ks)], vs[i % len(vs)], meta,
+                                                                         out=out),
+    }
+    res = {}
+    for name, fn in forms.items():
+        for i in range(10):
+            fn(i)
+        torch.cuda.synchronize()
+        host = 0.0
+        t0 = time.perf_counter()
+        for i in range(reps):
+            h0 = time.perf_counter()
+            fn(i)
+            host += time.perf_counter() - h0
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        res[name] = {"us_per_call": round(wall / reps * 1e6, 2), "host_us_per_call": round(host / reps * 1e6, 2)}
+    res["sample"] = f"{reps} eager calls each, cycling the cold K/V copies; one synchronisation at the end"
+    return res
+
+
+def workload_timing(name: str, steps: int, cold_mib: int):
+    """One forward workload (split-KV + combine) timed as the headline is:
+    graph of `steps` calls, the combine alone, cold K/V copies."""
+    import torch
+
+    from tsfa import _lib, configs
+    import tree_sparse_flashattn as tsf
+
+    w = configs.WORKLOADS[name]
+    dev = torch.device("cuda", 0)
+    q, k, v = configs.make_qkv(w)
+    mask = configs.make_tree_mask(w)
+    kvb = w.kv_bytes()
+    copies = max(1, min(64, math.ceil(cold_mib * 2 ** 20 / kvb)))
+    qd = q.to(dev)
+    ks = [k.to(dev) for _ in range(copies)]
+    vs = [v.to(dev) for _ in range(copies)]
+    build = tsf.prepare_tree_sparse_metadata_batched if w.per_sequence else tsf.prepare_tree_sparse_metadata
+    meta = build(mask.to(dev), w.prefix_len, w.block_m, w.block_n)
+    out = torch.empty_like(qd)
+    lib = _lib.load()
+
+    def call(i):
+        tsf.tree_sparse_attention_fwd(qd, ks[i % copies], vs[i % copies], meta, out=out)
+
+    for i in range(3):
+        call(i)
+    torch.cuda.synchronize()
+    secs = {}
+    for region, kmask in (("full", 3), ("combine", 2)):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        _lib.check("tsfa_fwd_set_kernel_mask", lib.tsfa_fwd_set_kernel_mask(kmask))
+        try:
+            with torch.cuda.stream(s):
+                call(0)
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    for i in range(steps):
+                        call(i)
+        finally:
+            _lib.check("tsfa_fwd_set_kernel_mask", lib.tsfa_fwd_set_kernel_mask(3))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            a.record()
+            g.replay()
+            b.record()
+        torch.cuda.synchronize()
+        secs[region] = a.elapsed_time(b) / 1e3 / steps
+        del g
+    split_s = secs["full"] - secs["combine"]
+    flops = algorithmic_flops(w, mask)
+    mfma_bound = flops / kvb > RIDGE_FLOP_PER_BYTE
+    tflops, gbps = flops / split_s / 1e12, kvb / split_s / 1e9
+    del ks, vs
+    torch.cuda.empty_cache()
+    return {"us_per_call": round(secs["full"] * 1e6, 2), "split_kernel_us": round(split_s * 1e6, 2),
+            "combine_kernel_us": round(secs["combine"] * 1e6, 2), "bound": "mfma" if mfma_bound else "hbm",
+            "frac": round(tflops / MFMA_PEAK_TFLOPS if mfma_bound else gbps / HBM_PEAK_GBPS, 4),
+            "achieved": round(tflops, 1) if mfma_bound else round(gbps, 1),
+            "unit": "TFLOP/s" if mfma_bound else "GB/s", "algorithmic_flops": flops, "algorithmic_bytes": kvb,
+            "steps": steps, "kv_copies_cycled": copies,
+            "plan": _lib.fwd_plan(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len, w.head_dim)}
 
 
 def paged_timing(w, qd, ks, vs, meta, steps: int, page_size: int, contiguous_us: float):
@@ -298,6 +436,9 @@ def main():
     ap.add_argument("--no-backward", action="store_true", help="skip the backward timing")
     ap.add_argument("--paged-page-size", type=int, default=16,
                     help="also time the paged-cache forward at this page size (0: skip)")
+    ap.add_argument("--workloads", default="batched-decode-b16-p2048:100,wide-tree-1024-p16384:10,"
+                    "llama3-70b-b4-p32768:5",
+                    help="other forward workloads timed into the `workloads` object, as name:steps ('' skips)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (rocprofv3 PMC calibration) and exit")
     args = ap.parse_args()
@@ -362,19 +503,29 @@ def main():
         torch.cuda.synchronize()
         return g, s
 
+    # each region: `reps` replays of its graph of exactly `steps` calls,
+    # synchronised on both sides; the median replay is reported (at least
+    # 100 calls over the replays)
+    reps = max(5, math.ceil(100 / steps))
+
     def timed(g, s):
         g.replay()  # upload / warm
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(s):
-            a.record()
-            g.replay()
-            b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / 1e3
+        out_s = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                a.record()
+                g.replay()
+                b.record()
+            torch.cuda.synchronize()
+            out_s.append(a.elapsed_time(b) / 1e3)
+        return sorted(out_s)
 
     regions = {name: capture(mask) for name, mask in (("full", 3), ("combine", 2), ("split", 1))}
-    secs = {name: timed(*gs) / steps for name, gs in regions.items()}
+    samples = {name: timed(*gs) for name, gs in regions.items()}
+    secs = {name: v[len(v) // 2] / steps for name, v in samples.items()}
     per_call_s = secs["full"]
     split_avg_s = secs["full"] - secs["combine"]
     _log(f"[bench] {steps} calls: {per_call_s * 1e6:.2f} us/call = split-KV {split_avg_s * 1e6:.2f} + combine "
@@ -405,8 +556,14 @@ def main():
             "batch": w.batch, "q_heads": w.q_heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
             "prefix_len": w.prefix_len, "tree_len": w.tree_len, "block_m": w.block_m, "block_n": w.block_n,
             "kv_bytes_per_call": kvb, "kv_copies_cycled": copies, "plan": plan,
-            "timing": "hip graph of all steps; HIP events on the replay stream",
+            "timing": f"hip graph of all steps, replayed {reps} times (median replay); HIP events on the replay "
+                      "stream",
         },
+        "samples": {"replays": reps, "calls_per_replay": steps,
+                    "us_per_call": [round(x / steps * 1e6, 3) for x in samples["full"]],
+                    "median_us_per_call": round(per_call_s * 1e6, 3),
+                    "min_us_per_call": round(samples["full"][0] / steps * 1e6, 3),
+                    "max_us_per_call": round(samples["full"][-1] / steps * 1e6, 3)},
         "roofline": {
             "bound": "mfma" if mfma_bound else "hbm",
             "kernel": "tsfa::fwd::split_kernel",
@@ -425,19 +582,32 @@ def main():
         },
         "cpu_baseline": None,
         "metadata": None,
+        "eager": None,
+        "workloads": None,
         "paged": None,
         "backward": None,
     }
     _log("[bench] metadata build ...")
     result["metadata"] = metadata_timing(w, mask.to(dev), mask)
+    _log("[bench] eager calls ...")
+    result["eager"] = eager_call_timing(w, qd, ks, vs, mask.to(dev), meta)
     if not args.no_backward:
         _log("[bench] backward ...")
         result["backward"] = backward_timing(w, mask, qd, ks, vs, meta, steps, flops,
                                              0.0 if args.no_cpu_baseline else min(5.0, args.cpu_seconds))
     if args.paged_page_size > 0:
         _log(f"[bench] paged cache, page_size {args.paged_page_size} ...")
-        del regions
+        regions = None
         result["paged"] = paged_timing(w, qd, ks, vs, meta, steps, args.paged_page_size, per_call_s * 1e6)
+    others = [x for x in args.workloads.split(",") if x and x.split(":")[0] != w.name]
+    if others:
+        regions = None
+        torch.cuda.empty_cache()
+        result["workloads"] = {}
+        for item in others:
+            name, _, n = item.partition(":")
+            _log(f"[bench] workload {name} ...")
+            result["workloads"][name] = workload_timing(name, int(n or 10), args.cold_mib)
     if not args.no_cpu_baseline:
         _log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, q, k, v, mask, args.cpu_seconds)

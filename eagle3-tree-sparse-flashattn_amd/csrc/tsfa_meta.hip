@@ -37,8 +37,23 @@ using meta::meta_geom;
 constexpr int kSmallBlocks = 256;
 constexpr int kSmallWords = 8192;  // 32 KB of packed words in LDS
 
+// Nonzero bytes of x (4 mask bytes, first byte lowest) as bits 0-3: the
+// high bit of each byte of (x & 0x7f7f7f7f) + 0x7f7f7f7f | x is set iff the
+// byte is nonzero; the multiply moves bits 7, 15, 23, 31 to 28..31 (its other
+// partial products land on distinct positions below 28, so no carry reaches
+// them).
+__device__ inline uint32_t nonzero_nibble(uint32_t x) {
+  const uint32_t t = ((((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x) & 0x80808080u);
+  return (t * 0x00204081u) >> 28;
+}
+
 // Bits [32*wi, 32*wi + 32) of block (qb, tb) of the sequence whose mask
 // starts at m0, zero-padded past the block's clipped h x w extent (:44-64).
+// When the 32 bits are one run of a block row inside the clipped block, the
+// 32 mask bytes come in two 16-byte loads (aligned) or 32 independent byte
+// loads; otherwise every byte load is issued before any is used (addresses
+// clamped to the block's first byte where the bit is padding), so a word
+// costs one memory latency.
 __device__ inline uint32_t block_word(const uint8_t* m0, int64_t row_stride, const MetaGeom& g, int qb, int tb,
                                       int wi) {
   const int q0 = qb * g.block_m, k0 = tb * g.block_n;
@@ -46,14 +61,41 @@ __device__ inline uint32_t block_word(const uint8_t* m0, int64_t row_stride, con
   const int w = min(g.block_n, g.q_len - k0);
   const uint8_t* m = m0 + (int64_t)q0 * row_stride + k0;
   const int64_t n_flat = (int64_t)g.block_m * g.block_n;
-  int64_t flat = (int64_t)wi * 32;
-  int r = (int)(flat / g.block_n);
-  int c = (int)(flat - (int64_t)r * g.block_n);
-  uint32_t word = 0;
-  for (int i = 0; i < 32 && flat + i < n_flat; ++i) {
-    if (r < h && c < w && m[(int64_t)r * row_stride + c] != 0) word |= 1u << i;
-    if (++c == g.block_n) { c = 0; ++r; }
+  const int64_t flat = (int64_t)wi * 32;
+  const int r0 = (int)(flat / g.block_n);
+  const int c0 = (int)(flat - (int64_t)r0 * g.block_n);
+  if (r0 < h && c0 + 32 <= w && flat + 32 <= n_flat) {
+    const uint8_t* p = m + (int64_t)r0 * row_stride + c0;
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+      const uint4 a = *reinterpret_cast<const uint4*>(p);
+      const uint4 b = *reinterpret_cast<const uint4*>(p + 16);
+      return nonzero_nibble(a.x) | nonzero_nibble(a.y) << 4 | nonzero_nibble(a.z) << 8 |
+             nonzero_nibble(a.w) << 12 | nonzero_nibble(b.x) << 16 | nonzero_nibble(b.y) << 20 |
+             nonzero_nibble(b.z) << 24 | nonzero_nibble(b.w) << 28;
+    }
+    uint8_t v[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = p[i];
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) word |= (uint32_t)(v[i] != 0) << i;
+    return word;
   }
+  uint8_t v[32];
+  bool in[32];
+  int r = r0, c = c0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    in[i] = flat + i < n_flat && r < h && c < w;
+    v[i] = m[in[i] ? (int64_t)r * row_stride + c : 0];
+    if (++c == g.block_n) {
+      c = 0;
+      ++r;
+    }
+  }
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) word |= (uint32_t)(in[i] && v[i] != 0) << i;
   return word;
 }
 
