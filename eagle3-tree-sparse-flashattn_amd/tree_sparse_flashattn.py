@@ -151,31 +151,51 @@ def _pack_block_mask_to_int32(mask_2d: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# validated geometry and buffer layout of metadata builds, by shape and block size
+_META_GEOMETRY: dict = {}
+
+
 def _meta_build(masks_u8: torch.Tensor, block_m: int, block_n: int, dev: torch.device):
     """tsfa_meta_build over [n_seq, q_len, q_len] uint8 masks on `dev` (a HIP
     device), or tsfa_meta_build_host when `dev` is the CPU."""
     lib = _lib.load()
     n_seq, q_len = masks_u8.shape[0], masks_u8.shape[1]
-    _lib.check("prepare_tree_sparse_metadata", lib.tsfa_meta_check_args(n_seq, q_len, block_m, block_n))
-    nqb = (q_len + block_m - 1) // block_m
-    ntb = (q_len + block_n - 1) // block_n
-    words = (block_m * block_n + 31) // 32
-    cap = nqb * ntb
-    i32 = dict(dtype=torch.int32, device=dev)
-    row_ptr = torch.empty((n_seq, nqb + 1), **i32)
-    col_idx = torch.empty((n_seq, cap), **i32)
-    blk_type = torch.empty((n_seq, cap), dtype=torch.int8, device=dev)
-    payload = torch.empty((n_seq, cap * words), **i32)
-    offset = torch.empty((n_seq, cap), **i32)
-    counts = torch.empty((n_seq, 2), **i32)
+    geo_key = (n_seq, q_len, block_m, block_n, dev.type)
+    geo = _META_GEOMETRY.get(geo_key)
+    if geo is None:
+        _lib.check("prepare_tree_sparse_metadata", lib.tsfa_meta_check_args(n_seq, q_len, block_m, block_n))
+        nqb = (q_len + block_m - 1) // block_m
+        ntb = (q_len + block_n - 1) // block_n
+        words = (block_m * block_n + 31) // 32
+        cap = nqb * ntb
+        # one allocation holds the six outputs (256-byte aligned sections)
+        # and, on a device, the build's workspace
+        sections = ((n_seq * (nqb + 1), torch.int32), (n_seq * cap, torch.int32), (n_seq * cap, torch.int8),
+                    (n_seq * cap * words, torch.int32), (n_seq * cap, torch.int32), (n_seq * 2, torch.int32))
+        ws_bytes = 0 if dev.type == "cpu" else lib.tsfa_meta_workspace_bytes(n_seq, q_len, block_m, block_n)
+        spans, at = [], 0
+        for n, dt in sections:
+            nbytes = n * (4 if dt == torch.int32 else 1)
+            spans.append((at, at + nbytes, dt))
+            at += (nbytes + 255) // 256 * 256
+        geo = (nqb, ntb, words, cap, tuple(spans), at, ws_bytes)
+        if len(_META_GEOMETRY) >= 64:
+            _META_GEOMETRY.clear()
+        _META_GEOMETRY[geo_key] = geo
+    nqb, ntb, words, cap, spans, at, ws_bytes = geo
+    buf = torch.empty((at + max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    views = [buf[a:b].view(dt) for a, b, dt in spans]
+    row_ptr = views[0].view(n_seq, nqb + 1)
+    col_idx, blk_type, offset = (views[i].view(n_seq, cap) for i in (1, 2, 4))
+    payload = views[3].view(n_seq, cap * words)
+    counts = views[5].view(n_seq, 2)
     if dev.type == "cpu":
         st = lib.tsfa_meta_build_host(_lib.ptr(masks_u8), masks_u8.stride(0), masks_u8.stride(1), n_seq, q_len,
                                       block_m, block_n, _lib.ptr(row_ptr), _lib.ptr(col_idx), _lib.ptr(blk_type),
                                       _lib.ptr(payload), _lib.ptr(offset), _lib.ptr(counts))
         _lib.check("prepare_tree_sparse_metadata", st)
         return row_ptr, col_idx, blk_type, payload, offset, counts, nqb, ntb
-    ws_bytes = lib.tsfa_meta_workspace_bytes(n_seq, q_len, block_m, block_n)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    ws = buf[at:]
     with torch.cuda.device(dev):
         st = lib.tsfa_meta_build(_lib.ptr(masks_u8), masks_u8.stride(0), masks_u8.stride(1), n_seq, q_len,
                                  block_m, block_n, _lib.ptr(row_ptr), _lib.ptr(col_idx), _lib.ptr(blk_type),
@@ -448,7 +468,14 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     tree_sparse_attention_bwd needs.  ``workspace`` optionally supplies the
     split-KV partials buffer (uint8, ``fwd_workspace_bytes`` of the shape).
     """
+    # repeated calls of one geometry skip the host checks the first call made
+    # (the C entry point still validates every argument)
+    key = _fwd_key(q, k, v, meta, out, return_lse)
+    entry = _FWD_CALLS.get(key)
+    if entry is not None:
+        return _fwd_cached(entry, q, k, v, meta, sm_scale, out, return_lse, workspace)
     _check_qkv(q, k, v, out=out)
+    q_in, k_in, v_in = q, k, v
     head_dim = q.shape[-1]
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(head_dim)
@@ -483,6 +510,64 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     _launch_fwd(q, k, v, out, *tensors, meta_strides, strides, sm_scale, bsz, n_heads, n_kv_heads, q_len,
                 kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, n_heads // n_kv_heads,
                 meta.block_m, meta.block_n, head_dim, lse=lse, workspace=workspace)
+    if key is not None and q is q_in and k is k_in and v is v_in:
+        # the geometry ran as given (no copies): remember its launch arguments
+        if len(_FWD_CALLS) >= 64:
+            _FWD_CALLS.clear()
+        lib = _lib.load()
+        _FWD_CALLS[key] = (
+            _lib.i64_array(meta_strides), _lib.i64_array(strides),
+            (bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks,
+             n_heads // n_kv_heads, meta.block_m, meta.block_n, head_dim, _lib.dtype_code(q.dtype)),
+            lib.tsfa_fwd_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, head_dim),
+            1.0 / math.sqrt(head_dim))
+    return (out, lse) if return_lse else out
+
+
+# launch arguments of forward geometries already validated, by _fwd_key
+_FWD_CALLS: dict = {}
+
+
+def reload_config() -> None:
+    """Re-read the TSFA_* environment switches (the library reads them once)
+    and forget launch arguments planned under the old ones."""
+    _lib.check("tsfa_config_reload", _lib.load().tsfa_config_reload())
+    _FWD_CALLS.clear()
+
+
+def _fwd_key(q, k, v, meta, out, return_lse):
+    """Everything a forward's validation and launch arguments depend on,
+    pointers excepted (their 16-byte alignment included)."""
+    if not (q.is_cuda and k.is_cuda and v.is_cuda) or (out is not None and not out.is_cuda):
+        return None
+    tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
+    align = q.data_ptr() | k.data_ptr() | v.data_ptr() | (0 if out is None else out.data_ptr())
+    return (q.shape, q.stride(), k.shape, k.stride(), v.shape, v.stride(), q.dtype, k.dtype, v.dtype,
+            None if out is None else (out.shape, out.stride(), out.dtype), align & 15, q.device,
+            tuple(t.device for t in tensors), type(meta), getattr(meta, "n_trees", 0),
+            tuple(t.stride(0) for t in tensors) if isinstance(meta, BatchedTreeSparseMetadata) else None,
+            meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks, meta.block_m, meta.block_n, return_lse)
+
+
+def _fwd_cached(entry, q, k, v, meta, sm_scale, out, return_lse, workspace):
+    meta_strides, strides, args, ws_bytes, default_scale = entry
+    lib = _lib.load()
+    dev = q.device
+    if out is None:
+        out = torch.empty_like(q)
+    ws = _workspace(workspace, ws_bytes, dev)
+    scale = default_scale if sm_scale is None else float(sm_scale)
+    tensors = (meta.row_ptr, meta.col_idx, meta.blk_type, meta.mixed_mask_payload, meta.mixed_mask_offset)
+    ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), *(t.data_ptr() for t in tensors))
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        if return_lse:
+            lse = torch.empty((args[0], args[1], args[3]), dtype=torch.float32, device=dev)
+            st = lib.tsfa_fwd_lse(*ptrs[:4], lse.data_ptr(), *ptrs[4:], meta_strides, strides, scale, *args,
+                                  ws.data_ptr(), ws_bytes, stream)
+        else:
+            st = lib.tsfa_fwd(*ptrs, meta_strides, strides, scale, *args, ws.data_ptr(), ws_bytes, stream)
+    _lib.check("block_sparse_tree_fwd_kernel", st)
     return (out, lse) if return_lse else out
 
 

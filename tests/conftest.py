@@ -29,12 +29,10 @@ _mp_setenv, _mp_delenv, _mp_undo = pytest.MonkeyPatch.setenv, pytest.MonkeyPatch
 
 def _reload_config():
     try:
-        from tsfa import _lib
-        lib = _lib.load()
-    except Exception:  # library not built: nothing to reload
-        return
-    if hasattr(lib, "tsfa_config_reload"):
-        lib.tsfa_config_reload()
+        import tree_sparse_flashattn as tsf
+        tsf.reload_config()
+    except Exception:  # library not built (or host-only): nothing to reload
+        pass
 
 
 def _setenv(self, name, value, prepend=None):
