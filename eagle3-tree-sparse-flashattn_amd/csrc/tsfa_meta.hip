@@ -16,8 +16,10 @@
 // packs words and counts bits; `compact` (one workgroup per sequence) scans
 // the block classes and scatters the CSR arrays and MIXED payload.  A tree
 // whose packed words fit in LDS (at most kSmallBlocks blocks and
-// kSmallWords words: every EAGLE draft tree) takes one launch instead:
-// `build_small` packs, classifies and compacts a sequence in one workgroup.
+// kSmallWords words) takes one launch instead: `build_small` packs,
+// classifies and compacts a sequence in one workgroup, and `build_tree`
+// does so for at most 64 blocks (every EAGLE draft tree) with ballots in
+// place of the block-wide scan.
 
 #include <stdlib.h>
 
@@ -36,6 +38,7 @@ using meta::meta_geom;
 
 constexpr int kSmallBlocks = 256;
 constexpr int kSmallWords = 8192;  // 32 KB of packed words in LDS
+constexpr int kTreeBlocks = 64;    // one wave's lanes
 
 // Nonzero bytes of x (4 mask bytes, first byte lowest) as bits 0-3: the
 // high bit of each byte of (x & 0x7f7f7f7f) + 0x7f7f7f7f | x is set iff the
@@ -54,16 +57,14 @@ __device__ inline uint32_t nonzero_nibble(uint32_t x) {
 // loads; otherwise every byte load is issued before any is used (addresses
 // clamped to the block's first byte where the bit is padding), so a word
 // costs one memory latency.
-__device__ inline uint32_t block_word(const uint8_t* m0, int64_t row_stride, const MetaGeom& g, int qb, int tb,
-                                      int wi) {
+// (r0, c0): row and column of the word's first bit, flat = 32 * wi.
+__device__ inline uint32_t block_word_at(const uint8_t* m0, int64_t row_stride, const MetaGeom& g, int qb, int tb,
+                                         int64_t flat, int r0, int c0) {
   const int q0 = qb * g.block_m, k0 = tb * g.block_n;
   const int h = min(g.block_m, g.q_len - q0);
   const int w = min(g.block_n, g.q_len - k0);
   const uint8_t* m = m0 + (int64_t)q0 * row_stride + k0;
   const int64_t n_flat = (int64_t)g.block_m * g.block_n;
-  const int64_t flat = (int64_t)wi * 32;
-  const int r0 = (int)(flat / g.block_n);
-  const int c0 = (int)(flat - (int64_t)r0 * g.block_n);
   if (r0 < h && c0 + 32 <= w && flat + 32 <= n_flat) {
     const uint8_t* p = m + (int64_t)r0 * row_stride + c0;
     if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
@@ -97,6 +98,13 @@ __device__ inline uint32_t block_word(const uint8_t* m0, int64_t row_stride, con
 #pragma unroll
   for (int i = 0; i < 32; ++i) word |= (uint32_t)(in[i] && v[i] != 0) << i;
   return word;
+}
+
+__device__ inline uint32_t block_word(const uint8_t* m0, int64_t row_stride, const MetaGeom& g, int qb, int tb,
+                                      int wi) {
+  const int64_t flat = (int64_t)wi * 32;
+  const int r0 = (int)(flat / g.block_n);
+  return block_word_at(m0, row_stride, g, qb, tb, flat, r0, (int)(flat - (int64_t)r0 * g.block_n));
 }
 
 // ZERO / FULL / MIXED from the set-bit count of a block (:113-124).
@@ -250,6 +258,76 @@ __global__ __launch_bounds__(kMetaThreads) void build_small_kernel(
   compact_seq(g, seq, s_cls, s_words, s_rank, row_ptr, col_idx, blk_type, payload, offset, counts);
 }
 
+// Arguments of build_tree_kernel, with the divisors its threads use.
+struct TreeArgs {
+  const uint8_t* mask;
+  int64_t seq_stride, row_stride;
+  MetaGeom g;
+  FastDiv fd_words, fd_ntb, fd_block_n;
+  int32_t* row_ptr;
+  int32_t* col_idx;
+  int8_t* blk_type;
+  int32_t* payload;
+  int32_t* offset;
+  int32_t* counts;
+};
+
+__device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One workgroup per sequence of at most kTreeBlocks blocks (an EAGLE draft
+// tree): packed words and block bit counts in LDS; then every wave
+// classifies the blocks, lane i block i, and ranks the present and the MIXED
+// blocks by ballot and popcount of the lanes below, so each thread places
+// the packed words it owns from the ballot alone -- no block-wide scan, two
+// barriers in all.
+__global__ __launch_bounds__(kMetaThreads) void build_tree_kernel(TreeArgs a) {
+  __shared__ int32_t s_words[kSmallWords];
+  __shared__ int s_ones[kTreeBlocks];
+  const MetaGeom& g = a.g;
+  const int seq = blockIdx.x;
+  const int nb = (int)g.cap, n_words = nb * g.words;
+  if (threadIdx.x < kTreeBlocks) s_ones[threadIdx.x] = 0;
+  sync_lds();
+  const uint8_t* m0 = a.mask + seq * a.seq_stride;
+  for (int e = threadIdx.x; e < n_words; e += kMetaThreads) {
+    const int blk = (int)fdiv(e, a.fd_words), wi = e - blk * g.words;
+    const int qb = (int)fdiv(blk, a.fd_ntb), tb = blk - qb * g.ntb;
+    const int flat = wi * 32, r0 = (int)fdiv(flat, a.fd_block_n);
+    const uint32_t word = block_word_at(m0, a.row_stride, g, qb, tb, flat, r0, flat - r0 * g.block_n);
+    s_words[e] = (int32_t)word;
+    if (word != 0) atomicAdd(&s_ones[blk], __popc(word));
+  }
+  sync_lds();
+  const int lane = threadIdx.x & 63;
+  const int qb = (int)fdiv(lane, a.fd_ntb), tb = lane - qb * g.ntb;
+  const int8_t c = lane < nb ? block_class(g, qb, tb, s_ones[lane]) : kZero;
+  const uint64_t nz = __ballot(c != kZero), mx = __ballot(c == kMixed);
+  if (threadIdx.x < 64) {
+    const int nz_below = __builtin_amdgcn_mbcnt_hi((uint32_t)(nz >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)nz, 0));
+    const int mx_below = __builtin_amdgcn_mbcnt_hi((uint32_t)(mx >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mx, 0));
+    int32_t* rp = a.row_ptr + (int64_t)seq * (g.nqb + 1);
+    if (lane < nb && tb == 0) rp[qb] = nz_below;  // present blocks before row qb
+    if (c != kZero) {
+      a.col_idx[(int64_t)seq * nb + nz_below] = tb;
+      a.blk_type[(int64_t)seq * nb + nz_below] = (c == kFull) ? TSFA_FULL_BLOCK : TSFA_MIXED_BLOCK;
+      a.offset[(int64_t)seq * nb + nz_below] = (c == kMixed) ? mx_below * g.words : 0;
+    }
+    if (lane == 0) {
+      rp[g.nqb] = __popcll(nz);
+      a.counts[2 * seq] = __popcll(nz);
+      a.counts[2 * seq + 1] = __popcll(mx);
+    }
+  }
+  int32_t* pl = a.payload + (int64_t)seq * nb * g.words;
+  for (int e = threadIdx.x; e < n_words; e += kMetaThreads) {
+    const int blk = (int)fdiv(e, a.fd_words);
+    if ((mx >> blk) & 1) {
+      const int rank = __popcll(mx & ((1ull << blk) - 1));  // MIXED blocks before blk
+      pl[rank * g.words + (e - blk * g.words)] = s_words[e];
+    }
+  }
+}
+
 __global__ void pack_bits_kernel(const uint8_t* __restrict__ bits, int64_t n_bits, int32_t* __restrict__ words,
                                  int64_t n_words) {
   const int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -291,6 +369,24 @@ extern "C" int tsfa_meta_build(const uint8_t* mask, int64_t mask_seq_stride, int
       reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(nb) + align256(nb * g.words * 4));
   const bool small = g.cap > 0 && g.cap <= kSmallBlocks && g.cap * g.words <= kSmallWords &&
                      config().meta_small != 0;  // TSFA_META_SMALL=0: always two launches
+  if (small && g.cap <= kTreeBlocks) {
+    TreeArgs ta;
+    ta.mask = mask;
+    ta.seq_stride = mask_seq_stride;
+    ta.row_stride = mask_row_stride;
+    ta.g = g;
+    ta.fd_words = make_fastdiv((uint32_t)g.words);
+    ta.fd_ntb = make_fastdiv((uint32_t)g.ntb);
+    ta.fd_block_n = make_fastdiv((uint32_t)g.block_n);
+    ta.row_ptr = row_ptr;
+    ta.col_idx = col_idx;
+    ta.blk_type = blk_type;
+    ta.payload = payload;
+    ta.offset = offset;
+    ta.counts = counts;
+    hipLaunchKernelGGL(build_tree_kernel, dim3((unsigned)n_seq), dim3(kMetaThreads), 0, stream, ta);
+    return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+  }
   if (small) {
     hipLaunchKernelGGL(build_small_kernel, dim3((unsigned)n_seq), dim3(kMetaThreads), 0, stream, mask,
                        mask_seq_stride, mask_row_stride, g, row_ptr, col_idx, blk_type, payload, offset, counts);

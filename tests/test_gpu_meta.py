@@ -40,7 +40,8 @@ def _sweep_cases():
     rng = np.random.default_rng(7)
     cases = []
     for q_len, bm, bn in [(1, 16, 16), (64, 16, 64), (100, 32, 48), (37, 16, 16), (130, 64, 64), (129, 1, 1),
-                          (70, 3, 5), (256, 128, 128), (33, 7, 32), (200, 64, 16), (64, 256, 8)]:
+                          (70, 3, 5), (256, 128, 128), (33, 7, 32), (200, 64, 16), (64, 256, 8),
+                          (64, 4, 16), (96, 8, 8)]:  # 64 blocks (one wave ranks them), 144 (block-wide scan)
         for kind in ("random", "tree", "ones", "zeros", "eye"):
             cases.append((q_len, bm, bn, kind, int(rng.integers(1 << 30))))
     return cases

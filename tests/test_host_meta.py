@@ -41,7 +41,7 @@ def _mask(kind, q_len, rng):
 
 
 SHAPES = [(0, 16, 16), (1, 16, 16), (64, 16, 64), (100, 32, 48), (37, 16, 16), (130, 64, 64), (129, 1, 1),
-          (70, 3, 5), (256, 128, 128), (33, 7, 32), (200, 64, 16), (64, 256, 8)]
+          (70, 3, 5), (256, 128, 128), (33, 7, 32), (200, 64, 16), (64, 256, 8), (64, 4, 16), (96, 8, 8)]
 
 
 @pytest.mark.parametrize("kind", ["random", "tree", "ones", "zeros", "eye"])
