@@ -61,6 +61,7 @@ namespace fwd {
 // kWaves, kMaxRows, kUnitKeys, kRingBytes, kMaskWords, kMaxTreeUnits and
 // kMiscInts come from tsfa_plan.h (the planner sizes the grid and LDS by them)
 constexpr float kRescaleLog2 = 8.0f;
+constexpr int kOneShotSync = 2;  // steps between the barriers of a one-shot prefix run
 
 // Per-workgroup timestamps for timeline measurements: compiled in only with
 // -DTSFA_STAMPS (a separate measurement build); TSFA_STAMP is empty otherwise.
@@ -69,6 +70,12 @@ __device__ unsigned long long g_stamps[4096 * 64];
 #define TSFA_STAMP(k)                                                                      \
   do {                                                                                     \
     if (threadIdx.x == 0) g_stamps[(size_t)blockIdx.x * 64 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+// slot k + wave, written by lane 0 of every wave
+#define TSFA_STAMPW(k)                                                                               \
+  do {                                                                                               \
+    if ((threadIdx.x & 63) == 0)                                                                     \
+      g_stamps[(size_t)blockIdx.x * 64 + (k) + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 // Per-wave cycle sums of loop phases (s_memtime deltas; each reading waits
 // for the wave's outstanding LDS/scalar loads, so this build perturbs the loop).
@@ -88,6 +95,9 @@ __device__ unsigned long long g_cyc[4096 * 32];
 #else
 #define TSFA_STAMP(k) \
   do {            \
+  } while (0)
+#define TSFA_STAMPW(k) \
+  do {             \
   } while (0)
 #define TSFA_CYC_DECL
 #define TSFA_CYC(k) \
@@ -525,7 +535,8 @@ void split_kernel(const SplitArgs a) {
   static_assert(NS >= 4 && (NS & (NS - 1)) == 0 && LPU >= 1 && LPU * (NS - 2) < 64 && LPH % (RG / 2) == 0,
                 "ring geometry");
   static_assert(QS >= 1 && QS < NS && QROWS * ROWB == QS * SB, "Q staging");
-  static_assert(S == 1 || kWaves * DT * 64 * 64 / 2 + ROWS * ROWB <= kRingBytes, "merge buffer");
+  static_assert(S == 1 || (kWaves * (DT / 2) * 4 * 64 * 16 <= kRingBytes && S * ROWS * 8 <= kMaskWords * 4),
+                "stream merge buffers");
 
   extern __shared__ __attribute__((aligned(256))) unsigned char smem[];  // stage bases keep bits 0-7 clear
   unsigned char* ring = smem;
@@ -542,6 +553,7 @@ void split_kernel(const SplitArgs a) {
   const int item = work_item(a);
   if (item < 0) return;
   TSFA_STAMP(0);
+  TSFA_STAMPW(52);
 #ifdef TSFA_STAMPS
   if (threadIdx.x == 0) g_stamps[(size_t)blockIdx.x * 64 + 63] = (unsigned long long)item;
 #endif
@@ -1048,11 +1060,18 @@ void split_kernel(const SplitArgs a) {
       read_k(ring + (stage(0) - ring_lds), kf);
       s_cur = qk(kf);
     }
-    // unit j+1 landed for every wave of the stream; ring stage (j-1)%NS is free
+    // Ring: unit j+1 landed for every wave of the stream; ring stage
+    // (j-1)%NS is free.  One-shot: no stage is reused, so the waves meet
+    // every kOneShotSync steps only, each time for the units of those steps
+    // (units up to j + kOneShotSync landed); fewer barriers let the two
+    // waves of a SIMD drift apart.
     auto ring_step = [&](int j) {
-      if (j + 1 < mine) {
-        if (oneshot) wait_units<LPU, NOS - S>(mine - 2 - j);
-        else wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
+      if (oneshot) {
+        if (j % kOneShotSync != 0) return;
+        const int last = min(j + kOneShotSync, mine - 1);
+        if (j + 1 < mine) wait_units<LPU, NOS - S>(mine - 1 - last);
+      } else if (j + 1 < mine) {
+        wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
       }
       __builtin_amdgcn_sched_barrier(0);
       sync_lds();
@@ -1108,9 +1127,12 @@ void split_kernel(const SplitArgs a) {
       const int early = min(n, NOS - S), first = min(early, max(a.os_first, S));
       pre = early > ks ? (early - ks + S - 1) / S : 0;
       const int pre1 = first > ks ? (first - ks + S - 1) / S : 0;
+      TSFA_STAMP(62);
       issue_q(true);
       for (int j = 0; j < pre1; ++j) issue_at(stage(j), key0_of(ks + S * j));
+      TSFA_STAMP(60);
       wait_units<LPU, NOS - S>(pre1);
+      TSFA_STAMPW(35);
       for (int j = pre1; j < pre; ++j) issue_at(stage(j), key0_of(ks + S * j));
       sync_lds();
       TSFA_STAMP(1);
@@ -1226,84 +1248,94 @@ void split_kernel(const SplitArgs a) {
     }
   }
 
-  // Epilogue.  With two streams, stream 1 leaves (m, l) and O^T of its rows in
-  // LDS and stream 0 merges them into its own (log-sum-exp).  Each row's
-  // owner normalises and stages the row in the input dtype; then all waves
-  // store whole rows (1 KB per instruction).
+  // Epilogue.  With two streams, each stream merges (log-sum-exp) half the
+  // d-tiles of its rows: it leaves (m, l) and O^T of the other half in LDS
+  // for the other stream, then folds in the other stream's.  Every lane then
+  // normalises its own O^T elements and stores them straight into the
+  // partial row (8 bytes per element quad; a row's 16-byte pieces come from
+  // lanes l and l+32 of one instruction), so the partial needs no LDS
+  // staging pass.
   sync_all();
   TSFA_STAMP(50);
-  float2* mls = reinterpret_cast<float2*>(masks);                   // [row group][32]
-  unsigned char* stg = ring + (S == 2 ? kRingBytes - ROWS * ROWB : 0);  // [ROWS][D], chunks swizzled
-  if (S == 2 && ks == 1) {
-    const float lt = pair_sum(l_run);
-    if (lh == 0) mls[rg * 32 + ln] = make_float2(m_run, lt);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16) =
-            f32x4{o[dt][4 * q], o[dt][4 * q + 1], o[dt][4 * q + 2], o[dt][4 * q + 3]};
-  }
-  if (S == 2) sync_lds();
+  typedef T T4 __attribute__((ext_vector_type(4)));
   const int64_t part_row0 = ((int64_t)bk * a.n_slots + slot) * TG + row0;
-  if (ks == 0) {
-    const float lt = pair_sum(l_run);
-    float M = m_run, L = lt, w0 = 1.f, w1 = 0.f;
-    if (S == 2) {
-      const float2 other = mls[rg * 32 + ln];
-      M = fmaxf(m_run, other.x);
-      // weights 2^((m_s - M) * scale); 0 for a stream that saw no key
-      w0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - M) * sl2);
-      w1 = (other.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((other.x - M) * sl2);
-      L = w0 * lt + w1 * other.y;
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;  // empty partial: O = 0, weight 0 in the combine
-    const int r = rg * 32 + ln;
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    // stream 1's O^T, read before any staging write (the staging rows share
-    // the ring, so interleaved reads and writes would serialise on LDS)
-    f32x4 xo[DT][4];
-    if (S == 2) {
+  const int r = rg * 32 + ln;  // the lane's chunk row
+  T* dst = static_cast<T*>(a.ws_o) + (part_row0 + r) * D;
+  const bool row_ok = r < rows_chunk;
+  // Quads e (d = 8q + 4lh + [0,4), q = 2p) and f (q = 2p+1) of one row in
+  // lanes l and l+32 become 16 contiguous bytes per lane: lane l takes
+  // d = 16p + [0,8) (its e and the partner's), lane l+32 d = 16p + [8,16)
+  // (the partner's f and its own), by one row-swap per dword.
+  auto store16 = [&](T* row_p16, const T4& e, const T4& f) {
+    const auto w0 = __builtin_amdgcn_permlane32_swap(bit_cast<uint2>(e).x, bit_cast<uint2>(f).x, false, false);
+    const auto w1 = __builtin_amdgcn_permlane32_swap(bit_cast<uint2>(e).y, bit_cast<uint2>(f).y, false, false);
+    if (row_ok) *reinterpret_cast<uint4*>(row_p16 + 8 * lh) = uint4{w0[0], w1[0], w0[1], w1[1]};
+  };
+  const float lt = pair_sum(l_run);
+  if constexpr (S == 2) {
+    constexpr int DH = DT / 2;
+    float2* mls = reinterpret_cast<float2*>(masks);  // [stream][row]
+    // O^T of d-tiles [DH*(1-ks), DH*(1-ks) + DH), lane-major: the other
+    // stream's wave of row group rg reads the same lane positions
+    auto xbuf = [&](int src_ks, int dl, int q) {
+      return ring + ((((src_ks * RG + rg) * DH + dl) * 4 + q) * 64 + lane) * 16;
+    };
+    if (lh == 0) mls[ks * ROWS + r] = make_float2(m_run, lt);
+    // stream KS keeps d-tiles [DH*KS, DH*KS + DH) (compile-time indices:
+    // a runtime index into o[] would move the accumulators to scratch)
+    auto merge = [&](auto ks_c) {
+      constexpr int KS = decltype(ks_c)::value, GIVE = DH * (1 - KS), KEEP = DH * KS;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int dl = 0; dl < DH; ++dl)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          xo[dt][q] = *reinterpret_cast<const f32x4*>(ring + (((rg * DT + dt) * 4 + q) * 64 + lane) * 16);
-    }
+          *reinterpret_cast<f32x4*>(xbuf(KS, dl, q)) =
+              f32x4{o[GIVE + dl][4 * q], o[GIVE + dl][4 * q + 1], o[GIVE + dl][4 * q + 2], o[GIVE + dl][4 * q + 3]};
+      sync_lds();
+      const float2 other = mls[(1 - KS) * ROWS + r];
+      f32x4 xo[DH][4];
+#pragma unroll
+      for (int dl = 0; dl < DH; ++dl)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xo[dl][q] = *reinterpret_cast<const f32x4*>(xbuf(1 - KS, dl, q));
+      const float M = fmaxf(m_run, other.x);
+      // weights 2^((m_s - M) * scale); 0 for a stream that saw no key
+      const float w0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - M) * sl2);
+      const float w1 = (other.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((other.x - M) * sl2);
+      const float L = w0 * lt + w1 * other.y;
+      const float inv = L > 0.f ? 1.f / L : 0.f;  // empty partial: O = 0, weight 0 in the combine
+      const float a0 = w0 * inv, a1 = w1 * inv;
+#pragma unroll
+      for (int dl = 0; dl < DH; ++dl)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          T4 e, f;  // element quads q = 2p, 2p+1
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            e[i] = (T)(a0 * o[KEEP + dl][8 * p + i] + a1 * xo[dl][2 * p][i]);
+            f[i] = (T)(a0 * o[KEEP + dl][8 * p + 4 + i] + a1 * xo[dl][2 * p + 1][i]);
+          }
+          store16(dst + (KEEP + dl) * 32 + 16 * p, e, f);
+        }
+      if (KS == 0 && lh == 0 && row_ok) a.ws_ml[part_row0 + r] = make_float2(M, L);
+    };
+    if (ks == 0) merge(std::integral_constant<int, 0>{});
+    else merge(std::integral_constant<int, 1>{});
+  } else {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        T4 v4;
-        if (S == 2) {
-          const f32x4 x = xo[dt][q];
+      for (int p = 0; p < 2; ++p) {
+        T4 e, f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v4[i] = (T)((w0 * o[dt][4 * q + i] + w1 * x[i]) * inv);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v4[i] = (T)(o[dt][4 * q + i] * inv);
+        for (int i = 0; i < 4; ++i) {
+          e[i] = (T)(o[dt][8 * p + i] * inv);
+          f[i] = (T)(o[dt][8 * p + 4 + i] * inv);
         }
-        *reinterpret_cast<T4*>(stg + r * ROWB + (((4 * dt + q) ^ swz_k<D>(r)) << 4) + 8 * lh) = v4;
+        store16(dst + dt * 32 + 16 * p, e, f);
       }
-    if (lh == 0 && r < rows_chunk) a.ws_ml[part_row0 + r] = make_float2(M, L);
-  }
-  sync_lds();
-  // Whole rows out, 1 KB per wave instruction; the LDS reads go first so they
-  // overlap instead of each waiting on its own round trip.
-  constexpr int CPR = D / 8;
-  constexpr int NIT = ROWS * CPR / (kWaves * 64);
-  static_assert(NIT * kWaves * 64 == ROWS * CPR, "staging loop");
-  T* dst = static_cast<T*>(a.ws_o) + part_row0 * D;
-  i16x8 rowv[NIT];
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int idx = tid + it * kWaves * 64, r = idx / CPR, c = idx % CPR;
-    rowv[it] = *reinterpret_cast<const i16x8*>(stg + r * ROWB + ((c ^ swz_k<D>(r)) << 4));
-  }
-#pragma unroll
-  for (int it = 0; it < NIT; ++it) {
-    const int idx = tid + it * kWaves * 64, r = idx / CPR, c = idx % CPR;
-    if (r < rows_chunk) *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) = rowv[it];
+    if (lh == 0 && row_ok) a.ws_ml[part_row0 + r] = make_float2(m_run, lt);
   }
   TSFA_STAMP(51);
   TSFA_CYC_STORE;
