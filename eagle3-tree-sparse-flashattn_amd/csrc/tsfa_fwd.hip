@@ -593,6 +593,7 @@ void split_kernel(const SplitArgs a) {
   // only waits.  Latency under load is ~2.5 us, so a ring that requests a
   // unit two steps ahead stalls every step on short runs.
   constexpr int NOS = (kRingBytes + kMaskWords * 4) / SB;
+  constexpr bool RING2 = NS >= 8;  // ring loop meets every other step
   static_assert(S == 1 || QS == 1, "one-shot Q staging: one stage per stream");
   static_assert(NOS <= 32 && (NOS - S) * LPU < 64, "one-shot geometry");
   // LDS address of the stage of the stream's unit j: ring stage j % NS, or
@@ -1048,9 +1049,11 @@ void split_kernel(const SplitArgs a) {
       sync_lds();
       for (int j = pre; j < mine; ++j) issue_at(stage(j), key0_of(ks + S * j));
     } else {
-      for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + S * j));
-      if (PAGED && NS - 1 < mine) prefetch(key0_of(ks + S * (NS - 1)));
-      if (mine > 0) wait_units<LPU, NS - 2>(min(mine - 1, NS - 2));  // unit 0 landed
+      // RING2: NS-2 units ahead, two issued at every other step
+      constexpr int AHEAD = RING2 ? NS - 2 : NS - 1;
+      for (int j = pre; j < AHEAD && j < mine; ++j) issue(j, key0_of(ks + S * j));
+      if (PAGED && AHEAD < mine) prefetch(key0_of(ks + S * AHEAD));
+      if (mine > 0) wait_units<LPU, NS - 2>(min(mine, AHEAD) - 1);  // unit 0 landed
       sync_lds();
     }
     TSFA_STAMP(2);
@@ -1065,20 +1068,34 @@ void split_kernel(const SplitArgs a) {
     // every kOneShotSync steps only, each time for the units of those steps
     // (units up to j + kOneShotSync landed); fewer barriers let the two
     // waves of a SIMD drift apart.
+    // RING2 (rings of at least 8 stages): the same with the waves meeting
+    // every other step, units up to j+2 landed and stages (j-2)%NS and
+    // (j-1)%NS refilled at even steps j.
     auto ring_step = [&](int j) {
       if (oneshot) {
         if (j % kOneShotSync != 0) return;
         const int last = min(j + kOneShotSync, mine - 1);
         if (j + 1 < mine) wait_units<LPU, NOS - S>(mine - 1 - last);
-      } else if (j + 1 < mine) {
-        wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
+      } else if constexpr (RING2) {
+        if (j & 1) return;
+        // issued: units below min(mine, j + NS - 2)
+        if (j + 1 < mine) wait_units<LPU, NS - 5>(max(min(mine - j - 3, NS - 5), 0));
+      } else {
+        if (j + 1 < mine) wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
       }
       __builtin_amdgcn_sched_barrier(0);
       sync_lds();
       __builtin_amdgcn_sched_barrier(0);
       if (j < 40) TSFA_STAMP(3 + j);
       TSFA_CYC(2);
-      if (!oneshot && j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+      if (!oneshot) {
+        if constexpr (RING2) {
+          if (j + NS - 2 < mine) issue((j + NS - 2) % NS, key0_of(ks + S * (j + NS - 2)));
+          if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+        } else if (j + NS - 1 < mine) {
+          issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+        }
+      }
       if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
       __builtin_amdgcn_sched_barrier(0);
     };
