@@ -966,6 +966,18 @@ void split_kernel(const SplitArgs a) {
       pb[e >> 3][e & 7] = (T)p[e];
       pb[e >> 3][(e & 7) + 1] = (T)p[e + 1];
     };
+    // P V MFMA g of group 2: d-tile and k-step, ordered by k-step (keys 0-15
+    // of every d-tile, then keys 16-31), so the second half of the
+    // exponentials (P^T of keys 16-31) runs under the first half of the P V
+    // MFMAs instead of all of them under the S^T MFMAs (2 % at the 8B shape,
+    // 1 % at the 1024-token tree in one A/B; the same sums in the same order)
+    auto pv_dt = [&](int g) { return g % DT; };
+    auto pv_s2 = [&](int g) { return g / DT; };
+    auto rv2 = [&](int g) {  // V^T fragments of P V MFMA g
+      rv(pv_dt(g) * 4 + pv_s2(g) * 2);
+      rv(pv_dt(g) * 4 + pv_s2(g) * 2 + 1);
+    };
+    constexpr int NG1 = 4;  // exponential pairs in group 1 (keys 0-15)
     if constexpr (NEXT) {
       // group 1 in explicit order: K of unit j+1 read two k-steps ahead of
       // its MFMAs; the statistics above and then the exponentials and
@@ -978,29 +990,31 @@ void split_kernel(const SplitArgs a) {
       kf[1] = rk(1);
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_out[i] = 0.f;
-      constexpr int K0 = KSTEPS / 4;  // steps that carry the statistics; the 8 exponential pairs spread over the rest
+      constexpr int K0 = KSTEPS / 4;  // steps that carry the statistics; the exponential pairs spread over the rest
 #pragma unroll
       for (int kk = 0; kk < KSTEPS; ++kk) {
         if (kk + 2 < KSTEPS) kf[kk + 2] = rk(kk + 2);
         s_out = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[kk]), s_out);
         if (kk >= K0) {
 #pragma unroll
-          for (int pr = (kk - K0) * 8 / (KSTEPS - K0); pr < (kk - K0 + 1) * 8 / (KSTEPS - K0); ++pr) expo2(2 * pr);
+          for (int pr = (kk - K0) * NG1 / (KSTEPS - K0); pr < (kk - K0 + 1) * NG1 / (KSTEPS - K0); ++pr) expo2(2 * pr);
         }
-        if (kk == KSTEPS - 1)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rv(r);
+        if (kk == KSTEPS - 1) {
+          rv2(0);
+          rv2(1);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
-      // P exists here: the exponentials and conversions stay in group 1 (its
-      // block ends at the mask branch) instead of sinking into group 2
-      asm volatile("" : "+v"(pb[0]), "+v"(pb[1]));
+      // P (its group-1 half) exists here: the exponentials and conversions
+      // stay in group 1 (its block ends at the mask branch) instead of
+      // sinking into group 2
+      asm volatile("" : "+v"(pb[0]));
       TSFA_CYC(0);
     } else {
+      rv2(0);
+      rv2(1);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) rv(r);
-#pragma unroll
-      for (int pr = 0; pr < 8; ++pr) expo2(2 * pr);
+      for (int pr = 0; pr < NG1; ++pr) expo2(2 * pr);
     }
     // O re-base for unit j: after P V of unit j-1 (issued an iteration ago),
     // before that of unit j
@@ -1009,28 +1023,29 @@ void split_kernel(const SplitArgs a) {
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
     if constexpr (NEXT) TSFA_CYC(3);
-    // group 2 in explicit order: MFMA g with V^T of MFMA g+2 read behind it
-    // and a share of the row sum of unit j
+    // group 2 in explicit order: MFMA g with V^T of MFMA g+2 read behind it,
+    // the remaining exponentials under the k-step-0 MFMAs and the row sum
+    // of unit j under the k-step-1 MFMAs
 #pragma unroll
     for (int g = 0; g < NPV; ++g) {
-      if (2 * (g + 2) < 4 * DT) {
-        rv(2 * (g + 2));
-        rv(2 * (g + 2) + 1);
-      }
-      const int dt = g >> 1, s2 = g & 1;
+      if (g + 2 < NPV) rv2(g + 2);
+      const int dt = pv_dt(g), s2 = pv_s2(g);
       const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
       o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
-      // tree sum of p: 8 + 4 + 2 + 1 adds spread over the MFMAs
-      if (g == 0)
+      if (g < DT) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = p[i] + p[i + 8];
-      if (g == 1)
+        for (int pr = NG1 + g * (8 - NG1) / DT; pr < NG1 + (g + 1) * (8 - NG1) / DT; ++pr) expo2(2 * pr);
+        if (g == DT - 1) asm volatile("" : "+v"(pb[1]));
+      }
+      // tree sum of p: 8 + 4 + 2 + 1 adds over the k-step-1 MFMAs
+      const int h = g - DT;
+      if (h == 0)
 #pragma unroll
-        for (int i = 4; i < 8; ++i) p[i] = p[i] + p[i + 8];
-      if (g == 2)
+        for (int i = 0; i < 8; ++i) p[i] = p[i] + p[i + 8];
+      if (h == DT / 2)
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = p[i] + p[i + 4];
-      if (g == 3) {
+      if (h == DT - 1) {
         p[0] = p[0] + p[2];
         p[1] = p[1] + p[3];
         l_run += p[0] + p[1];
