@@ -80,7 +80,13 @@ void config_reload() {
 namespace fwd {
 
 // Kernel, key streams per workgroup, prefix run length (units per split) and
-// the grid.  The 8-wave kernel: two key streams of 128-row chunks below 1024
+// the grid.  Runs are chosen by the makespan model below, which counts the
+// short tree items apart from the prefix runs: one round of 256-unit runs
+// with the tree folded in beats 5 splits of 103 on the 1024-token wide tree
+// (338 -> 306 us per call), one 1024-unit run beats 8 of 128 on the 70B
+// shape (1243 -> 1180 us), one 64-unit run beats 2 of 32 on the 16-sequence
+// decode shape (71 -> 66 us; same-box A/B).  The 8-wave kernel: two key
+// streams of 128-row chunks below 1024
 // rows per (batch, kv head), one stream of 256-row chunks from 1024 rows on
 // (TSFA_STREAMS=1/2 forces one or two).  One stream loads each K/V unit once
 // for 256 rows, halving the loads per MFMA and leaving six units in flight
@@ -109,19 +115,28 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   if (p->n_pu > 0) {
     ups = cfg.prefix_units;
     if (ups <= 0) {
-      // Makespan model (microseconds): one workgroup per CU; a workgroup
-      // costs a fixed start/finish plus its longest stream; every slot of
-      // partials is written once and read once by the combine.
-      const double t_unit = (p->wide ? 0.6 : 0.5) * head_dim / 128.0, t_fixed = 1.5;
+      // Makespan model (microseconds, measured on MI355X): one workgroup per
+      // CU, dispatched as CUs free up; a workgroup costs a fixed start/finish
+      // plus one step per unit of its stream (a step is the same MFMA work
+      // with one or two streams); every slot of partials is written once and
+      // read once by the combine.  The prefix runs go out first: after their
+      // full rounds, the last partial round of runs and the (shorter) tree
+      // items share the CUs.  A tree item runs only its visible units,
+      // estimated as 60 % of the tree's.
+      const double t_step = (p->wide ? 1.4 : 1.15) * head_dim / 128.0, t_fixed = 5.0;
       const double part_bytes = (double)batch * num_heads * q_len * (2.0 * head_dim + 8.0);
+      const int64_t tree_units = ceil_div(std::max(0, kv_len - prefix_len), kUnitKeys);
+      const double c_tree =
+          t_fixed + 0.6 * (double)ceil_div((int)std::min<int64_t>(tree_units, INT32_MAX), p->streams) * t_step;
       double best = 1e300;
       for (int cand = 1; cand <= p->n_pu; ++cand) {
         const int64_t splits = ceil_div(p->n_pu, cand);
         if (cand > 1 && ceil_div(p->n_pu, cand - 1) == splits) continue;
-        const int64_t items = groups * (splits + 1);
-        const int64_t rounds = (items + cus - 1) / cus;
-        const double cost = (double)rounds * (t_fixed + ceil_div(cand, p->streams) * t_unit) +
-                            part_bytes * (double)(splits + 1) * 2.0 / 5.0e6;
+        const double c_run = t_fixed + ceil_div(cand, p->streams) * t_step;
+        const int64_t runs = groups * splits, full = runs / cus, rest = runs % cus;
+        const double tail = rest > 0 ? std::max(c_run, (double)((groups + cus - rest - 1) / (cus - rest)) * c_tree)
+                                     : (double)((groups + cus - 1) / cus) * c_tree;
+        const double cost = (double)full * c_run + tail + part_bytes * (double)(splits + 1) * 2.0 / 5.0e6;
         if (cost < best * (1.0 - 1e-9)) {
           best = cost;
           ups = cand;

@@ -62,19 +62,21 @@ def test_noalloc_matches_tsfa_fwd_on_two_calls():
 
 
 def test_noalloc_refuses_calls_past_its_array():
-    # the 70B shape's partials exceed the array: refused on the host before
-    # any launch (the data pointers are never read, so none are passed)
+    # the 70B layout at 32 sequences: its partials (at least one slot of
+    # 32*64*256 rows) exceed the array, so the call is refused on the host
+    # before any launch (the data pointers are never read, so none are passed)
     w = configs.WORKLOADS["llama3-70b-b4-p32768"]
+    batch = 32
     lib = _lib.load()
-    need = lib.tsfa_fwd_workspace_bytes(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len,
+    need = lib.tsfa_fwd_workspace_bytes(batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len,
                                         w.head_dim)
-    print(f"[noalloc] {w.name} needs {need} bytes", flush=True)
+    print(f"[noalloc] {w.name} at {batch} sequences needs {need} bytes", flush=True)
     assert need > NOALLOC_MAX_BYTES
     nqb = -(-w.tree_len // w.block_m)
     ntb = -(-w.tree_len // w.block_n)
     strides = (0,) * 16
     st = lib.tsfa_fwd_noalloc(None, None, None, None, None, None, None, None, None, _lib.i64_array((0,) * 5),
-                              _lib.i64_array(strides), 0.088, w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len,
+                              _lib.i64_array(strides), 0.088, batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len,
                               w.prefix_len, nqb, ntb, w.q_heads // w.kv_heads, w.block_m, w.block_n, w.head_dim,
                               _lib.dtype_code(w.dtype), None)
     assert st == _lib.TSFA_ERR_WORKSPACE
