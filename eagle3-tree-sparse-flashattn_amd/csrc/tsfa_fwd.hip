@@ -2292,6 +2292,9 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   // folded: the last run of each chunk carries the tree units, the longest
   // items, so those go first (longest first)
   if (p.fold_tree && order < 0) sa.item_order = sa.item_order ? 2 : 0;
+  // one round (every XCD's items start together): the order cannot matter,
+  // and the natural one costs each wave no scalar divisions to decode
+  if (order < 0 && (int64_t)p.items_per_xcd * 8 <= cus) sa.item_order = 0;
 
   CombineArgs ca;
   ca.o = o;
