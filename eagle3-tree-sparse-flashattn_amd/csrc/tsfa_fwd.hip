@@ -1054,7 +1054,7 @@ void split_kernel(const SplitArgs a) {
     }
     if constexpr (NEXT) TSFA_CYC(1);
   };
-  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
+  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     if (oneshot) {
@@ -1062,11 +1062,11 @@ void split_kernel(const SplitArgs a) {
       // every wave has read Q (the barrier below)
       if (mine > 0) wait_units<LPU, NOS - S>(pre - 1);  // unit 0 landed
       sync_lds();
-      for (int j = pre; j < mine; ++j) issue_at(stage(j), key0_of(ks + S * j));
+      for (int j = pre; j < mine; ++j) issue_of(stage(j), ks + S * j);
     } else {
       // RING2: NS-2 units ahead, two issued at every other step
       constexpr int AHEAD = RING2 ? NS - 2 : NS - 1;
-      for (int j = pre; j < AHEAD && j < mine; ++j) issue(j, key0_of(ks + S * j));
+      for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(sring_lds + j * SB, ks + S * j);
       if (PAGED && AHEAD < mine) prefetch(key0_of(ks + S * AHEAD));
       if (mine > 0) wait_units<LPU, NS - 2>(min(mine, AHEAD) - 1);  // unit 0 landed
       sync_lds();
@@ -1105,10 +1105,10 @@ void split_kernel(const SplitArgs a) {
       TSFA_CYC(2);
       if (!oneshot) {
         if constexpr (RING2) {
-          if (j + NS - 2 < mine) issue((j + NS - 2) % NS, key0_of(ks + S * (j + NS - 2)));
-          if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+          if (j + NS - 2 < mine) issue_of(sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
+          if (j + NS - 1 < mine) issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
         } else if (j + NS - 1 < mine) {
-          issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
+          issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
         }
       }
       if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
@@ -1127,8 +1127,9 @@ void split_kernel(const SplitArgs a) {
     // no later load targets it (a load into it would be of unit >= mine).
     if (mine > 0 && active) pipe_iter(mine - 1, ks + S * (mine - 1), std::false_type{}, s_cur, s_cur, masked_of, mask_of);
   };
-  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
-    if constexpr (PIPE) run_units_pipe(n, pre, key0_of, masked_of, mask_of);
+  // issue_of(lds stage, i) requests run unit i (keys key0_of(i)) into a stage
+  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of) {
+    if constexpr (PIPE) run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of);
     else run_units(n, pre, key0_of, masked_of, mask_of);
   };
 
@@ -1144,6 +1145,26 @@ void split_kernel(const SplitArgs a) {
     auto key0_of = [&](int i) {
       const int r = i + rot;
       return (u_lo + (r >= n ? r - n : r)) * kUnitKeys;
+    };
+    // Contiguous K/V: run unit i's row pointer is this wave's base for the
+    // run plus one product (the general path rebuilds it from the key with
+    // 64-bit scalar arithmetic and range checks, on the scalar unit the
+    // workgroup's waves share); units reaching past kv_len take that path.
+    // (Set up for ring runs only: a one-shot run issues its few units in the
+    // prologue, where the setup would delay Q.)
+    int64_t unit_bytes = 0;
+    const char* run_rows = nullptr;
+    int n_fast = 0;
+    uint32_t m0_off = 0;
+    auto issue_prefix = [&](uint32_t sb, int i) {
+      const int r = i + rot, ri = r >= n ? r - n : r;
+      if (!PAGED && !oneshot && ri < n_fast) {
+        const char* rowp = run_rows + ri * unit_bytes;
+        if (kv_nt) dma_rows<LPU, true>(rowp, doff, sb + m0_off);
+        else dma_rows<LPU, false>(rowp, doff, sb + m0_off);
+      } else {
+        issue_at(sb, key0_of(i));
+      }
     };
     // Q and the first NS-QS units of each stream leave together; wait for Q
     // only (loads complete in order), then every wave reads its fragments.
@@ -1161,18 +1182,22 @@ void split_kernel(const SplitArgs a) {
       const int pre1 = first > ks ? (first - ks + S - 1) / S : 0;
       TSFA_STAMP(62);
       issue_q(true);
-      for (int j = 0; j < pre1; ++j) issue_at(stage(j), key0_of(ks + S * j));
+      for (int j = 0; j < pre1; ++j) issue_prefix(stage(j), ks + S * j);
       TSFA_STAMP(60);
       wait_units<LPU, NOS - S>(pre1);
       TSFA_STAMPW(35);
-      for (int j = pre1; j < pre; ++j) issue_at(stage(j), key0_of(ks + S * j));
+      for (int j = pre1; j < pre; ++j) issue_prefix(stage(j), ks + S * j);
       sync_lds();
       TSFA_STAMP(1);
       read_q(true);
     } else {
       pre = min(mine, NS - QS);
       issue_q(false);
-      for (int j = 0; j < pre; ++j) issue(j, key0_of(ks + S * j));
+      unit_bytes = (int64_t)kUnitKeys * dstride * (int64_t)sizeof(T);
+      run_rows = reinterpret_cast<const char*>(dbase + ((int64_t)u_lo * kUnitKeys + dma_u0 * DRPL) * dstride);
+      n_fast = rows_fast ? max(0, min(n, a.kv_len / kUnitKeys - u_lo)) : 0;
+      m0_off = dlds + (uint32_t)dma_u0 * 1024u;
+      for (int j = 0; j < pre; ++j) issue_prefix(sring_lds + j * SB, ks + S * j);
       wait_units<LPU, NS - QS>(pre);
       sync_lds();
       TSFA_STAMP(1);
@@ -1181,7 +1206,7 @@ void split_kernel(const SplitArgs a) {
     }
     units(
         n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
-        [&](int i) { return (1u << (P - key0_of(i))) - 1u; });
+        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix);
     // a folded tree phase runs on the rings
     oneshot = false;
     st_base = sring_lds;
@@ -1273,9 +1298,10 @@ void split_kernel(const SplitArgs a) {
         reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
       }
       sync_lds();
+      auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
       units(
-          nb, 0, [&](int i) { return P + vis[vb0 + i] * kUnitKeys; }, [&](int) { return true; },
-          [&](int i) { return masks[row_tt * a.vt_max + i]; });
+          nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
+          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); });
       sync_all();  // ring and masks free for the next batch
     }
   }
