@@ -512,8 +512,11 @@ __device__ inline int work_item(const SplitArgs& a) {
 }
 
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  PIPE
-// selects the software-pipelined unit loop (run_units_pipe).
-template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false>
+// selects the software-pipelined unit loop (run_units_pipe).  FAST (one
+// stream, contiguous K/V, every prefix unit full, no non-temporal hint):
+// prefix runs issue every unit by the run-base path and skip the per-unit
+// mask test, and their steady ring steps use a fixed wait count.
+template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, bool FAST = false>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
@@ -1054,7 +1057,7 @@ void split_kernel(const SplitArgs a) {
     }
     if constexpr (NEXT) TSFA_CYC(1);
   };
-  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of) {
+  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     if (oneshot) {
@@ -1093,6 +1096,24 @@ void split_kernel(const SplitArgs a) {
         if (j + 1 < mine) wait_units<LPU, NOS - S>(mine - 1 - last);
       } else if constexpr (RING2) {
         if (j & 1) return;
+        if constexpr (decltype(fast_c)::value) {
+          // steady state (both refill units exist): fixed wait, unchecked
+          // refills -- scalar work and branches here stall the wave's
+          // MFMA issue (measured ~8 cycles per scalar instruction and
+          // ~35 per taken branch per unit in a replica of this loop)
+          if (j + NS - 1 < mine) {
+            vm_wait<(NS - 5) * LPU>();
+            __builtin_amdgcn_sched_barrier(0);
+            sync_lds();
+            __builtin_amdgcn_sched_barrier(0);
+            if (j < 40) TSFA_STAMP(3 + j);
+            TSFA_CYC(2);
+            issue_of(sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
+            issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            return;
+          }
+        }
         // issued: units below min(mine, j + NS - 2)
         if (j + 1 < mine) wait_units<LPU, NS - 5>(max(min(mine - j - 3, NS - 5), 0));
       } else {
@@ -1128,8 +1149,8 @@ void split_kernel(const SplitArgs a) {
     if (mine > 0 && active) pipe_iter(mine - 1, ks + S * (mine - 1), std::false_type{}, s_cur, s_cur, masked_of, mask_of);
   };
   // issue_of(lds stage, i) requests run unit i (keys key0_of(i)) into a stage
-  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of) {
-    if constexpr (PIPE) run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of);
+  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
+    if constexpr (PIPE) run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c);
     else run_units(n, pre, key0_of, masked_of, mask_of);
   };
 
@@ -1158,7 +1179,9 @@ void split_kernel(const SplitArgs a) {
     uint32_t m0_off = 0;
     auto issue_prefix = [&](uint32_t sb, int i) {
       const int r = i + rot, ri = r >= n ? r - n : r;
-      if (!PAGED && !oneshot && ri < n_fast) {
+      if constexpr (FAST) {
+        dma_rows<LPU, false>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
+      } else if (!PAGED && !oneshot && ri < n_fast) {
         const char* rowp = run_rows + ri * unit_bytes;
         if (kv_nt) dma_rows<LPU, true>(rowp, doff, sb + m0_off);
         else dma_rows<LPU, false>(rowp, doff, sb + m0_off);
@@ -1205,8 +1228,12 @@ void split_kernel(const SplitArgs a) {
       if (QS > 1) sync_lds();
     }
     units(
-        n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
-        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix);
+        n, pre, key0_of,
+        [&](int i) {
+          if constexpr (FAST) return false;
+          else return P - key0_of(i) < kUnitKeys;
+        },
+        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix, std::bool_constant<FAST>{});
     // a folded tree phase runs on the rings
     oneshot = false;
     st_base = sring_lds;
@@ -1301,7 +1328,7 @@ void split_kernel(const SplitArgs a) {
       auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
       units(
           nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
-          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); });
+          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, std::false_type{});
       sync_all();  // ring and masks free for the next batch
     }
   }
@@ -2007,7 +2034,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
   merge_row<T, D, NB>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR));
 }
 
-template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false>
+template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, bool FAST = false>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -2016,12 +2043,12 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32, PIPE>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32, PIPE, FAST>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32, PIPE>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream,
+  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32, PIPE, FAST>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream,
                      args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
@@ -2046,6 +2073,16 @@ int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
 
+// One-stream contiguous runs whose prefix units are all full and need no
+// non-temporal hint take the kernel with the unchecked prefix ring steps
+// (split_kernel<..., FAST = true>).  Every prefix unit lies below kv_len
+// (prefix_len <= kv_len), and the run-base path needs a row stride of at
+// least D in both K and V.
+template <int D> inline bool fast_ring(const SplitArgs& sa, const Plan& p) {
+  return config().fast_ring != 0 && p.streams == 1 && sa.prefix_len % kUnitKeys == 0 && !sa.kv_nt && sa.skn >= D &&
+         sa.svn >= D;
+}
+
 // The paged forward always runs the 8-wave split kernel.
 template <typename T, int D, bool PAGED>
 int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
@@ -2063,7 +2100,8 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
            : p.streams == 2   ? (pipe ? launch_split<T, D, 2, false, false, true>(sa, p, stream)
                                       : launch_split<T, D, 2, false>(sa, p, stream))
-                              : (pipe ? launch_split<T, D, 1, false, false, true>(sa, p, stream)
+                              : (pipe ? (fast_ring<D>(sa, p) ? launch_split<T, D, 1, false, false, true, true>(sa, p, stream)
+                                                          : launch_split<T, D, 1, false, false, true>(sa, p, stream))
                                       : launch_split<T, D, 1, false>(sa, p, stream));
     if (st != TSFA_OK) return st;
   }
