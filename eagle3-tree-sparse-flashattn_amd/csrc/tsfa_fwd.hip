@@ -512,11 +512,12 @@ __device__ inline int work_item(const SplitArgs& a) {
 }
 
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  PIPE
-// selects the software-pipelined unit loop (run_units_pipe).  FAST (one
-// stream, contiguous K/V, every prefix unit full, no non-temporal hint):
-// prefix runs issue every unit by the run-base path and skip the per-unit
-// mask test, and their steady ring steps use a fixed wait count.
-template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, bool FAST = false>
+// selects the software-pipelined unit loop (run_units_pipe).  FAST
+// (contiguous K/V, every prefix unit full; 1: plain loads, 2: non-temporal
+// K/V loads): prefix runs skip the per-unit mask test, ring runs issue every
+// unit by the run-base path, and their steady ring steps use a fixed wait
+// count.
+template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   typedef typename Mma<T>::vec8 V8;
@@ -1117,6 +1118,20 @@ void split_kernel(const SplitArgs a) {
         // issued: units below min(mine, j + NS - 2)
         if (j + 1 < mine) wait_units<LPU, NS - 5>(max(min(mine - j - 3, NS - 5), 0));
       } else {
+        if constexpr (decltype(fast_c)::value) {
+          // steady state (the refill unit exists): fixed wait, unchecked refill
+          if (j + NS - 1 < mine) {
+            vm_wait<(NS - 3) * LPU>();
+            __builtin_amdgcn_sched_barrier(0);
+            sync_lds();
+            __builtin_amdgcn_sched_barrier(0);
+            if (j < 40) TSFA_STAMP(3 + j);
+            TSFA_CYC(2);
+            issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            return;
+          }
+        }
         if (j + 1 < mine) wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1179,8 +1194,11 @@ void split_kernel(const SplitArgs a) {
     uint32_t m0_off = 0;
     auto issue_prefix = [&](uint32_t sb, int i) {
       const int r = i + rot, ri = r >= n ? r - n : r;
-      if constexpr (FAST) {
-        dma_rows<LPU, false>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
+      if constexpr (FAST != 0) {
+        // one-shot runs (two streams only) issue by the general path: their
+        // run base is not set up, to keep Q's request first
+        if (!(S == 2 && oneshot)) dma_rows<LPU, FAST == 2>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
+        else issue_at(sb, key0_of(i));
       } else if (!PAGED && !oneshot && ri < n_fast) {
         const char* rowp = run_rows + ri * unit_bytes;
         if (kv_nt) dma_rows<LPU, true>(rowp, doff, sb + m0_off);
@@ -1230,10 +1248,10 @@ void split_kernel(const SplitArgs a) {
     units(
         n, pre, key0_of,
         [&](int i) {
-          if constexpr (FAST) return false;
+          if constexpr (FAST != 0) return false;
           else return P - key0_of(i) < kUnitKeys;
         },
-        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix, std::bool_constant<FAST>{});
+        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix, std::bool_constant<FAST != 0>{});
     // a folded tree phase runs on the rings
     oneshot = false;
     st_base = sring_lds;
@@ -2034,7 +2052,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
   merge_row<T, D, NB>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR));
 }
 
-template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, bool FAST = false>
+template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -2073,14 +2091,16 @@ int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
 
-// One-stream contiguous runs whose prefix units are all full and need no
-// non-temporal hint take the kernel with the unchecked prefix ring steps
-// (split_kernel<..., FAST = true>).  Every prefix unit lies below kv_len
-// (prefix_len <= kv_len), and the run-base path needs a row stride of at
-// least D in both K and V.
-template <int D> inline bool fast_ring(const SplitArgs& sa, const Plan& p) {
-  return config().fast_ring != 0 && p.streams == 1 && sa.prefix_len % kUnitKeys == 0 && !sa.kv_nt && sa.skn >= D &&
-         sa.svn >= D;
+// Contiguous calls whose prefix units are all full take the kernel with the
+// unchecked prefix ring steps (split_kernel<..., FAST>): 1 with plain K/V
+// loads, 2 with non-temporal ones (instantiated for two streams, where the
+// planner asks for them); 0 keeps the checked steps.  Every prefix unit lies
+// below kv_len (prefix_len <= kv_len), and the run-base path needs a row
+// stride of at least D in both K and V.
+template <int D> inline int fast_ring(const SplitArgs& sa, const Plan& p) {
+  if (config().fast_ring == 0 || sa.prefix_len % kUnitKeys != 0 || sa.skn < D || sa.svn < D) return 0;
+  if (!sa.kv_nt) return 1;
+  return p.streams == 2 ? 2 : 0;
 }
 
 // The paged forward always runs the 8-wave split kernel.
@@ -2098,11 +2118,13 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
                                     : launch_split<T, D, 1, true>(sa, p, stream));
     else
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
-           : p.streams == 2   ? (pipe ? launch_split<T, D, 2, false, false, true>(sa, p, stream)
-                                      : launch_split<T, D, 2, false>(sa, p, stream))
-                              : (pipe ? (fast_ring<D>(sa, p) ? launch_split<T, D, 1, false, false, true, true>(sa, p, stream)
-                                                          : launch_split<T, D, 1, false, false, true>(sa, p, stream))
-                                      : launch_split<T, D, 1, false>(sa, p, stream));
+           : p.streams == 2   ? (!pipe                  ? launch_split<T, D, 2, false>(sa, p, stream)
+                                 : fast_ring<D>(sa, p) == 2 ? launch_split<T, D, 2, false, false, true, 2>(sa, p, stream)
+                                 : fast_ring<D>(sa, p) == 1 ? launch_split<T, D, 2, false, false, true, 1>(sa, p, stream)
+                                                            : launch_split<T, D, 2, false, false, true>(sa, p, stream))
+                              : (!pipe                  ? launch_split<T, D, 1, false>(sa, p, stream)
+                                 : fast_ring<D>(sa, p) == 1 ? launch_split<T, D, 1, false, false, true, 1>(sa, p, stream)
+                                                            : launch_split<T, D, 1, false, false, true>(sa, p, stream));
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;

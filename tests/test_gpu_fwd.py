@@ -161,20 +161,22 @@ def test_cases_other_kernels(case, kernel, monkeypatch):
     assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
 
 
-# One key stream over a long prefix without the non-temporal hint takes the
-# kernel with unchecked prefix ring steps (prefix length a multiple of 32).
-# Its runs here are 24, 24 and 16 units (a shorter last run), rotated per row
-# chunk, so the steady ring steps, the checked tail and the wrap of the
+# A prefix whose length is a multiple of 32 takes the kernel with unchecked
+# prefix ring steps (one key stream or two; with two, its non-temporal
+# flavour too).  The runs here are 24, 24 and 16 units (a shorter last run;
+# with two streams and D = 64 the last one is a one-shot run), rotated per
+# row chunk, so the steady ring steps, the checked tail and the wrap of the
 # rotation all run; the result must equal the checked kernel's bit for bit
 # (the same arithmetic in the same order) and match the oracle.
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("rot", ["0", "5"])
-def test_fast_ring_matches_checked_steps(d, rot, monkeypatch):
+@pytest.mark.parametrize("streams,nt", [("1", "0"), ("2", "0"), ("2", "1")])
+def test_fast_ring_matches_checked_steps(d, rot, streams, nt, monkeypatch):
     b, hq, hkv, t, p, dtype = 2, 8, 2, 96, 2048, torch.bfloat16
-    for key, val in {"TSFA_WIDE": "0", "TSFA_STREAMS": "1", "TSFA_KV_NT": "0", "TSFA_ROT": rot,
+    for key, val in {"TSFA_WIDE": "0", "TSFA_STREAMS": streams, "TSFA_KV_NT": nt, "TSFA_ROT": rot,
                      "TSFA_PREFIX_UNITS_PER_SPLIT": "24"}.items():
         monkeypatch.setenv(key, val)
-    print(f"[fwd] fast ring d={d} rot={rot}", flush=True)
+    print(f"[fwd] fast ring d={d} rot={rot} streams={streams} nt={nt}", flush=True)
     rng = np.random.default_rng(d + int(rot))
     mask = torch.from_numpy(_tree("random", t, rng))
     q, k, v = _qkv(b, hq, hkv, t, p, d, dtype, seed=d)
