@@ -511,6 +511,15 @@ __device__ inline int work_item(const SplitArgs& a) {
   return j < np ? kth_prefix(plo + j) : kth_tree(lo - plo + j - np);
 }
 
+// The steady refills of a run with unchecked ring steps (FastSeq<true>):
+// init(t) points at the stream's t-th unit, next() requests it and moves to
+// the following one.  FastSeq<false> marks runs without them.
+template <bool V, typename I = int, typename N = int> struct FastSeq {
+  static constexpr bool value = V;
+  I init;
+  N next;
+};
+
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  PIPE
 // selects the software-pipelined unit loop (run_units_pipe).  FAST
 // (contiguous K/V, every prefix unit full; 1: plain loads, 2: non-temporal
@@ -1071,6 +1080,7 @@ void split_kernel(const SplitArgs a) {
       // RING2: NS-2 units ahead, two issued at every other step
       constexpr int AHEAD = RING2 ? NS - 2 : NS - 1;
       for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(sring_lds + j * SB, ks + S * j);
+      if constexpr (decltype(fast_c)::value) fast_c.init(AHEAD);  // the steady refills start there
       if (PAGED && AHEAD < mine) prefetch(key0_of(ks + S * AHEAD));
       if (mine > 0) wait_units<LPU, NS - 2>(min(mine, AHEAD) - 1);  // unit 0 landed
       sync_lds();
@@ -1109,8 +1119,8 @@ void split_kernel(const SplitArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (j < 40) TSFA_STAMP(3 + j);
             TSFA_CYC(2);
-            issue_of(sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
-            issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+            fast_c.next();  // units j + NS - 2 and j + NS - 1 of the stream
+            fast_c.next();
             __builtin_amdgcn_sched_barrier(0);
             return;
           }
@@ -1127,7 +1137,7 @@ void split_kernel(const SplitArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (j < 40) TSFA_STAMP(3 + j);
             TSFA_CYC(2);
-            issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+            fast_c.next();  // unit j + NS - 1 of the stream
             __builtin_amdgcn_sched_barrier(0);
             return;
           }
@@ -1245,13 +1255,27 @@ void split_kernel(const SplitArgs a) {
       read_q(false);
       if (QS > 1) sync_lds();
     }
+    // Steady refills (FAST, rotation off): the next unit's row pointer and
+    // ring stage advance by S units and one stage per refill.
+    const char* seq_rows = nullptr;
+    uint32_t seq_stage = 0;
+    auto seq_init = [&](int t) {
+      seq_rows = run_rows + (int64_t)(ks + S * t) * unit_bytes;
+      seq_stage = (uint32_t)(t % NS) * SB;
+    };
+    auto seq_next = [&]() {
+      dma_rows<LPU, FAST == 2>(seq_rows, doff, sring_lds + seq_stage + m0_off);
+      seq_rows += S * unit_bytes;
+      seq_stage = (seq_stage + SB) & (uint32_t)(NS * SB - 1);
+    };
     units(
         n, pre, key0_of,
         [&](int i) {
           if constexpr (FAST != 0) return false;
           else return P - key0_of(i) < kUnitKeys;
         },
-        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix, std::bool_constant<FAST != 0>{});
+        [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix,
+        FastSeq<FAST != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next});
     // a folded tree phase runs on the rings
     oneshot = false;
     st_base = sring_lds;
@@ -1346,7 +1370,7 @@ void split_kernel(const SplitArgs a) {
       auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
       units(
           nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
-          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, std::false_type{});
+          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{});
       sync_all();  // ring and masks free for the next batch
     }
   }
@@ -2091,14 +2115,16 @@ int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
 
-// Contiguous calls whose prefix units are all full take the kernel with the
-// unchecked prefix ring steps (split_kernel<..., FAST>): 1 with plain K/V
+// Contiguous calls whose prefix units are all full (and prefix runs not
+// rotated) take the kernel with the unchecked prefix ring steps
+// (split_kernel<..., FAST>): 1 with plain K/V
 // loads, 2 with non-temporal ones (instantiated for two streams, where the
 // planner asks for them); 0 keeps the checked steps.  Every prefix unit lies
 // below kv_len (prefix_len <= kv_len), and the run-base path needs a row
 // stride of at least D in both K and V.
 template <int D> inline int fast_ring(const SplitArgs& sa, const Plan& p) {
-  if (config().fast_ring == 0 || sa.prefix_len % kUnitKeys != 0 || sa.skn < D || sa.svn < D) return 0;
+  if (config().fast_ring == 0 || sa.prefix_len % kUnitKeys != 0 || sa.skn < D || sa.svn < D || sa.rot_step != 0)
+    return 0;
   if (!sa.kv_nt) return 1;
   return p.streams == 2 ? 2 : 0;
 }
