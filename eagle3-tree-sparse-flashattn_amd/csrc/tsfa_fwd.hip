@@ -1999,12 +1999,12 @@ void wide_kernel(const SplitArgs a) {
 constexpr int kEpt = 8;
 constexpr int kCombineThreads = 128;
 
-// HALVES: the row's slots are split between two groups of D/kEpt threads
-// (half h takes slots h, h+2, ...), merged through a lane exchange, and half
-// 0 writes the row: twice the threads for the same 16-byte loads, half the
-// conversions and multiply-adds per thread (the combine is bound by those
-// VALU instructions at one or two waves per SIMD, not by its loads).
-template <typename T, int D, int NB, bool HALVES = false>
+// GR > 1: the row's slots are split between GR groups of D/kEpt threads
+// (group h takes slots h, h+GR, ...), merged through lane exchanges, and
+// group 0 writes the row: GR times the threads for the same 16-byte loads,
+// 1/GR of the conversions and multiply-adds per thread (the combine is bound
+// by those VALU instructions at one or two waves per SIMD, not by its loads).
+template <typename T, int D, int NB, int GR = 1>
 __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int part, int half = 0) {
   const int64_t TG = (int64_t)a.q_len * a.group;
   const int t = R / a.group, g = R - t * a.group;
@@ -2023,8 +2023,8 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
   float acc[kEpt];
 #pragma unroll
   for (int e = 0; e < kEpt; ++e) acc[e] = 0.f;
-  constexpr int SS = HALVES ? 2 : 1;  // slot step of this thread
-  for (int s0 = HALVES ? half : 0; s0 < a.n_slots; s0 += SS * NB) {
+  constexpr int SS = GR;  // slot step of this thread
+  for (int s0 = half; s0 < a.n_slots; s0 += SS * NB) {
     const int nb = min(NB, (a.n_slots - s0 + SS - 1) / SS);
     float2 v[NB];
     TV x[NB];
@@ -2054,21 +2054,23 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
       for (int e = 0; e < kEpt; ++e) acc[e] += w * (float)x[i][e];
     }
   }
-  if constexpr (HALVES) {
-    // the other half's (M, L, acc) from lane ^ D/kEpt; an empty half
-    // (M = -inf) weighs 0, and two empty halves leave l = 0
-    constexpr int TPR = D / kEpt;
-    const float pm = __shfl_xor(mx, TPR), pl = __shfl_xor(l, TPR);
-    float pacc[kEpt];
+  if constexpr (GR > 1) {
+    // the other groups' (M, L, acc) from lane ^ off (off = D/kEpt, 2*D/kEpt,
+    // ...); an empty group (M = -inf) weighs 0, and all empty leave l = 0
 #pragma unroll
-    for (int e = 0; e < kEpt; ++e) pacc[e] = __shfl_xor(acc[e], TPR);
-    const float M = fmaxf(mx, pm);
-    const float w0 = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mx - M) * a.scale_log2);
-    const float w1 = (pm == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((pm - M) * a.scale_log2);
-    l = w0 * l + w1 * pl;
+    for (int off = D / kEpt; off < GR * (D / kEpt); off *= 2) {
+      const float pm = __shfl_xor(mx, off), pl = __shfl_xor(l, off);
+      float pacc[kEpt];
 #pragma unroll
-    for (int e = 0; e < kEpt; ++e) acc[e] = w0 * acc[e] + w1 * pacc[e];
-    mx = M;
+      for (int e = 0; e < kEpt; ++e) pacc[e] = __shfl_xor(acc[e], off);
+      const float M = fmaxf(mx, pm);
+      const float w0 = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((mx - M) * a.scale_log2);
+      const float w1 = (pm == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((pm - M) * a.scale_log2);
+      l = w0 * l + w1 * pl;
+#pragma unroll
+      for (int e = 0; e < kEpt; ++e) acc[e] = w0 * acc[e] + w1 * pacc[e];
+      mx = M;
+    }
     if (half != 0) return;
   }
   // l == 0 (no visible key anywhere) gives 0 * inf = NaN, as acc / l_i does in
@@ -2089,19 +2091,18 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
 
 // Merge the n_slots partials of every row and write O.  Threads walk the
 // workspace rows in order (coalesced partial loads).
-template <typename T, int D, int NB, bool HALVES = false>
+template <typename T, int D, int NB, int GR = 1>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineArgs a) {
   constexpr int TPR = D / kEpt;
-  constexpr int RPB = kCombineThreads / (TPR * (HALVES ? 2 : 1));  // rows per block
+  static_assert(GR * TPR <= 64 && kCombineThreads % (GR * TPR) == 0, "a row's groups share one wave");
+  constexpr int RPB = kCombineThreads / (TPR * GR);  // rows per block
   const int x = blockIdx.x & 7;
   const int64_t TG = (int64_t)a.q_len * a.group;
-  const int tr = HALVES ? (int)threadIdx.x / (2 * TPR) : (int)threadIdx.x / TPR;
-  const int64_t row = a.xcd_row[x] + (int64_t)(blockIdx.x >> 3) * RPB + tr;  // over B*Hkv*TG
-  // (a whole row's threads leave together: the halves exchange within it)
+  const int64_t row = a.xcd_row[x] + (int64_t)(blockIdx.x >> 3) * RPB + threadIdx.x / (GR * TPR);  // over B*Hkv*TG
+  // (a whole row's threads leave together: its groups exchange within it)
   if (row >= a.xcd_row[x + 1]) return;
   const int64_t bk = row / TG;
-  merge_row<T, D, NB, HALVES>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR),
-                              HALVES ? (int)(threadIdx.x / TPR) & 1 : 0);
+  merge_row<T, D, NB, GR>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR), (int)(threadIdx.x / TPR) % GR);
 }
 
 template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
@@ -2187,9 +2188,11 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   // slot), so the partials are read from the L2 they were written to and the
   // next call's partial stores find no copies in other XCDs' L2s.
   CombineArgs c = ca;
-  // more than 4 slots: the halves kernel (twice the threads per row)
-  const bool halves = ca.n_slots > 4;
-  const int RPB = kCombineThreads / (D / kEpt) / (halves ? 2 : 1);
+  // more than 4 slots: 2 groups of threads per row; more than 8: 4 groups
+  // (16 slots at the Llama-3-8B decode shape: 3.86 us per combine with one
+  // group, 3.60 with two, 3.19 with four; same-call A/B)
+  const int gr = ca.n_slots > 8 ? 4 : ca.n_slots > 4 ? 2 : 1;
+  const int RPB = kCombineThreads / (D / kEpt) / gr;
   const int64_t TG = (int64_t)ca.q_len * ca.group;
   const int64_t groups = (int64_t)ca.batch * ca.num_kv_heads * p.n_chunks;
   auto first_row = [&](int64_t g) { return (g / p.n_chunks) * TG + (g % p.n_chunks) * p.rows_per_chunk; };
@@ -2217,9 +2220,9 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   else if (ns <= 4)
     hipLaunchKernelGGL((combine_kernel<T, D, 4>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
   else if (ns <= 8)
-    hipLaunchKernelGGL((combine_kernel<T, D, 4, true>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 2>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
   else
-    hipLaunchKernelGGL((combine_kernel<T, D, 8, true>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 4>), dim3(blocks), dim3(kCombineThreads), 0, stream, c);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
