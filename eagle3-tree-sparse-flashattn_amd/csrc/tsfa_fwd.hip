@@ -1162,7 +1162,34 @@ void split_kernel(const SplitArgs a) {
     };
     // (unrolling by two to alternate the S^T registers instead of copying
     // them made the allocator shuffle the O accumulators: 281 copies)
-    for (int j = 0; j < steps; ++j) {
+    int j0 = 0;
+    if constexpr (RING2 && decltype(fast_c)::value) {
+      // Unchecked steady state in pairs of steps (the even one meets and
+      // refills two units): no parity test and one loop test per two units;
+      // the scheduling fences keep the two iterations' registers apart (the
+      // 2x unrolled body spills without them).  1024-token wide tree -2 %,
+      // 70B shape -3 to -6 % (same-call A/B).
+      if (!oneshot && active) {
+        for (; j0 + NS - 1 < mine; j0 += 2) {
+          vm_wait<(NS - 5) * LPU>();
+          __builtin_amdgcn_sched_barrier(0);
+          sync_lds();
+          __builtin_amdgcn_sched_barrier(0);
+          if (j0 < 40) TSFA_STAMP(3 + j0);
+          TSFA_CYC(2);
+          fast_c.next();  // units j0 + NS - 2 and j0 + NS - 1 of the stream
+          fast_c.next();
+          __builtin_amdgcn_sched_barrier(0);
+          pipe_iter(j0, ks + S * j0, std::true_type{}, s_cur, s_next, masked_of, mask_of);
+          s_cur = s_next;
+          __builtin_amdgcn_sched_barrier(0);
+          pipe_iter(j0 + 1, ks + S * (j0 + 1), std::true_type{}, s_cur, s_next, masked_of, mask_of);
+          s_cur = s_next;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    for (int j = j0; j < steps; ++j) {
       ring_step(j);
       if (j + 1 < mine && active) {
         pipe_iter(j, ks + S * j, std::true_type{}, s_cur, s_next, masked_of, mask_of);
