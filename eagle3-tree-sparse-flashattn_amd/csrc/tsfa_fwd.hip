@@ -1188,6 +1188,24 @@ void split_kernel(const SplitArgs a) {
           __builtin_amdgcn_sched_barrier(0);
         }
       }
+    } else if constexpr (decltype(fast_c)::value) {
+      // the same for rings that meet and refill at every step
+      if (!oneshot && active) {
+        for (; j0 + NS < mine; j0 += 2) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            vm_wait<(NS - 3) * LPU>();
+            __builtin_amdgcn_sched_barrier(0);
+            sync_lds();
+            __builtin_amdgcn_sched_barrier(0);
+            fast_c.next();  // unit j0 + h + NS - 1 of the stream
+            __builtin_amdgcn_sched_barrier(0);
+            pipe_iter(j0 + h, ks + S * (j0 + h), std::true_type{}, s_cur, s_next, masked_of, mask_of);
+            s_cur = s_next;
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
     }
     for (int j = j0; j < steps; ++j) {
       ring_step(j);
