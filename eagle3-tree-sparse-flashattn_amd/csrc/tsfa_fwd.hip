@@ -521,11 +521,11 @@ template <bool V, typename I = int, typename N = int> struct FastSeq {
 };
 
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  PIPE
-// selects the software-pipelined unit loop (run_units_pipe).  FAST
-// (contiguous K/V, every prefix unit full; 1: plain loads, 2: non-temporal
-// K/V loads): prefix runs skip the per-unit mask test, ring runs issue every
-// unit by the run-base path, and their steady ring steps use a fixed wait
-// count.
+// selects the software-pipelined unit loop (run_units_pipe).  FAST (every
+// prefix unit full; 1: plain loads, 2: non-temporal K/V loads; paged runs
+// choose the hint at run time and take 1): prefix runs skip the per-unit
+// mask test, contiguous ring runs issue every unit by the run-base path, and
+// the steady ring steps use a fixed wait count.
 template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
@@ -1119,8 +1119,8 @@ void split_kernel(const SplitArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (j < 40) TSFA_STAMP(3 + j);
             TSFA_CYC(2);
-            fast_c.next();  // units j + NS - 2 and j + NS - 1 of the stream
-            fast_c.next();
+            fast_c.next(mine);  // units j + NS - 2 and j + NS - 1 of the stream
+            fast_c.next(mine);
             __builtin_amdgcn_sched_barrier(0);
             return;
           }
@@ -1137,7 +1137,7 @@ void split_kernel(const SplitArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             if (j < 40) TSFA_STAMP(3 + j);
             TSFA_CYC(2);
-            fast_c.next();  // unit j + NS - 1 of the stream
+            fast_c.next(mine);  // unit j + NS - 1 of the stream
             __builtin_amdgcn_sched_barrier(0);
             return;
           }
@@ -1177,8 +1177,8 @@ void split_kernel(const SplitArgs a) {
           __builtin_amdgcn_sched_barrier(0);
           if (j0 < 40) TSFA_STAMP(3 + j0);
           TSFA_CYC(2);
-          fast_c.next();  // units j0 + NS - 2 and j0 + NS - 1 of the stream
-          fast_c.next();
+          fast_c.next(mine);  // units j0 + NS - 2 and j0 + NS - 1 of the stream
+          fast_c.next(mine);
           __builtin_amdgcn_sched_barrier(0);
           pipe_iter(j0, ks + S * j0, std::true_type{}, s_cur, s_next, masked_of, mask_of);
           s_cur = s_next;
@@ -1198,7 +1198,7 @@ void split_kernel(const SplitArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             sync_lds();
             __builtin_amdgcn_sched_barrier(0);
-            fast_c.next();  // unit j0 + h + NS - 1 of the stream
+            fast_c.next(mine);  // unit j0 + h + NS - 1 of the stream
             __builtin_amdgcn_sched_barrier(0);
             pipe_iter(j0 + h, ks + S * (j0 + h), std::true_type{}, s_cur, s_next, masked_of, mask_of);
             s_cur = s_next;
@@ -1249,7 +1249,7 @@ void split_kernel(const SplitArgs a) {
     uint32_t m0_off = 0;
     auto issue_prefix = [&](uint32_t sb, int i) {
       const int r = i + rot, ri = r >= n ? r - n : r;
-      if constexpr (FAST != 0) {
+      if constexpr (FAST != 0 && !PAGED) {
         // one-shot runs (two streams only) issue by the general path: their
         // run base is not set up, to keep Q's request first
         if (!(S == 2 && oneshot)) dma_rows<LPU, FAST == 2>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
@@ -1304,14 +1304,26 @@ void split_kernel(const SplitArgs a) {
     // ring stage advance by S units and one stage per refill.
     const char* seq_rows = nullptr;
     uint32_t seq_stage = 0;
+    int seq_t = 0;  // paged: the stream's next unit
     auto seq_init = [&](int t) {
-      seq_rows = run_rows + (int64_t)(ks + S * t) * unit_bytes;
-      seq_stage = (uint32_t)(t % NS) * SB;
+      if constexpr (PAGED) {
+        seq_t = t;
+      } else {
+        seq_rows = run_rows + (int64_t)(ks + S * t) * unit_bytes;
+        seq_stage = (uint32_t)(t % NS) * SB;
+      }
     };
-    auto seq_next = [&]() {
-      dma_rows<LPU, FAST == 2>(seq_rows, doff, sring_lds + seq_stage + m0_off);
-      seq_rows += S * unit_bytes;
-      seq_stage = (seq_stage + SB) & (uint32_t)(NS * SB - 1);
+    auto seq_next = [&](int mine_units) {
+      if constexpr (PAGED) {
+        // the page-table path, then the lookup of the unit after it
+        issue_prefix(sring_lds + (uint32_t)(seq_t % NS) * SB, ks + S * seq_t);
+        ++seq_t;
+        if (seq_t < mine_units) prefetch(key0_of(ks + S * seq_t));
+      } else {
+        dma_rows<LPU, FAST == 2>(seq_rows, doff, sring_lds + seq_stage + m0_off);
+        seq_rows += S * unit_bytes;
+        seq_stage = (seq_stage + SB) & (uint32_t)(NS * SB - 1);
+      }
     };
     units(
         n, pre, key0_of,
@@ -2209,13 +2221,20 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
   if (g_kernel_mask & 1) {
     int st;
     const bool pipe = config().pipe != 0;
+    // paged: the unchecked steps need only full prefix units (the page-table
+    // path serves every refill)
+    const bool fp = pipe && config().fast_ring != 0 && sa.prefix_len % kUnitKeys == 0;
     if constexpr (PAGED)
-      st = (sa.cache32 && p.streams == 2) ? (pipe ? launch_split<T, D, 2, true, true, true>(sa, p, stream)
-                                                  : launch_split<T, D, 2, true, true>(sa, p, stream))
-           : p.streams == 2 ? (pipe ? launch_split<T, D, 2, true, false, true>(sa, p, stream)
-                                    : launch_split<T, D, 2, true>(sa, p, stream))
-                            : (pipe ? launch_split<T, D, 1, true, false, true>(sa, p, stream)
-                                    : launch_split<T, D, 1, true>(sa, p, stream));
+      st = (sa.cache32 && p.streams == 2)
+               ? (!pipe ? launch_split<T, D, 2, true, true>(sa, p, stream)
+                  : fp  ? launch_split<T, D, 2, true, true, true, 1>(sa, p, stream)
+                        : launch_split<T, D, 2, true, true, true>(sa, p, stream))
+           : p.streams == 2 ? (!pipe ? launch_split<T, D, 2, true>(sa, p, stream)
+                               : fp  ? launch_split<T, D, 2, true, false, true, 1>(sa, p, stream)
+                                     : launch_split<T, D, 2, true, false, true>(sa, p, stream))
+                            : (!pipe ? launch_split<T, D, 1, true>(sa, p, stream)
+                               : fp  ? launch_split<T, D, 1, true, false, true, 1>(sa, p, stream)
+                                     : launch_split<T, D, 1, true, false, true>(sa, p, stream));
     else
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
            : p.streams == 2   ? (!pipe                  ? launch_split<T, D, 2, false>(sa, p, stream)

@@ -33,6 +33,7 @@ CASES = [
     (2, 4, 2, 33, 61, 64, FP, 16, 16, "kary", 32, "NHD", "dense"),      # D = 64, P % 8 = 5
     (1, 16, 1, 200, 1000, 128, FP, 64, 32, "random", 256, "NHD", "csr"),
     (1, 32, 8, 64, 1, 128, BF, 16, 64, "eagle", 128, "NHD", "csr"),     # prefix of one key
+    (2, 8, 2, 96, 2048, 128, BF, 64, 64, "random", 16, "NHD", "csr"),   # long prefix, P % 32 = 0
 ]
 
 
@@ -81,7 +82,7 @@ def test_paged_cases(case):
     assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
 
 
-@pytest.mark.parametrize("case", [CASES[i] for i in (2, 4, 5)], ids=["p2", "p4", "p5"])
+@pytest.mark.parametrize("case", [CASES[i] for i in (2, 4, 5, 9)], ids=["p2", "p4", "p5", "p9"])
 def test_paged_one_stream_kernel(case, monkeypatch):
     monkeypatch.setenv("TSFA_WIDE", "0")
     monkeypatch.setenv("TSFA_STREAMS", "1")
