@@ -174,6 +174,20 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                              ? 1
                                              : 0);
   }
+  // A folded tree lengthens the last run of each chunk: the earlier runs of
+  // a plan of several splits take the modelled tree cost off it, spread over
+  // the splits, while the split count stays (the 1024-token wide tree: 256
+  // -> 266 units per split, 270 -> 266-268 us per call in one sweep, within
+  // noise of it in a later A/B).
+  if (p->fold_tree && p->n_splits >= 2 && cfg.prefix_units <= 0) {
+    const int64_t tree_units = ceil_div(std::max(0, kv_len - prefix_len), kUnitKeys);
+    const int extra = (int)std::min<int64_t>((int64_t)(0.6 * (double)tree_units / p->streams), p->n_pu);
+    const int ups2 = ceil_div(p->n_pu + extra, p->n_splits);
+    if (ups2 > ups && ceil_div(p->n_pu, ups2) == p->n_splits) {
+      ups = ups2;
+      p->units_per_split = ups;
+    }
+  }
   p->n_slots = p->n_splits + (p->fold_tree ? 0 : 1);
   const int64_t items = groups * p->n_slots;
   if (items > (int64_t)INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
