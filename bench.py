@@ -241,7 +241,8 @@ def eager_call_timing(w, qd, ks, vs, mask_dev, meta, reps: int = 100, batches: i
 
 def workload_timing(name: str, steps: int, cold_mib: int):
     """One forward workload (split-KV + combine) timed as the headline is:
-    graph of `steps` calls, the combine alone, cold K/V copies."""
+    graph of `steps` calls (median of 5 replays), the combine alone, cold
+    K/V copies."""
     import torch
 
     from tsfa import _lib, configs
@@ -285,13 +286,19 @@ def workload_timing(name: str, steps: int, cold_mib: int):
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
+        # the median of 5 replays: one replay can catch a stall of the host
+        # process or the GPU (a combine once read 41 us against ~5)
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(s):
-            a.record()
-            g.replay()
-            b.record()
-        torch.cuda.synchronize()
-        secs[region] = a.elapsed_time(b) / 1e3 / steps
+        reps = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                a.record()
+                g.replay()
+                b.record()
+            torch.cuda.synchronize()
+            reps.append(a.elapsed_time(b) / 1e3 / steps)
+        secs[region] = sorted(reps)[len(reps) // 2]
         del g
     split_s = secs["full"] - secs["combine"]
     flops = algorithmic_flops(w, mask)
