@@ -158,6 +158,10 @@ struct SplitArgs {
   int fold_tree;   // no tree items: the last prefix split of each chunk also runs the tree units
   int os_first;    // one-shot prefix runs: run units requested with Q (the rest once Q landed)
   int rot_step;    // prefix run of chunk c starts at its unit (c * rot_step) mod n and wraps
+  // One-slot plans with O contiguous [B, Hq, q_len, D] and no LSE asked: the
+  // split kernel writes O itself (ws_o is O; split_kernel<..., FAST | 4>)
+  // and no combine runs.  Host-side only.
+  int direct_out;
 };
 
 
@@ -529,6 +533,8 @@ template <bool V, typename I = int, typename N = int> struct FastSeq {
 template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
+  constexpr int FM = FAST & 3;              // unchecked ring steps: 0 off, 1 plain, 2 non-temporal loads
+  constexpr bool DIRECT = (FAST & 4) != 0;  // one-slot plan: write O, no combine
   typedef typename Mma<T>::vec8 V8;
   constexpr int RG = kWaves / S;             // row groups (waves per stream)
   constexpr int ROWS = 32 * RG;              // rows per chunk
@@ -1249,10 +1255,10 @@ void split_kernel(const SplitArgs a) {
     uint32_t m0_off = 0;
     auto issue_prefix = [&](uint32_t sb, int i) {
       const int r = i + rot, ri = r >= n ? r - n : r;
-      if constexpr (FAST != 0 && !PAGED) {
+      if constexpr (FM != 0 && !PAGED) {
         // one-shot runs (two streams only) issue by the general path: their
         // run base is not set up, to keep Q's request first
-        if (!(S == 2 && oneshot)) dma_rows<LPU, FAST == 2>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
+        if (!(S == 2 && oneshot)) dma_rows<LPU, FM == 2>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
         else issue_at(sb, key0_of(i));
       } else if (!PAGED && !oneshot && ri < n_fast) {
         const char* rowp = run_rows + ri * unit_bytes;
@@ -1320,7 +1326,7 @@ void split_kernel(const SplitArgs a) {
         ++seq_t;
         if (seq_t < mine_units) prefetch(key0_of(ks + S * seq_t));
       } else {
-        dma_rows<LPU, FAST == 2>(seq_rows, doff, sring_lds + seq_stage + m0_off);
+        dma_rows<LPU, FM == 2>(seq_rows, doff, sring_lds + seq_stage + m0_off);
         seq_rows += S * unit_bytes;
         seq_stage = (seq_stage + SB) & (uint32_t)(NS * SB - 1);
       }
@@ -1328,11 +1334,11 @@ void split_kernel(const SplitArgs a) {
     units(
         n, pre, key0_of,
         [&](int i) {
-          if constexpr (FAST != 0) return false;
+          if constexpr (FM != 0) return false;
           else return P - key0_of(i) < kUnitKeys;
         },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix,
-        FastSeq<FAST != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next});
+        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next});
     // a folded tree phase runs on the rings
     oneshot = false;
     st_base = sring_lds;
@@ -1444,8 +1450,27 @@ void split_kernel(const SplitArgs a) {
   typedef T T4 __attribute__((ext_vector_type(4)));
   const int64_t part_row0 = ((int64_t)bk * a.n_slots + slot) * TG + row0;
   const int r = rg * 32 + ln;  // the lane's chunk row
-  T* dst = static_cast<T*>(a.ws_o) + (part_row0 + r) * D;
   const bool row_ok = r < rows_chunk;
+  // One-slot plans write the lane's row of O itself: token t, head kvh*G+g
+  // (rows past the chunk's end store nothing).  A row that saw no key gets
+  // NaN (0/0, as the combine and the reference give) instead of a partial
+  // of weight 0.
+  constexpr bool direct = DIRECT;
+  T* dst;
+  if constexpr (direct) {
+    // row (token t, head kvh*G + g) of O [B, Hq, q_len, D]
+    const int R = min(row0 + r, TG - 1);
+    const int t = (int)fdiv((uint32_t)R, a.fd_group);
+    const int64_t h = (int64_t)kvh * G + (R - t * G);
+    dst = static_cast<T*>(a.ws_o) + (((int64_t)b * a.num_kv_heads * G + h) * a.q_len + t) * D;
+  } else {
+    dst = static_cast<T*>(a.ws_o) + (part_row0 + r) * D;
+  }
+  const float empty_inv = direct ? __builtin_nanf("") : 0.f;  // (compile-time)
+  // (m, l) of the lane's row into the workspace (none when writing O)
+  auto put_ml = [&](float m, float l) {
+    if constexpr (!direct) a.ws_ml[part_row0 + r] = make_float2(m, l);
+  };
   // Quads e (d = 8q + 4lh + [0,4), q = 2p) and f (q = 2p+1) of one row in
   // lanes l and l+32 become 16 contiguous bytes per lane: lane l takes
   // d = 16p + [0,8) (its e and the partner's), lane l+32 d = 16p + [8,16)
@@ -1487,7 +1512,7 @@ void split_kernel(const SplitArgs a) {
       const float w0 = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((m_run - M) * sl2);
       const float w1 = (other.x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((other.x - M) * sl2);
       const float L = w0 * lt + w1 * other.y;
-      const float inv = L > 0.f ? 1.f / L : 0.f;  // empty partial: O = 0, weight 0 in the combine
+      const float inv = L > 0.f ? 1.f / L : empty_inv;  // empty partial: O = 0, weight 0 in the combine
       const float a0 = w0 * inv, a1 = w1 * inv;
 #pragma unroll
       for (int dl = 0; dl < DH; ++dl)
@@ -1501,12 +1526,12 @@ void split_kernel(const SplitArgs a) {
           }
           store16(dst + (KEEP + dl) * 32 + 16 * p, e, f);
         }
-      if (KS == 0 && lh == 0 && row_ok) a.ws_ml[part_row0 + r] = make_float2(M, L);
+      if (KS == 0 && lh == 0 && row_ok) put_ml(M, L);
     };
     if (ks == 0) merge(std::integral_constant<int, 0>{});
     else merge(std::integral_constant<int, 1>{});
   } else {
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const float inv = lt > 0.f ? 1.f / lt : empty_inv;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -1519,7 +1544,7 @@ void split_kernel(const SplitArgs a) {
         }
         store16(dst + dt * 32 + 16 * p, e, f);
       }
-    if (lh == 0 && row_ok) a.ws_ml[part_row0 + r] = make_float2(m_run, lt);
+    if (lh == 0 && row_ok) put_ml(m_run, lt);
   }
   TSFA_STAMP(51);
   TSFA_CYC_STORE;
@@ -2217,10 +2242,17 @@ template <int D> inline int fast_ring(const SplitArgs& sa, const Plan& p) {
 
 // The paged forward always runs the 8-wave split kernel.
 template <typename T, int D, bool PAGED>
-int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
+int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
+  const bool pipe = config().pipe != 0;
+  // contiguous: the unchecked-step flavour, +4 for the kernel that writes O
+  // itself (one-slot plans, with the unchecked steps only): then its
+  // "partial" goes straight to O and the combine is not launched
+  const int fm0 = PAGED || !pipe ? 0 : fast_ring<D>(sa_in, p);
+  const int fm = fm0 != 0 && sa_in.direct_out ? fm0 | 4 : fm0;
+  SplitArgs sa = sa_in;
+  if (fm & 4) sa.ws_o = ca.o;
   if (g_kernel_mask & 1) {
     int st;
-    const bool pipe = config().pipe != 0;
     // paged: the unchecked steps need only full prefix units (the page-table
     // path serves every refill)
     const bool fp = pipe && config().fast_ring != 0 && sa.prefix_len % kUnitKeys == 0;
@@ -2237,16 +2269,20 @@ int launch_all(const SplitArgs& sa, const CombineArgs& ca, const Plan& p, hipStr
                                      : launch_split<T, D, 1, true, false, true>(sa, p, stream));
     else
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
-           : p.streams == 2   ? (!pipe                  ? launch_split<T, D, 2, false>(sa, p, stream)
-                                 : fast_ring<D>(sa, p) == 2 ? launch_split<T, D, 2, false, false, true, 2>(sa, p, stream)
-                                 : fast_ring<D>(sa, p) == 1 ? launch_split<T, D, 2, false, false, true, 1>(sa, p, stream)
-                                                            : launch_split<T, D, 2, false, false, true>(sa, p, stream))
-                              : (!pipe                  ? launch_split<T, D, 1, false>(sa, p, stream)
-                                 : fast_ring<D>(sa, p) == 1 ? launch_split<T, D, 1, false, false, true, 1>(sa, p, stream)
-                                                            : launch_split<T, D, 1, false, false, true>(sa, p, stream));
+           : p.streams == 2   ? (!pipe    ? launch_split<T, D, 2, false>(sa, p, stream)
+                                 : fm == 6 ? launch_split<T, D, 2, false, false, true, 6>(sa, p, stream)
+                                 : fm == 5 ? launch_split<T, D, 2, false, false, true, 5>(sa, p, stream)
+                                 : fm == 2 ? launch_split<T, D, 2, false, false, true, 2>(sa, p, stream)
+                                 : fm == 1 ? launch_split<T, D, 2, false, false, true, 1>(sa, p, stream)
+                                           : launch_split<T, D, 2, false, false, true>(sa, p, stream))
+                              : (!pipe    ? launch_split<T, D, 1, false>(sa, p, stream)
+                                 : fm == 5 ? launch_split<T, D, 1, false, false, true, 5>(sa, p, stream)
+                                 : fm == 1 ? launch_split<T, D, 1, false, false, true, 1>(sa, p, stream)
+                                           : launch_split<T, D, 1, false, false, true>(sa, p, stream));
     if (st != TSFA_OK) return st;
   }
-  if ((g_kernel_mask & 2) == 0) return TSFA_OK;
+  // no combine when the split kernel wrote O
+  if ((g_kernel_mask & 2) == 0 || (fm & 4)) return TSFA_OK;
   // Each XCD merges the rows of the chunks its split workgroups ran (item i
   // runs on XCD i / items_per_xcd; a chunk's rows go to the XCD of its middle
   // slot), so the partials are read from the L2 they were written to and the
@@ -2504,6 +2540,17 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   // one round (every XCD's items start together): the order cannot matter,
   // and the natural one costs each wave no scalar divisions to decode
   if (order < 0 && (int64_t)p.items_per_xcd * 8 <= cus) sa.item_order = 0;
+
+  // One slot (one prefix run per chunk with the tree folded in, or a tree
+  // alone): the split kernel's partial is O itself, so with O contiguous
+  // [B, Hq, q_len, D] and no LSE asked it writes O and the combine is
+  // skipped (the 16-sequence decode shape: its ~5 us combine of ~55 us).
+  const bool o_dense = o_strides[3] == 1 && o_strides[2] == head_dim && o_strides[1] == (int64_t)q_len * head_dim &&
+                       o_strides[0] == (int64_t)num_heads * q_len * head_dim;
+  sa.direct_out = p.n_slots == 1 && !p.wide && !kv.paged() && lse == nullptr && o_dense && config().direct_out != 0 &&
+                         config().pipe != 0
+                     ? 1
+                     : 0;
 
   CombineArgs ca;
   ca.o = o;

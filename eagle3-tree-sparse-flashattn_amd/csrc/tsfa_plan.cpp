@@ -40,6 +40,7 @@ Config read_config() {
   c.fold_tree = env_int("TSFA_FOLD_TREE", -1);
   c.pipe = env_int("TSFA_PIPE", 1);
   c.fast_ring = env_int("TSFA_FAST_RING", 1);
+  c.direct_out = env_int("TSFA_DIRECT_OUT", 1);
   c.kv_nt = env_int("TSFA_KV_NT", -1);
   c.item_order = env_int("TSFA_ITEM_ORDER", -1);
   c.os_first = env_int("TSFA_OS_FIRST", 64);

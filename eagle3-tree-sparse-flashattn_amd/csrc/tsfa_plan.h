@@ -46,6 +46,7 @@ struct Config {
   int fold_tree;       // TSFA_FOLD_TREE: 0/1 forces, -1 planner
   int pipe;            // TSFA_PIPE: 0 the unpipelined unit loop
   int fast_ring;       // TSFA_FAST_RING: 0 keeps the checked ring steps for full prefix runs
+  int direct_out;      // TSFA_DIRECT_OUT: 0 keeps the combine for one-slot plans
   int kv_nt;           // TSFA_KV_NT: 0/1 forces non-temporal K/V loads, -1 planner
   int item_order;      // TSFA_ITEM_ORDER: 0/1/2 forces, -1 planner
   int os_first;        // TSFA_OS_FIRST: one-shot run units requested with Q

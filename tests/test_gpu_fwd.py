@@ -189,6 +189,32 @@ def test_fast_ring_matches_checked_steps(d, rot, streams, nt, monkeypatch):
     assert_close_to_oracle(outs["1"], oracle_out(q, k, v, mask, p), dtype)
 
 
+# A plan of one slot (one prefix run per chunk with the tree folded in, or
+# the tree alone) writes O from the split kernel and skips the combine; the
+# result must equal the combine's bit for bit (a one-slot merge returns the
+# partial) and match the oracle.  Two streams with non-temporal loads and one
+# stream with plain ones.
+@pytest.mark.parametrize("streams,nt,p", [("2", "1", 512), ("1", "0", 512), ("2", "1", 0), ("1", "0", 1024)])
+def test_one_slot_direct_output_matches_combine(streams, nt, p, monkeypatch):
+    b, hq, hkv, t, dtype = 3, 8, 2, 40, torch.float16
+    env = {"TSFA_WIDE": "0", "TSFA_STREAMS": streams, "TSFA_KV_NT": nt, "TSFA_FOLD_TREE": "1"}
+    if p:
+        env["TSFA_PREFIX_UNITS_PER_SPLIT"] = str(p // 32)
+    for key, val in env.items():
+        monkeypatch.setenv(key, val)
+    print(f"[fwd] one-slot direct output streams={streams} nt={nt} p={p}", flush=True)
+    rng = np.random.default_rng(p + int(streams))
+    mask = torch.from_numpy(_tree("kary", t, rng))
+    q, k, v = _qkv(b, hq, hkv, t, p, 64 if streams == "1" else 128, dtype, seed=p + 7)
+    outs = {}
+    for direct in ("1", "0"):
+        monkeypatch.setenv("TSFA_DIRECT_OUT", direct)
+        outs[direct] = _run_nan_filled(q, k, v, mask, p, 16, 32)
+        torch.cuda.synchronize()
+    assert torch.equal(outs["1"], outs["0"])
+    assert_close_to_oracle(outs["1"], oracle_out(q, k, v, mask, p), dtype, relative=p < 256)
+
+
 @pytest.mark.parametrize("kernel", sorted(KERNELS))
 def test_workload_other_kernels(kernel, monkeypatch):
     for key, val in KERNELS[kernel].items():
