@@ -2247,26 +2247,29 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, hip
   // contiguous: the unchecked-step flavour, +4 for the kernel that writes O
   // itself (one-slot plans, with the unchecked steps only): then its
   // "partial" goes straight to O and the combine is not launched
-  const int fm0 = PAGED || !pipe ? 0 : fast_ring<D>(sa_in, p);
+  const bool fp = pipe && config().fast_ring != 0 && sa_in.prefix_len % kUnitKeys == 0;
+  const int fm0 = !pipe ? 0 : PAGED ? (fp ? 1 : 0) : fast_ring<D>(sa_in, p);
   const int fm = fm0 != 0 && sa_in.direct_out ? fm0 | 4 : fm0;
   SplitArgs sa = sa_in;
   if (fm & 4) sa.ws_o = ca.o;
   if (g_kernel_mask & 1) {
     int st;
     // paged: the unchecked steps need only full prefix units (the page-table
-    // path serves every refill)
-    const bool fp = pipe && config().fast_ring != 0 && sa.prefix_len % kUnitKeys == 0;
+    // path serves every refill); FAST 5 also writes O (one-slot plans)
     if constexpr (PAGED)
       st = (sa.cache32 && p.streams == 2)
-               ? (!pipe ? launch_split<T, D, 2, true, true>(sa, p, stream)
-                  : fp  ? launch_split<T, D, 2, true, true, true, 1>(sa, p, stream)
-                        : launch_split<T, D, 2, true, true, true>(sa, p, stream))
-           : p.streams == 2 ? (!pipe ? launch_split<T, D, 2, true>(sa, p, stream)
-                               : fp  ? launch_split<T, D, 2, true, false, true, 1>(sa, p, stream)
-                                     : launch_split<T, D, 2, true, false, true>(sa, p, stream))
-                            : (!pipe ? launch_split<T, D, 1, true>(sa, p, stream)
-                               : fp  ? launch_split<T, D, 1, true, false, true, 1>(sa, p, stream)
-                                     : launch_split<T, D, 1, true, false, true>(sa, p, stream));
+               ? (!pipe     ? launch_split<T, D, 2, true, true>(sa, p, stream)
+                  : fm == 5 ? launch_split<T, D, 2, true, true, true, 5>(sa, p, stream)
+                  : fm == 1 ? launch_split<T, D, 2, true, true, true, 1>(sa, p, stream)
+                            : launch_split<T, D, 2, true, true, true>(sa, p, stream))
+           : p.streams == 2 ? (!pipe     ? launch_split<T, D, 2, true>(sa, p, stream)
+                               : fm == 5 ? launch_split<T, D, 2, true, false, true, 5>(sa, p, stream)
+                               : fm == 1 ? launch_split<T, D, 2, true, false, true, 1>(sa, p, stream)
+                                         : launch_split<T, D, 2, true, false, true>(sa, p, stream))
+                            : (!pipe     ? launch_split<T, D, 1, true>(sa, p, stream)
+                               : fm == 5 ? launch_split<T, D, 1, true, false, true, 5>(sa, p, stream)
+                               : fm == 1 ? launch_split<T, D, 1, true, false, true, 1>(sa, p, stream)
+                                         : launch_split<T, D, 1, true, false, true>(sa, p, stream));
     else
       st = p.wide             ? launch_wide<T, D>(sa, p, stream)
            : p.streams == 2   ? (!pipe    ? launch_split<T, D, 2, false>(sa, p, stream)
@@ -2547,7 +2550,7 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   // skipped (the 16-sequence decode shape: its ~5 us combine of ~55 us).
   const bool o_dense = o_strides[3] == 1 && o_strides[2] == head_dim && o_strides[1] == (int64_t)q_len * head_dim &&
                        o_strides[0] == (int64_t)num_heads * q_len * head_dim;
-  sa.direct_out = p.n_slots == 1 && !p.wide && !kv.paged() && lse == nullptr && o_dense && config().direct_out != 0 &&
+  sa.direct_out = p.n_slots == 1 && !p.wide && lse == nullptr && o_dense && config().direct_out != 0 &&
                          config().pipe != 0
                      ? 1
                      : 0;
