@@ -37,9 +37,15 @@ eager        = the drop-in called eagerly as the reference's callers do:
                run_tree_sparse_kernel(q, k, v, tree_mask) (metadata built per
                call) and the forward with prebuilt metadata, host cost included
 workloads    = the other forward workloads (16-sequence decode, 1024-token
-               wide tree, 70B layout), each timed like the headline: us per
-               call, split-KV and combine, roofline fraction and bound
-cpu_baseline = also records the host CPU model and the oracle's dtype
+               wide tree, 70B layout and its BLOCK_M x BLOCK_N sweep
+               64x32 / 64x128 / 16x64), each timed like the headline: us per
+               call, split-KV and combine, roofline fraction and bound, and
+               its own cpu_baseline (the oracle over a bounded sample, query
+               heads chunked to bound the fp32 score tensor; the sweep
+               entries reuse their base workload's, the oracle having no
+               block sizes)
+cpu_baseline = also records the host CPU model, the oracle's dtype and the
+               head chunking
 backward     = tree_sparse_attention_bwd (dQ, dK, dV) over the same cycled
                K/V, against the MFMA and HBM peaks
 paged        = the same forward reading FlashInfer's paged cache in place
@@ -93,7 +99,12 @@ def algorithmic_flops(w, mask) -> float:
     return 4.0 * w.q_heads * w.head_dim * (w.batch * w.tree_len * w.prefix_len + pairs)
 
 
-def cpu_baseline(w, q, k, v, mask, seconds: float):
+def cpu_baseline(w, q, k, v, mask, seconds: float, head_chunk: int = 8):
+    """The fp32 dense+mask oracle (benchmark.py:8-35 restated) on the host
+    cores over a bounded sample: one warm-up call, then as many full calls as
+    fit in `seconds` (at least one).  `head_chunk` query heads are processed
+    at a time (the [B, chunk, T, KV] fp32 score tensor bounds memory; the
+    result does not depend on it)."""
     import torch
 
     from oracle.attn_oracle import dense_mask_attention
@@ -101,13 +112,14 @@ def cpu_baseline(w, q, k, v, mask, seconds: float):
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     t0 = time.perf_counter()
-    dense_mask_attention(q, k, v, mask, w.prefix_len, head_chunk=8)
+    dense_mask_attention(q, k, v, mask, w.prefix_len, head_chunk=head_chunk)
     t1 = time.perf_counter() - t0
     n = max(1, min(1000, int(seconds / max(t1, 1e-6))))
     t0 = time.perf_counter()
     for _ in range(n):
-        dense_mask_attention(q, k, v, mask, w.prefix_len, head_chunk=8)
+        dense_mask_attention(q, k, v, mask, w.prefix_len, head_chunk=head_chunk)
     dt = (time.perf_counter() - t0) / n
+    score_mib = w.batch * min(head_chunk, w.q_heads) * w.tree_len * w.kv_len * 4 / 2 ** 20
     return {
         "value": w.kv_bytes() / dt / 1e12,
         "unit": "TB/s",
@@ -116,7 +128,10 @@ def cpu_baseline(w, q, k, v, mask, seconds: float):
         "cpu_model": _cpu_model(),
         "dtype": "fp32",
         "kind": "port",
-        "sample": f"{n} full calls of the fp32 dense+mask oracle on the same inputs (torch CPU, {cores} threads)",
+        "head_chunk": head_chunk,
+        "sample": f"{n} full calls of the fp32 dense+mask oracle on the same inputs after one warm-up call "
+                  f"(torch CPU, {cores} threads; {head_chunk} query heads per chunk, "
+                  f"{score_mib:.0f} MiB of fp32 scores per chunk)",
     }
 
 
@@ -239,16 +254,31 @@ def eager_call_timing(w, qd, ks, vs, mask_dev, meta, reps: int = 100, batches: i
     return res
 
 
-def workload_timing(name: str, steps: int, cold_mib: int):
-    """One forward workload (split-KV + combine) timed as the headline is:
-    graph of `steps` calls (median of 5 replays), the combine alone, cold
-    K/V copies."""
+def workload_by_name(name: str):
+    """A named workload, or `name@BMxBN`: the same workload at other block sizes."""
+    from tsfa import configs
+
+    base, _, blocks = name.partition("@")
+    w = configs.WORKLOADS[base]
+    if blocks:
+        bm, bn = (int(x) for x in blocks.lower().split("x"))
+        w = w.with_blocks(bm, bn)
+    return w
+
+
+def workload_timing(name: str, steps: int, cold_mib: int, cpu_seconds: float = 0.0, cpu_cache=None):
+    """One forward workload timed as the headline is: graph of `steps` calls
+    (median of 5 replays), the combine alone, cold K/V copies; plus its CPU
+    baseline (the fp32 oracle over a bounded sample) when cpu_seconds > 0.
+    One-slot plans launch no combine (the split kernel writes O): the combine
+    region is then not captured, and the split kernel is the whole call."""
     import torch
 
     from tsfa import _lib, configs
     import tree_sparse_flashattn as tsf
 
-    w = configs.WORKLOADS[name]
+    w = workload_by_name(name)
+    base = name.partition("@")[0]
     dev = torch.device("cuda", 0)
     q, k, v = configs.make_qkv(w)
     mask = configs.make_tree_mask(w)
@@ -261,6 +291,7 @@ def workload_timing(name: str, steps: int, cold_mib: int):
     meta = build(mask.to(dev), w.prefix_len, w.block_m, w.block_n)
     out = torch.empty_like(qd)
     lib = _lib.load()
+    plan = _lib.fwd_plan(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len, w.head_dim)
 
     def call(i):
         tsf.tree_sparse_attention_fwd(qd, ks[i % copies], vs[i % copies], meta, out=out)
@@ -268,8 +299,9 @@ def workload_timing(name: str, steps: int, cold_mib: int):
     for i in range(3):
         call(i)
     torch.cuda.synchronize()
-    secs = {}
-    for region, kmask in (("full", 3), ("combine", 2)):
+    secs = {"combine": 0.0}
+    regions = (("full", 3), ("combine", 2)) if plan["slots"] > 1 else (("full", 3),)
+    for region, kmask in regions:
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -306,13 +338,27 @@ def workload_timing(name: str, steps: int, cold_mib: int):
     tflops, gbps = flops / split_s / 1e12, kvb / split_s / 1e9
     del ks, vs
     torch.cuda.empty_cache()
-    return {"us_per_call": round(secs["full"] * 1e6, 2), "split_kernel_us": round(split_s * 1e6, 2),
-            "combine_kernel_us": round(secs["combine"] * 1e6, 2), "bound": "mfma" if mfma_bound else "hbm",
-            "frac": round(tflops / MFMA_PEAK_TFLOPS if mfma_bound else gbps / HBM_PEAK_GBPS, 4),
-            "achieved": round(tflops, 1) if mfma_bound else round(gbps, 1),
-            "unit": "TFLOP/s" if mfma_bound else "GB/s", "algorithmic_flops": flops, "algorithmic_bytes": kvb,
-            "steps": steps, "kv_copies_cycled": copies,
-            "plan": _lib.fwd_plan(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len, w.head_dim)}
+    res = {"us_per_call": round(secs["full"] * 1e6, 2), "split_kernel_us": round(split_s * 1e6, 2),
+           "combine_kernel_us": round(secs["combine"] * 1e6, 2), "bound": "mfma" if mfma_bound else "hbm",
+           "frac": round(tflops / MFMA_PEAK_TFLOPS if mfma_bound else gbps / HBM_PEAK_GBPS, 4),
+           "achieved": round(tflops, 1) if mfma_bound else round(gbps, 1),
+           "unit": "TFLOP/s" if mfma_bound else "GB/s", "algorithmic_flops": flops, "algorithmic_bytes": kvb,
+           "block_m": w.block_m, "block_n": w.block_n, "steps": steps, "kv_copies_cycled": copies, "plan": plan,
+           "tokens_per_s": round(w.batch * w.tree_len / secs["full"], 1), "cpu_baseline": None}
+    if cpu_seconds > 0:
+        cache = {} if cpu_cache is None else cpu_cache
+        if base not in cache:
+            # bound the fp32 score tensor to ~0.6 GB per head chunk
+            per_head = w.batch * w.tree_len * w.kv_len * 4
+            chunk = max(1, min(8, w.q_heads, int(0.6e9 // per_head)))
+            _log(f"[bench] cpu baseline {base} (head chunk {chunk}) ...")
+            cache[base] = cpu_baseline(w, q, k, v, mask, cpu_seconds, head_chunk=chunk)
+        cb = dict(cache[base])
+        if base != name:
+            cb["sample"] += f"; measured on {base} (the oracle does not depend on BLOCK_M / BLOCK_N)"
+        cb["vs_gpu"] = round(cb["us_per_call"] / res["us_per_call"], 1)
+        res["cpu_baseline"] = cb
+    return res
 
 
 def paged_timing(w, qd, ks, vs, meta, steps: int, page_size: int, contiguous_us: float):
@@ -453,8 +499,12 @@ def main():
     ap.add_argument("--paged-page-size", type=int, default=16,
                     help="also time the paged-cache forward at this page size (0: skip)")
     ap.add_argument("--workloads", default="batched-decode-b16-p2048:100,wide-tree-1024-p16384:10,"
-                    "llama3-70b-b4-p32768:5",
-                    help="other forward workloads timed into the `workloads` object, as name:steps ('' skips)")
+                    "llama3-70b-b4-p32768:5,llama3-70b-b4-p32768@64x32:5,llama3-70b-b4-p32768@64x128:5,"
+                    "llama3-70b-b4-p32768@16x64:5",
+                    help="other forward workloads timed into the `workloads` object, as name[@BMxBN]:steps "
+                         "('' skips)")
+    ap.add_argument("--workload-cpu-seconds", type=float, default=6.0,
+                    help="CPU baseline sample per other workload (0 skips)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain MIB-MiB device copy (rocprofv3 PMC calibration) and exit")
     args = ap.parse_args()
@@ -543,9 +593,13 @@ def main():
             out_s.append(a.elapsed_time(b) / 1e3)
         return sorted(out_s)
 
-    regions = {name: capture(mask) for name, mask in (("full", 3), ("combine", 2), ("split", 1))}
+    # one-slot plans launch no combine (the split kernel writes O): nothing to
+    # capture for it, and the split kernel is the whole call
+    kinds = (("full", 3), ("combine", 2), ("split", 1)) if plan["slots"] > 1 else (("full", 3), ("split", 1))
+    regions = {name: capture(mask) for name, mask in kinds}
     samples = {name: timed(*gs) for name, gs in regions.items()}
     secs = {name: v[len(v) // 2] / steps for name, v in samples.items()}
+    secs.setdefault("combine", 0.0)
     per_call_s = secs["full"]
     split_avg_s = secs["full"] - secs["combine"]
     _log(f"[bench] {steps} calls: {per_call_s * 1e6:.2f} us/call = split-KV {split_avg_s * 1e6:.2f} + combine "
@@ -623,10 +677,13 @@ def main():
         regions = None
         torch.cuda.empty_cache()
         result["workloads"] = {}
+        cpu_cache = {}
         for item in others:
             name, _, n = item.partition(":")
             _log(f"[bench] workload {name} ...")
-            result["workloads"][name] = workload_timing(name, int(n or 10), args.cold_mib)
+            result["workloads"][name] = workload_timing(
+                name, int(n or 10), args.cold_mib,
+                0.0 if args.no_cpu_baseline else args.workload_cpu_seconds, cpu_cache)
     if not args.no_cpu_baseline:
         _log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(w, q, k, v, mask, args.cpu_seconds)

@@ -38,3 +38,13 @@ int device_max_lds_per_block(int* out) {
 }
 
 }  // namespace tsfa
+
+extern "C" int tsfa_device_limits(int32_t* out2) {
+  if (out2 == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  int cus = 0, lds = 0;
+  if (tsfa::device_cu_count(&cus) != TSFA_OK || tsfa::device_max_lds_per_block(&lds) != TSFA_OK)
+    return TSFA_ERR_DEVICE;
+  out2[0] = cus;
+  out2[1] = lds;
+  return TSFA_OK;
+}

@@ -41,9 +41,6 @@
 //     one partial per row (O/l in the input dtype, fp32 (m, l)); a second
 //     kernel merges the partials (log-sum-exp) and writes O, each XCD merging
 //     the chunks its split workgroups wrote (the partials come from its L2).
-//   * wide_kernel runs the same work items with one wave per SIMD and 64 rows
-//     per wave (AGPR accumulators), halving LDS operand bytes per MFMA; the
-//     planner picks it for long prefixes under small trees.
 
 #include <math.h>
 #include <stdlib.h>
@@ -156,8 +153,6 @@ struct SplitArgs {
   uint32_t cps_b32, crs_b32;  // its page and row strides in bytes
   int item_order;  // within an XCD: 0 natural, 1 prefix runs first, 2 tree items first
   int fold_tree;   // no tree items: the last prefix split of each chunk also runs the tree units
-  int os_first;    // one-shot prefix runs: run units requested with Q (the rest once Q landed)
-  int rot_step;    // prefix run of chunk c starts at its unit (c * rot_step) mod n and wraps
   // One-slot plans with O contiguous [B, Hq, q_len, D] and no LSE asked: the
   // split kernel writes O itself (ws_o is O; split_kernel<..., FAST | 4>)
   // and no combine runs.  Host-side only.
@@ -281,7 +276,6 @@ template <int LPU, int K> __device__ inline void wait_units(int k) {
   }
 }
 
-__device__ inline void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // Workgroup barrier that also orders LDS accesses (compiler and hardware).
 __device__ inline void sync_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ inline void sync_all() { asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -304,69 +298,10 @@ __device__ inline float max3f(float a, float b, float c) {
   return r;
 }
 
-// Max / sum over lanes {l, l^32} (one gfx950 row-swap permute, no LDS).
-__device__ inline float pair_max(float x) {
-  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
-}
+// Sum over lanes {l, l^32} (one gfx950 row-swap permute, no LDS).
 __device__ inline float pair_sum(float x) {
   const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
-}
-
-// Loads [u_lo, u_lo + NL) of one half (K or V) of a 32-key unit, HBM -> LDS.
-// Load u covers 1 KB of the row-major tile (RPL key rows); 16-byte chunk pos
-// of key row `row` comes from chunk pos ^ swz(row) of the source row (the
-// reader applies the same XOR).
-// Fast path: the lane offset depends on u only through the swizzle, which
-// repeats every NOFF loads, so NOFF precomputed lane offsets and a scalar row
-// base per load address everything.  Slow path (a unit reaching past kv_len):
-// per-lane clamped rows; those keys are masked.  OFF32 addresses the slow
-// path like the fast one (scalar base, 32-bit lane offsets: fewer live VGPRs
-// for the wide kernel); otherwise per-lane 64-bit addresses (the 8-wave
-// kernel measured faster with them).
-template <typename T, int D, bool IS_V, int NL, bool OFF32 = false, bool NT = false>
-__device__ inline void dma_half(const T* base, int64_t stride, uint32_t lds_dst, int key0, int kv_len, int lane,
-                                int u_lo, const uint32_t* loff) {
-  constexpr int CPR = D / 8;
-  constexpr int RPL = 64 / CPR;
-  constexpr int NOFF = IS_V ? 1 : (D == 128 ? 4 : 2);
-  if (key0 + kUnitKeys <= kv_len) {
-    const char* rowp = reinterpret_cast<const char*>(base + (int64_t)(key0 + u_lo * RPL) * stride);
-    const int64_t step = (int64_t)RPL * stride * 2;
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int u = u_lo + i;
-      dma16_s<NT>(rowp, loff[u % NOFF], lds_dst + u * 1024);
-      rowp += step;
-    }
-  } else if (OFF32) {
-    // scalar base at row key0; a lane's row is at most 31 rows further and
-    // row strides stay below 2^26 elements, so its byte offset fits 32 bits.
-    // The lane index goes through an empty asm: this path runs once per run,
-    // and its lane terms hoisted out of the unit loop would hold registers
-    // (spilled) for the whole loop.
-    int ln_ = lane;
-    asm volatile("" : "+v"(ln_));
-    const char* rowp = reinterpret_cast<const char*>(base + (int64_t)key0 * stride);
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int u = u_lo + i;
-      const int row = u * RPL + ln_ / CPR, pos = ln_ % CPR;
-      const uint32_t rel = (uint32_t)(min(key0 + row, kv_len - 1) - key0);
-      const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
-      dma16_s(rowp, rel * (uint32_t)stride * 2u + (uint32_t)((pos ^ sw) << 4), lds_dst + u * 1024);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int u = u_lo + i;
-      const int row = u * RPL + lane / CPR, pos = lane % CPR;
-      const int key = min(key0 + row, kv_len - 1);
-      const int sw = IS_V ? swz_v<D>(row) : swz_k<D>(row);
-      dma16(base + (int64_t)key * stride + ((pos ^ sw) << 3), lds_dst + u * 1024);
-    }
-  }
 }
 
 // Loads [u_lo, u_lo + NL) of one half of a unit whose rows may reach past
@@ -524,13 +459,12 @@ template <bool V, typename I = int, typename N = int> struct FastSeq {
   N next;
 };
 
-// S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  PIPE
-// selects the software-pipelined unit loop (run_units_pipe).  FAST (every
+// S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  FAST (every
 // prefix unit full; 1: plain loads, 2: non-temporal K/V loads; paged runs
 // choose the hint at run time and take 1): prefix runs skip the per-unit
 // mask test, contiguous ring runs issue every unit by the run-base path, and
 // the steady ring steps use a fixed wait count.
-template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
+template <typename T, int D, int S, bool PAGED, bool C32 = false, int FAST = 0>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
   constexpr int FM = FAST & 3;              // unchecked ring steps: 0 off, 1 plain, 2 non-temporal loads
@@ -605,7 +539,7 @@ void split_kernel(const SplitArgs a) {
   unsigned char* sring = ring + ks * RB;
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
   const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-  // One-shot prefix runs (pipelined loop, contiguous K/V, two streams): unit i
+  // One-shot prefix runs (contiguous K/V, two streams): unit i
   // of a run of at most NOS units sits in stage i of the ring followed by the
   // mask area (a prefix run does not use it), Q in the last two stages; every
   // unit is requested up front (the two behind Q once Q is read) and the loop
@@ -693,7 +627,6 @@ void split_kernel(const SplitArgs a) {
       dma_tail<T, D, false, LPU>(dbase, dstride, sb, key0, a.kv_len, lane, dma_u0);
     }
   };
-  auto issue = [&](int st, int key0) { issue_at(sring_lds + st * SB, key0); };
 
   // Q^T operand fragments of the wave's row tile: row r = row0 + rg*32 + ln,
   // d = kk*16 + lh*8 + [0, 8); Q is negated for a negative scale.
@@ -790,137 +723,7 @@ void split_kernel(const SplitArgs a) {
     return s;
   };
 
-  // V^T fragments of one unit (stage base sv): lane i of 16-lane group x gets
-  // keys 16*s2 + 8*jj + 4*(x>>1) + [0,4) of d = dt*32 + 16*(x&1) + i.
-  auto read_v = [&](const unsigned char* sv, i16x4 (&vh)[DT][2][2]) {
-    const int base = (int)(sv - smem) + v_off0;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          vh[dt][s2][jj] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (TSFA_LDS i16x4*)(smem + (base ^ (dt << 6)) + (16 * s2 + 8 * jj) * ROWB));
-  };
-  // Online softmax of one unit's S^T (VALU only): masks the unit's invisible
-  // keys, re-bases (m, l, O) when the running max grows past the lazy
-  // threshold, and leaves P = exp2(s*scale - m) rounded to T in pb.
-  // One wave runs this while the other wave of its SIMD issues MFMAs, so its
-  // dependency chains are exposed: the max and the row sum are trees (depth
-  // 3 and 4), not chains.
-  auto softmax = [&](f32x16& s, bool masked, uint32_t mask, V8 (&pb)[2]) {
-    if (masked) {
-      // a real (wave-uniform) branch: the empty asm keeps the compiler from
-      // speculating the mask into selects that every unmasked unit would pay
-      asm volatile("" ::: "memory");
-      const uint32_t w = mask >> (4 * lh);
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (!((w >> (8 * (i >> 2) + (i & 3))) & 1u)) s[i] = -INFINITY;
-    }
-    const float mx = max3f(max3f(max3f(s[0], s[1], s[2]), max3f(s[3], s[4], s[5]), max3f(s[6], s[7], s[8])),
-                           max3f(max3f(s[9], s[10], s[11]), max3f(s[12], s[13], s[14]), s[15]), -INFINITY);
-    if (__ballot(mx > m_lim) != 0) {  // false while both are -inf
-      const float m_new = fmaxf(m_run, pair_max(mx));
-      // alpha = 1 when both are -inf (tree_sparse_flashattn.py:276, :324)
-      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sl2);
-      m_run = m_new;
-      mb = (m_new == -INFINITY) ? 0.f : m_new * sl2;
-      m_lim = m_new + thr_raw;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-    }
-    // p = 0 where the score is -inf (tree_sparse_flashattn.py:274, :322):
-    // with a finite reference point exp2(-inf) = 0; a row with no visible key
-    // yet keeps m = -inf and reference 0, so p = exp2(-inf) = 0.
-    float p[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -mb));
-      pb[i >> 3][i & 7] = (T)p[i];  // P rounded to the input dtype (:278)
-    }
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-      for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
-    l_run += p[0];
-  };
-  // O^T += V^T P^T; k-step s2 covers keys 16*s2 + 8*jj + 4*lh + [0,4), the
-  // order P^T's lane holds them in (elements 8*s2 .. 8*s2+7 of S^T).
-  auto pv = [&](const i16x4 (&vh)[DT][2][2], const V8 (&pb)[2]) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
-        o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
-      }
-  };
-
-  // The streams' shares of a run of n units (unit i of the run: key0_of(i),
-  // masked_of(i), mask_of(i)): stream s takes units s, s+S, ...  One
-  // workgroup barrier per step; units j and j+1 occupy two ring stages, NS-2
-  // more are in flight.  A step of a wave is a VALU phase (the softmax of
-  // unit j) and an MFMA phase (O^T += V^T P^T of unit j, then S^T of unit
-  // j+1).  The two waves of a SIMD (w and w+4) run half a step apart: waves
-  // 4..7 take their VALU phase before the step's barrier, waves 0..3 after
-  // it, so each SIMD has one wave issuing MFMAs while the other issues the
-  // softmax (the MFMA phase runs at raised wave priority).  Both read K of
-  // unit j+1 only after barrier j, and both finish reading unit j-1 before
-  // it, so the barrier still orders the ring.
-  auto run_units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
-    const int mine = n > ks ? (n - ks + S - 1) / S : 0;
-    const int steps = (n + S - 1) / S;
-    for (int j = pre; j < NS - 1 && j < mine; ++j) issue(j, key0_of(ks + S * j));
-    if (PAGED && NS - 1 < mine) prefetch(key0_of(ks + S * (NS - 1)));
-    f32x16 s_cur;
-    if (mine > 0) wait_units<LPU, NS - 2>(min(mine - 1, NS - 2));  // unit 0 landed
-    sync_lds();
-    if (mine > 0 && active) {
-      i16x8 kf[KSTEPS];
-      read_k(sring, kf);
-      s_cur = qk(kf);
-    }
-    const bool late = wave >= 4;  // barrier after the softmax (wave-uniform)
-    for (int j = 0; j < steps; ++j) {
-      const bool work = j < mine && active;
-      const int ui = ks + S * j;
-      // unit j+1 landed for every wave of the stream; stage (j-1)%NS is free
-      auto ring_step = [&]() {
-        if (j + 1 < mine) wait_units<LPU, NS - 3>(min(mine - 2 - j, NS - 3));
-        __builtin_amdgcn_sched_barrier(0);
-        sync_lds();
-        __builtin_amdgcn_sched_barrier(0);
-        if (j + NS - 1 < mine) issue((j + NS - 1) % NS, key0_of(ks + S * (j + NS - 1)));
-        if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
-      };
-      if (!late) ring_step();
-      V8 pb[2];
-      i16x4 vh[DT][2][2];
-      if (work) {
-        read_v(sring + (j % NS) * SB + HALF, vh);
-        softmax(s_cur, masked_of(ui), mask_of(ui), pb);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (late) ring_step();
-      if (work) {
-        // K of unit j+1 after the softmax (its registers are not live there);
-        // the O^T MFMAs cover the read.  On the last step this reads a stale
-        // stage that no load targets; that S^T is never used.
-        i16x8 kf[KSTEPS];
-        read_k(sring + ((j + 1) % NS) * SB, kf);
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(1);
-        pv(vh, pb);
-        s_cur = qk(kf);
-        __builtin_amdgcn_s_setprio(0);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  };
-  // ---- software-pipelined unit loop (PIPE) ----
+  // ---- the unit loop (software-pipelined) ----
   // Iteration j of a wave: the mask and row statistics of unit j (whose S^T
   // the previous iteration computed), then group 1 -- the S^T MFMAs of unit
   // j+1 with the exponentials and rounded P of unit j between them -- then
@@ -930,8 +733,9 @@ void split_kernel(const SplitArgs a) {
   // and statistics, O^T by the re-base) happens an MFMA group and a barrier
   // after the MFMAs that wrote it.  The running max moves without a branch
   // (a re-based row takes the unit's row max and scales l at once).  The ring
-  // is used as by run_units: iteration j reads K of unit j+1 and V of unit j
-  // after barrier j.
+  // is used this way: iteration j reads K of unit j+1 and V of unit j after
+  // barrier j, and both finish reading unit j-1 before it, so the barrier
+  // orders the ring.
   auto apply_mask = [&](f32x16& s, uint32_t mask) {
     const uint32_t w = mask >> (4 * lh);
 #pragma unroll
@@ -1226,8 +1030,7 @@ void split_kernel(const SplitArgs a) {
   };
   // issue_of(lds stage, i) requests run unit i (keys key0_of(i)) into a stage
   auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
-    if constexpr (PIPE) run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c);
-    else run_units(n, pre, key0_of, masked_of, mask_of);
+    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c);
   };
 
   if (!is_tree) {
@@ -1236,13 +1039,7 @@ void split_kernel(const SplitArgs a) {
     const int P = a.prefix_len;
     const int u_lo = slot * a.units_per_split;
     const int n = min(a.units_per_split, a.n_pu - u_lo);
-    // The row chunks of one split read its units in rotated orders, so that
-    // they do not all request the same K/V lines at the same time.
-    const int rot = n > 0 ? (int)((uint32_t)(chunk * a.rot_step) % (uint32_t)n) : 0;
-    auto key0_of = [&](int i) {
-      const int r = i + rot;
-      return (u_lo + (r >= n ? r - n : r)) * kUnitKeys;
-    };
+    auto key0_of = [&](int i) { return (u_lo + i) * kUnitKeys; };
     // Contiguous K/V: run unit i's row pointer is this wave's base for the
     // run plus one product (the general path rebuilds it from the key with
     // 64-bit scalar arithmetic and range checks, on the scalar unit the
@@ -1254,7 +1051,7 @@ void split_kernel(const SplitArgs a) {
     int n_fast = 0;
     uint32_t m0_off = 0;
     auto issue_prefix = [&](uint32_t sb, int i) {
-      const int r = i + rot, ri = r >= n ? r - n : r;
+      const int ri = i;
       if constexpr (FM != 0 && !PAGED) {
         // one-shot runs (two streams only) issue by the general path: their
         // run base is not set up, to keep Q's request first
@@ -1273,22 +1070,20 @@ void split_kernel(const SplitArgs a) {
     // With QS > 1 the ring prologue reuses Q stages: one more barrier first.
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     int pre;
-    if (PIPE && !PAGED && S == 2 && n <= NOS) {
+    if (!PAGED && S == 2 && n <= NOS) {
       // one-shot: Q in the last S stages, run units below NOS - S with it
       oneshot = true;
       st_base = ring_lds + ks * SB;
       st_step = S * SB;
       st_mask = 31;
-      const int early = min(n, NOS - S), first = min(early, max(a.os_first, S));
+      const int early = min(n, NOS - S);
       pre = early > ks ? (early - ks + S - 1) / S : 0;
-      const int pre1 = first > ks ? (first - ks + S - 1) / S : 0;
       TSFA_STAMP(62);
       issue_q(true);
-      for (int j = 0; j < pre1; ++j) issue_prefix(stage(j), ks + S * j);
+      for (int j = 0; j < pre; ++j) issue_prefix(stage(j), ks + S * j);
       TSFA_STAMP(60);
-      wait_units<LPU, NOS - S>(pre1);
+      wait_units<LPU, NOS - S>(pre);  // Q landed (loads complete in order)
       TSFA_STAMPW(35);
-      for (int j = pre1; j < pre; ++j) issue_prefix(stage(j), ks + S * j);
       sync_lds();
       TSFA_STAMP(1);
       read_q(true);
@@ -1550,525 +1345,6 @@ void split_kernel(const SplitArgs a) {
   TSFA_CYC_STORE;
 }
 
-// ------------------------------------------------------------- wide kernel
-// The same work item (a chunk's prefix run or tree units, one partial per row)
-// with one wave per SIMD and 64 query rows per wave (two 32-row tiles):
-//   * each K / V^T fragment read from LDS feeds two MFMAs, half the LDS bytes
-//     per MFMA of 32-row waves; the 128 O^T accumulators per lane fit beside
-//     the operands because a lone wave owns all 512 registers (AGPRs hold O);
-//   * a chunk is 256 rows and one key stream: every K/V unit is staged once
-//     per workgroup, 8 ring stages of 32 keys (D=128);
-//   * iteration j issues O^T += V^T P^T of unit j-1 and S^T of unit j+1 (32
-//     MFMAs) and, between them, the softmax of unit j: the lone wave keeps the
-//     matrix core busy while its VALU works.  The running max moves row by row
-//     without a branch; the rare O rescale waits for the end of the iteration
-//     (after O^T of unit j-1, before that of unit j).
-constexpr int kWideWaves = 4;
-
-template <typename T, int D>
-__global__ __launch_bounds__(kWideWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void wide_kernel(const SplitArgs a) {
-  typedef typename Mma<T>::vec8 V8;
-  constexpr int NW = kWideWaves;
-  constexpr int NT = NW * 64;
-  constexpr int ROWS = 64 * NW;        // rows per chunk
-  constexpr int ROWB = D * 2;          // bytes of one key row
-  constexpr int HALF = kUnitKeys * ROWB;
-  constexpr int SB = 2 * HALF;         // ring stage: K then V of one unit
-  constexpr int NS = kRingBytes / SB;  // stages
-  constexpr int LPH = HALF / 1024;     // 1 KB loads per half
-  constexpr int LPU = 2 * LPH / NW;    // loads per unit per wave
-  constexpr int QS = ROWS * ROWB / SB; // stages the chunk's Q occupies at start
-  constexpr int KSTEPS = D / 16;
-  constexpr int DT = D / 32;
-  static_assert(ROWS == kMaxRows, "chunk rows");
-  static_assert(NS >= 4 && QS < NS && QS * SB == ROWS * ROWB && LPU >= 1 && LPU * (NS - 2) < 64 &&
-                    LPH % (NW / 2) == 0,
-                "ring geometry");
-
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  unsigned char* ring = smem;
-  uint32_t* masks = reinterpret_cast<uint32_t*>(smem + kRingBytes);
-  int* vis = reinterpret_cast<int*>(masks + kMaskWords);
-  int* misc = vis + kMaxTreeUnits;  // kMiscInts ints
-
-  // An AGPR in use: the MFMAs keep their accumulators in AGPRs (O^T needs
-  // them: 128 per lane beside the VGPR operands).
-  asm volatile("" ::: "a0");
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ln = lane & 31, lh = lane >> 5;
-
-  const int item = work_item(a);
-  if (item < 0) return;
-  const int rest = fdiv(item, a.fd_chunks);
-  const int chunk = item - rest * a.n_chunks;
-  const int bk = fdiv(rest, a.fd_slots);
-  const int slot = rest - bk * a.n_slots;
-  const int b = fdiv(bk, a.fd_kvh);
-  const int kvh = bk - b * a.num_kv_heads;
-  const bool is_tree = !a.fold_tree && slot == a.n_slots - 1;  // as in split_kernel
-  const bool do_tree = slot == a.n_slots - 1;
-
-  const int G = a.group;
-  const int TG = a.q_len * G;
-  const int row0 = chunk * ROWS;
-  const int rows_chunk = min(ROWS, TG - row0);
-  const int tok_lo = (int)fdiv(row0, a.fd_group);
-  const float sl2 = a.scale_log2;
-  const float thr_raw = kRescaleLog2 / sl2;
-
-  const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
-  const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
-  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-
-  // Waves 0 .. NW/2-1 move the K half of each unit, the others the V half.
-  const bool dma_v = wave >= NW / 2;
-  const int dma_u0 = (wave % (NW / 2)) * LPU;
-  uint32_t loff[D == 128 ? 4 : 2];
-#pragma unroll
-  for (int u = 0; u < (D == 128 ? 4 : 2); ++u)
-    loff[u] = dma_v ? dma_lane_off<D, true>(u, a.svn, lane) : dma_lane_off<D, false>(u, a.skn, lane);
-  auto issue = [&](int st, int key0) {
-    const uint32_t sb = ring_lds + st * SB;
-    if (dma_v)
-      dma_half<T, D, true, LPU, true>(vbase, a.svn, sb + HALF, key0, a.kv_len, lane, dma_u0, loff);
-    else
-      dma_half<T, D, false, LPU, true>(kbase, a.skn, sb, key0, a.kv_len, lane, dma_u0, loff);
-  };
-
-  // Q^T fragments of the wave's two row tiles: tile t holds row
-  // row0 + wave*64 + t*32 + ln, d = kk*16 + lh*8 + [0, 8).
-  i16x8 qf[2][KSTEPS];
-  const short qsgn = a.neg_q ? (short)0x8000 : (short)0;
-  int row_tt[2];  // token of the lane's row in each tile, chunk-relative
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int qrow = row0 + wave * 64 + t * 32 + ln;
-    row_tt[t] = qrow < TG ? (int)fdiv(qrow, a.fd_group) - tok_lo : 0;
-  }
-  auto load_q = [&]() {  // straight into registers (rows past the end load zeros)
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) qf[t][kk] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
-      const int qrow = row0 + wave * 64 + t * 32 + ln;
-      if (qrow < TG) {
-        const int tq = (int)fdiv(qrow, a.fd_group);
-        const int g = qrow - tq * G;
-        const T* qp = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh +
-                      (int64_t)tq * a.sqm + lh * 8;
-#pragma unroll
-        for (int kk = 0; kk < KSTEPS; ++kk) qf[t][kk] = *reinterpret_cast<const i16x8*>(qp + kk * 16) ^ qsgn;
-      }
-    }
-    // consume the loads here, before any K/V prefetch joins the vmcnt queue
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk) asm volatile("" : : "v"(qf[t][kk]));
-  };
-  // Q through LDS: the chunk's rows go HBM -> LDS into the last QS stages,
-  // issued ahead of the first K/V units; rows past the end repeat the last
-  // row (their outputs are never stored).
-  auto issue_q = [&]() {
-    constexpr int RPL = 1024 / ROWB, CPR = D / 8;
-    constexpr int QL = ROWS / RPL / NW;  // 1 KB loads per wave
-#pragma unroll
-    for (int i = 0; i < QL; ++i) {
-      const int l0 = (wave * QL + i) * RPL;
-      const int row = l0 + lane / CPR, pos = lane % CPR;
-      const int R = min(row0 + row, TG - 1);
-      const int tq = (int)fdiv(R, a.fd_group);
-      const int g = R - tq * G;
-      const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)tq * a.sqm +
-                     ((pos ^ swz_k<D>(row)) << 3);
-      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(ring + (NS - QS) * SB + l0 * ROWB)));
-    }
-  };
-  auto read_q = [&]() {
-    const unsigned char* qs = ring + (NS - QS) * SB;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int r = wave * 64 + t * 32 + ln;
-#pragma unroll
-      for (int kk = 0; kk < KSTEPS; ++kk)
-        qf[t][kk] = *reinterpret_cast<const i16x8*>(qs + r * ROWB + (((2 * kk + lh) ^ swz_k<D>(r)) << 4)) ^ qsgn;
-    }
-  };
-
-  // Running state per lane and tile (query row ln of the tile): O^T element
-  // i of d-tile dt is d = dt*32 + 8*(i/4) + 4*lh + i%4; l_run is this lane's
-  // half of the row sum.
-  f32x16 o[2][DT];
-  float m_run[2], m_lim[2], mb[2], l_run[2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    m_run[t] = -INFINITY;
-    m_lim[t] = -INFINITY;
-    mb[t] = 0.f;
-    l_run[t] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) o[t][dt][i] = 0.f;
-  }
-
-  const int vx = lane >> 4, vi = lane & 15;
-  const int vkey = 4 * (vx >> 1) + (vi >> 2);
-  int v_off[DT], k_off[KSTEPS];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const int d = dt * 32 + 16 * (vx & 1) + 4 * (vi & 3);
-    v_off[dt] = vkey * ROWB + (((d >> 3) ^ swz_v<D>(vkey)) << 4) + ((d & 7) << 1);
-  }
-#pragma unroll
-  for (int kk = 0; kk < KSTEPS; ++kk) k_off[kk] = ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4);
-
-  auto read_k = [&](const unsigned char* sk, i16x8 (&kf)[KSTEPS]) {
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) kf[kk] = *reinterpret_cast<const i16x8*>(sk + k_off[kk]);
-  };
-  auto read_v = [&](const unsigned char* sv, i16x4 (&vh)[DT][2][2]) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          vh[dt][s2][jj] =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((TSFA_LDS i16x4*)(sv + v_off[dt] + (16 * s2 + 8 * jj) * ROWB));
-  };
-  // S^T of one unit for both tiles, tile 0 first: its MFMAs only need tile
-  // 0's scores consumed, so they can run while tile 1's softmax does.
-  auto qk1 = [&](const i16x8 (&kf)[KSTEPS], f32x16& st, int t) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) st[i] = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < KSTEPS; ++kk) st = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[t][kk]), st);
-  };
-  auto qk2 = [&](const i16x8 (&kf)[KSTEPS], f32x16 (&s)[2]) {
-    qk1(kf, s[0], 0);
-    qk1(kf, s[1], 1);
-  };
-  // O^T += V^T P^T for both tiles (k-step s2 covers keys 16*s2 + 8*jj + 4*lh
-  // + [0,4), the order P^T's lane holds them in).
-  auto pv1 = [&](const i16x4 (&vh)[DT][2][2], const V8 (&pbt)[2], int t) {
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
-        o[t][dt] = Mma<T>::run(bit_cast<V8>(vf), pbt[s2], o[t][dt]);
-      }
-  };
-  auto pv2 = [&](const i16x4 (&vh)[DT][2][2], const V8 (&pb)[2][2]) {
-    pv1(vh, pb[0], 0);
-    pv1(vh, pb[1], 1);
-  };
-  auto apply_mask = [&](f32x16& s, uint32_t mask) {
-    const uint32_t w = mask >> (4 * lh);
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (!((w >> (8 * (i >> 2) + (i & 3))) & 1u)) s[i] = -INFINITY;
-  };
-  // Row statistics of one tile (VALU, no branch): the row max over both lane
-  // halves; when it passes the lazy threshold the row re-bases on it and
-  // alpha scales l now and O at the end of the iteration.
-  auto stats = [&](const f32x16& s, int t, float& alpha) {
-    const float mx = max3f(max3f(max3f(s[0], s[1], s[2]), max3f(s[3], s[4], s[5]), max3f(s[6], s[7], s[8])),
-                           max3f(max3f(s[9], s[10], s[11]), max3f(s[12], s[13], s[14]), s[15]), -INFINITY);
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-    const float rmax = max3f(__uint_as_float(sw[0]), __uint_as_float(sw[1]), -INFINITY);
-    // rmax > m_lim >= m_run, so a re-based row takes rmax; false while both are -inf
-    const bool need = rmax > m_lim[t];
-    const float m_new = need ? rmax : m_run[t];
-    // m_run = -inf gives alpha = 0 (O and l are still 0) (tree_sparse_flashattn.py:276, :324)
-    alpha = need ? __builtin_amdgcn_exp2f((m_run[t] - m_new) * sl2) : 1.f;
-    m_run[t] = m_new;
-    mb[t] = (m_new == -INFINITY) ? 0.f : m_new * sl2;
-    m_lim[t] = m_new + thr_raw;
-    l_run[t] *= alpha;
-    return need;
-  };
-  // P = exp2(s*scale - m) rounded to T (tree_sparse_flashattn.py:274-278,
-  // :322): masked scores give exp2(-inf) = 0, and so does a row with no
-  // visible key yet (m = -inf, reference 0).
-  auto expo = [&](const f32x16& s, int t, float (&p)[16], int i0, int i1) {
-#pragma unroll
-    for (int i = i0; i < i1; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, -mb[t]));
-  };
-  auto sum_cvt = [&](float (&p)[16], int t, V8 (&pbt)[2]) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) pbt[i >> 3][i & 7] = (T)p[i];
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-      for (int i = 0; i < w; ++i) p[i] = p[i] + p[i + w];
-    l_run[t] += p[0];
-  };
-  // Empty asm that "writes" its operands: the values must exist at this point
-  // (keeps IR passes from sinking a phase's VALU work, whose results are only
-  // read in the next iteration, out of the phase it overlaps).
-  auto pin_f = [&](float (&p)[16], int i0, int i1) {
-#pragma unroll
-    for (int i = i0; i < i1; ++i) asm volatile("" : "+v"(p[i]));
-  };
-  auto pin_pb = [&](V8 (&pbt)[2]) {
-    asm volatile("" : "+v"(pbt[0]));
-    asm volatile("" : "+v"(pbt[1]));
-  };
-  auto pin_v = [&](i16x4 (&vh)[DT][2][2]) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) asm volatile("" : "+v"(vh[dt][s2][jj]));
-  };
-  // One phase of an iteration: NM MFMAs, each followed by up to NV VALU ops.
-  auto interleave = [&](auto nm, auto nv) {
-#pragma unroll
-    for (int g = 0; g < decltype(nm)::value; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x402, decltype(nv)::value, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // A run of n units (unit i: keys key0_of(i); masked_of(i) / mask_of(i, t)
-  // the visibility of its keys for tile t).  Units pre .. NS-2 are issued
-  // here, the first pre by the caller.
-  auto run_units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of) {
-    for (int j = pre; j < NS - 1 && j < n; ++j) issue(j, key0_of(j));
-    if (n > 0) wait_units<LPU, NS - 2>(min(n - 1, NS - 2));  // unit 0 landed
-    sync_lds();
-    f32x16 s[2];
-    i16x4 vh[DT][2][2];
-    V8 pb[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) pb[t][s2] = bit_cast<V8>(i16x8{0, 0, 0, 0, 0, 0, 0, 0});
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) vh[dt][s2][jj] = i16x4{0, 0, 0, 0};
-    if (n > 0) {
-      i16x8 kf[KSTEPS];
-      read_k(ring, kf);
-      qk2(kf, s);
-      if (masked_of(0)) {
-        asm volatile("" ::: "memory");
-        apply_mask(s[0], mask_of(0, 0));
-        apply_mask(s[1], mask_of(0, 1));
-      }
-    }
-    for (int j = 0; j < n; ++j) {
-      // unit j+1 landed for every wave; stage (j-1)%NS is free
-      if (j + 1 < n) wait_units<LPU, NS - 3>(min(n - 2 - j, NS - 3));
-      __builtin_amdgcn_sched_barrier(0);
-      sync_lds();
-      __builtin_amdgcn_sched_barrier(0);
-      if (j + NS - 1 < n) issue((j + NS - 1) % NS, key0_of(j + NS - 1));
-      __builtin_amdgcn_sched_barrier(0);
-      {
-        // K of unit j+1 (on the last step a stale stage that no load targets;
-        // that S^T is never used).  O^T += V^T P^T of unit j-1 (zeros before
-        // the first unit) with the statistics and exponentials of unit j,
-        // then V^T of unit j and S^T of unit j+1 with the rest.
-        // Four phases of 8 MFMAs; every register an MFMA overwrites was
-        // consumed in an earlier phase (P^T of a tile by its O^T MFMAs, the
-        // scores of a tile by its exponentials).
-        constexpr int NM = 2 * DT;
-        i16x8 kf[KSTEPS];
-        float alpha[2], p0[16], p1[16];
-        read_k(ring + ((j + 1) % NS) * SB, kf);
-        pv1(vh, pb[0], 0);
-        const bool need0 = stats(s[0], 0, alpha[0]);
-        const bool need1 = stats(s[1], 1, alpha[1]);
-        expo(s[0], 0, p0, 0, 8);
-        pin_f(p0, 0, 8);
-        interleave(std::integral_constant<int, NM>{}, std::integral_constant<int, 6>{});
-        pv1(vh, pb[1], 1);
-        expo(s[0], 0, p0, 8, 16);
-        sum_cvt(p0, 0, pb[0]);
-        pin_pb(pb[0]);
-        interleave(std::integral_constant<int, NM>{}, std::integral_constant<int, 5>{});
-        qk1(kf, s[0], 0);
-        read_v(ring + (j % NS) * SB + HALF, vh);
-        expo(s[1], 1, p1, 0, 16);
-        pin_f(p1, 0, 16);
-        interleave(std::integral_constant<int, KSTEPS>{}, std::integral_constant<int, 5>{});
-        qk1(kf, s[1], 1);
-        sum_cvt(p1, 1, pb[1]);
-        pin_pb(pb[1]);
-        interleave(std::integral_constant<int, KSTEPS>{}, std::integral_constant<int, 4>{});
-        pin_v(vh);
-        if (__ballot(need0 || need1) != 0) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-              f32x16 x = o[t][dt];
-              asm volatile("" : "+v"(x));
-              x *= alpha[t];
-              asm volatile("" : "+v"(x));
-              o[t][dt] = x;
-            }
-        }
-        if (j + 1 < n && masked_of(j + 1)) {
-          asm volatile("" ::: "memory");
-          apply_mask(s[0], mask_of(j + 1, 0));
-          apply_mask(s[1], mask_of(j + 1, 1));
-        }
-      }
-    }
-    if (n > 0) pv2(vh, pb);  // O^T += V^T P^T of the last unit
-  };
-
-  if (!is_tree) {
-    const int P = a.prefix_len;
-    const int u_lo = slot * a.units_per_split;
-    const int n = min(a.units_per_split, a.n_pu - u_lo);
-    auto key0_of = [&](int i) { return (u_lo + i) * kUnitKeys; };
-    // Q and the first NS-QS units leave together; wait for Q only (loads
-    // complete in order), read the fragments, then free Q's stages.
-    const int pre = min(n, NS - QS);
-    issue_q();
-    for (int j = 0; j < pre; ++j) issue(j, key0_of(j));
-    wait_units<LPU, NS - QS>(pre);
-    sync_lds();
-    read_q();
-    sync_lds();
-    run_units(
-        n, pre, key0_of, [&](int i) { return P - key0_of(i) < kUnitKeys; },
-        [&](int i, int) { return (1u << (P - key0_of(i))) - 1u; });
-  }
-  if (do_tree) {
-    if (is_tree) load_q();
-    else sync_all();  // the prefix run's ring reads and loads done; Q stays in registers
-    const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-    const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);
-    const int ntok = tok_hi - tok_lo + 1;
-    const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
-    const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
-    const int32_t* ci = a.col_idx + b * a.ms_col_idx;
-    const int8_t* bt = a.blk_type + b * a.ms_blk_type;
-    const int32_t* pl = a.payload + b * a.ms_payload;
-    const int32_t* of = a.offset + b * a.ms_offset;
-    int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
-    int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
-    auto build_state = [&]() {
-      for (int i = tid; i < nqbc * ntb; i += NT) st[i] = 0;
-      if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
-      sync_lds();
-      const int e_begin = rps[0], e_end = rps[nqbc];
-      for (int e = e_begin + tid; e < e_end; e += NT) {
-        int qq = 0;
-        while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
-        const int tb = ci[e];
-        if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
-      }
-      sync_lds();
-    };
-    build_state();
-    const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
-    for (int i = tid; i < n_tu; i += NT) vis[i] = 0;
-    sync_lds();
-    for (int i = tid; i < nqbc * ntb; i += NT) {
-      if (st[i] != 0) {
-        const int tb = i % ntb;
-        const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
-        for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
-      }
-    }
-    sync_lds();
-    if (wave == 0) {
-      int nv = 0;
-      for (int base = 0; base < n_tu; base += 64) {
-        const int idx = base + lane;
-        const bool f = idx < n_tu && vis[idx] != 0;
-        const uint64_t bal = __ballot(f);
-        const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-        if (f) vis[nv + pre] = idx;
-        nv += __popcll(bal);
-      }
-      if (lane == 0) misc[0] = nv;
-    }
-    sync_lds();
-    const int n_vis = misc[0];
-    for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
-      const int nb = min(a.vt_max, n_vis - vb0);
-      if (vb0 > 0) build_state();
-      for (int it = tid; it < ntok * nb * 2; it += NT) {
-        const int q2 = it & 1, jt = it >> 1;
-        const int j = jt % nb, tt = jt / nb;
-        const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
-        const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
-        uint32_t bits = 0;
-        if (c0 < a.tree_key_limit) {
-          const int tb = c0 / BN;
-          const int e = st[(qb - qb_lo) * ntb + tb];
-          if (e < 0) {
-            bits = 0xffffu;
-          } else if (e > 0) {
-            const int flat = tl * BN + (c0 - tb * BN);
-            bits = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 0xffffu;
-          }
-          const int valid = a.tree_key_limit - c0;
-          if (valid < 16) bits &= (1u << valid) - 1u;
-        }
-        reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
-      }
-      sync_lds();
-      run_units(
-          nb, 0, [&](int i) { return P + vis[vb0 + i] * kUnitKeys; }, [&](int) { return true; },
-          [&](int i, int t) { return masks[row_tt[t] * a.vt_max + i]; });
-      sync_all();  // ring and masks free for the next batch
-    }
-  }
-
-  // Epilogue: each tile's rows normalised and staged in LDS in the input
-  // dtype, then whole rows stored (1 KB per instruction).
-  sync_all();
-  unsigned char* stg = ring;  // [ROWS][D], chunks swizzled
-  const int64_t part_row0 = ((int64_t)bk * a.n_slots + slot) * TG + row0;
-  typedef T T4 __attribute__((ext_vector_type(4)));
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float lt = pair_sum(l_run[t]);
-    const float inv = lt > 0.f ? 1.f / lt : 0.f;  // empty partial: O = 0, weight 0 in the combine
-    const int r = wave * 64 + t * 32 + ln;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      // one d-tile at a time into VGPRs (keeps the allocator from giving the
-      // accumulators a VGPR home for the whole kernel)
-      f32x16 x = o[t][dt];
-      asm volatile("" : "+v"(x));
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        T4 v4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v4[i] = (T)(x[4 * q + i] * inv);
-        *reinterpret_cast<T4*>(stg + r * ROWB + (((4 * dt + q) ^ swz_k<D>(r)) << 4) + 8 * lh) = v4;
-      }
-    }
-    if (lh == 0 && r < rows_chunk) a.ws_ml[part_row0 + r] = make_float2(m_run[t], lt);
-  }
-  sync_lds();
-  constexpr int CPR = D / 8;
-  T* dst = static_cast<T*>(a.ws_o) + part_row0 * D;
-  for (int idx = tid; idx < rows_chunk * CPR; idx += NT) {
-    const int r = idx / CPR, c = idx % CPR;
-    *reinterpret_cast<i16x8*>(dst + (int64_t)r * D + c * 8) =
-        *reinterpret_cast<const i16x8*>(stg + r * ROWB + ((c ^ swz_k<D>(r)) << 4));
-  }
-}
-
 // Merge of the n_slots partials of workspace row R of (batch, kv head) bk
 // into O (and the row's LSE when asked): kEpt outputs per thread, part
 // selects them.  16-byte loads and stores (measured 19.0 -> 12.8 us at B=16
@@ -2187,7 +1463,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
   merge_row<T, D, NB, GR>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR), (int)(threadIdx.x / TPR) % GR);
 }
 
-template <typename T, int D, int S, bool PAGED, bool C32 = false, bool PIPE = false, int FAST = 0>
+template <typename T, int D, int S, bool PAGED, bool C32 = false, int FAST = 0>
 int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   // The LDS limit attribute is set once per device (the first call on a
   // device, before any graph capture that replays it).
@@ -2196,29 +1472,13 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32, PIPE, FAST>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&split_kernel<T, D, S, PAGED, C32, FAST>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
-  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32, PIPE, FAST>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream,
+  hipLaunchKernelGGL((split_kernel<T, D, S, PAGED, C32, FAST>), dim3(p.grid), dim3(kWaves * 64), p.lds_bytes, stream,
                      args);
-  return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
-}
-
-template <typename T, int D>
-int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
-  static std::atomic<uint64_t> attr_set{0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
-  const uint64_t bit = 1ull << (dev & 63);
-  if ((attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_kernel<T, D>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
-      return TSFA_ERR_LAUNCH;
-    attr_set.fetch_or(bit, std::memory_order_acq_rel);
-  }
-  hipLaunchKernelGGL((wide_kernel<T, D>), dim3(p.grid), dim3(kWideWaves * 64), p.lds_bytes, stream, args);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -2226,29 +1486,28 @@ int launch_wide(const SplitArgs& args, const Plan& p, hipStream_t stream) {
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
 
-// Contiguous calls whose prefix units are all full (and prefix runs not
-// rotated) take the kernel with the unchecked prefix ring steps
-// (split_kernel<..., FAST>): 1 with plain K/V
+// Contiguous calls whose prefix units are all full take the kernel with the
+// unchecked prefix ring steps (split_kernel<..., FAST>): 1 with plain K/V
 // loads, 2 with non-temporal ones (instantiated for two streams, where the
 // planner asks for them); 0 keeps the checked steps.  Every prefix unit lies
 // below kv_len (prefix_len <= kv_len), and the run-base path needs a row
 // stride of at least D in both K and V.
-template <int D> inline int fast_ring(const SplitArgs& sa, const Plan& p) {
-  if (config().fast_ring == 0 || sa.prefix_len % kUnitKeys != 0 || sa.skn < D || sa.svn < D || sa.rot_step != 0)
-    return 0;
+template <int D> inline int fast_ring(const SplitArgs& sa, const Plan& p, const Config& cfg) {
+  if (cfg.fast_ring == 0 || sa.prefix_len % kUnitKeys != 0 || sa.skn < D || sa.svn < D) return 0;
   if (!sa.kv_nt) return 1;
   return p.streams == 2 ? 2 : 0;
 }
 
-// The paged forward always runs the 8-wave split kernel.
+// The kernels of one call, for the switches of one configuration snapshot
+// (cfg, read once by the caller).
 template <typename T, int D, bool PAGED>
-int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, hipStream_t stream) {
-  const bool pipe = config().pipe != 0;
+int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, const Config& cfg,
+               hipStream_t stream) {
   // contiguous: the unchecked-step flavour, +4 for the kernel that writes O
   // itself (one-slot plans, with the unchecked steps only): then its
   // "partial" goes straight to O and the combine is not launched
-  const bool fp = pipe && config().fast_ring != 0 && sa_in.prefix_len % kUnitKeys == 0;
-  const int fm0 = !pipe ? 0 : PAGED ? (fp ? 1 : 0) : fast_ring<D>(sa_in, p);
+  const bool fp = cfg.fast_ring != 0 && sa_in.prefix_len % kUnitKeys == 0;
+  const int fm0 = PAGED ? (fp ? 1 : 0) : fast_ring<D>(sa_in, p, cfg);
   const int fm = fm0 != 0 && sa_in.direct_out ? fm0 | 4 : fm0;
   SplitArgs sa = sa_in;
   if (fm & 4) sa.ws_o = ca.o;
@@ -2258,30 +1517,24 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, hip
     // path serves every refill); FAST 5 also writes O (one-slot plans)
     if constexpr (PAGED)
       st = (sa.cache32 && p.streams == 2)
-               ? (!pipe     ? launch_split<T, D, 2, true, true>(sa, p, stream)
-                  : fm == 5 ? launch_split<T, D, 2, true, true, true, 5>(sa, p, stream)
-                  : fm == 1 ? launch_split<T, D, 2, true, true, true, 1>(sa, p, stream)
-                            : launch_split<T, D, 2, true, true, true>(sa, p, stream))
-           : p.streams == 2 ? (!pipe     ? launch_split<T, D, 2, true>(sa, p, stream)
-                               : fm == 5 ? launch_split<T, D, 2, true, false, true, 5>(sa, p, stream)
-                               : fm == 1 ? launch_split<T, D, 2, true, false, true, 1>(sa, p, stream)
-                                         : launch_split<T, D, 2, true, false, true>(sa, p, stream))
-                            : (!pipe     ? launch_split<T, D, 1, true>(sa, p, stream)
-                               : fm == 5 ? launch_split<T, D, 1, true, false, true, 5>(sa, p, stream)
-                               : fm == 1 ? launch_split<T, D, 1, true, false, true, 1>(sa, p, stream)
-                                         : launch_split<T, D, 1, true, false, true>(sa, p, stream));
+               ? (fm == 5   ? launch_split<T, D, 2, true, true, 5>(sa, p, stream)
+                  : fm == 1 ? launch_split<T, D, 2, true, true, 1>(sa, p, stream)
+                            : launch_split<T, D, 2, true, true>(sa, p, stream))
+           : p.streams == 2 ? (fm == 5   ? launch_split<T, D, 2, true, false, 5>(sa, p, stream)
+                               : fm == 1 ? launch_split<T, D, 2, true, false, 1>(sa, p, stream)
+                                         : launch_split<T, D, 2, true, false>(sa, p, stream))
+                            : (fm == 5   ? launch_split<T, D, 1, true, false, 5>(sa, p, stream)
+                               : fm == 1 ? launch_split<T, D, 1, true, false, 1>(sa, p, stream)
+                                         : launch_split<T, D, 1, true, false>(sa, p, stream));
     else
-      st = p.wide             ? launch_wide<T, D>(sa, p, stream)
-           : p.streams == 2   ? (!pipe    ? launch_split<T, D, 2, false>(sa, p, stream)
-                                 : fm == 6 ? launch_split<T, D, 2, false, false, true, 6>(sa, p, stream)
-                                 : fm == 5 ? launch_split<T, D, 2, false, false, true, 5>(sa, p, stream)
-                                 : fm == 2 ? launch_split<T, D, 2, false, false, true, 2>(sa, p, stream)
-                                 : fm == 1 ? launch_split<T, D, 2, false, false, true, 1>(sa, p, stream)
-                                           : launch_split<T, D, 2, false, false, true>(sa, p, stream))
-                              : (!pipe    ? launch_split<T, D, 1, false>(sa, p, stream)
-                                 : fm == 5 ? launch_split<T, D, 1, false, false, true, 5>(sa, p, stream)
-                                 : fm == 1 ? launch_split<T, D, 1, false, false, true, 1>(sa, p, stream)
-                                           : launch_split<T, D, 1, false, false, true>(sa, p, stream));
+      st = p.streams == 2 ? (fm == 6   ? launch_split<T, D, 2, false, false, 6>(sa, p, stream)
+                             : fm == 5 ? launch_split<T, D, 2, false, false, 5>(sa, p, stream)
+                             : fm == 2 ? launch_split<T, D, 2, false, false, 2>(sa, p, stream)
+                             : fm == 1 ? launch_split<T, D, 2, false, false, 1>(sa, p, stream)
+                                       : launch_split<T, D, 2, false, false>(sa, p, stream))
+                          : (fm == 5   ? launch_split<T, D, 1, false, false, 5>(sa, p, stream)
+                             : fm == 1 ? launch_split<T, D, 1, false, false, 1>(sa, p, stream)
+                                       : launch_split<T, D, 1, false, false>(sa, p, stream));
     if (st != TSFA_OK) return st;
   }
   // no combine when the split kernel wrote O
@@ -2341,10 +1594,9 @@ namespace {
 // memoised per host thread: a call's workspace query and its launch plan the
 // same shape once.
 int device_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
-                bool paged, Plan* p) {
+                bool paged, const Config& cfg, Plan* p) {
   int cus = 0, max_lds = 0;
   if (device_cu_count(&cus) != TSFA_OK || device_max_lds_per_block(&max_lds) != TSFA_OK) return TSFA_ERR_DEVICE;
-  const Config& cfg = config();
   struct Entry {
     int key[12];
     Plan plan;
@@ -2376,9 +1628,10 @@ extern "C" size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_
                                            int prefix_len, int head_dim) {
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
   // enough for both the contiguous and the paged plan of the shape
+  const Config cfg = config();
   Plan p, pp;
-  if (device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, false, &p) != TSFA_OK ||
-      device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, true, &pp) != TSFA_OK)
+  if (device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, false, cfg, &p) != TSFA_OK ||
+      device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, true, cfg, &pp) != TSFA_OK)
     return 0;
   return std::max(p.ws_acc_bytes + p.ws_ml_bytes, pp.ws_acc_bytes + pp.ws_ml_bytes);
 }
@@ -2388,7 +1641,7 @@ extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_l
   if (out6 == nullptr || batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return TSFA_ERR_INVALID_ARGUMENT;
   Plan p;
-  const int st = device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, false, &p);
+  const int st = device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, false, config(), &p);
   if (st != TSFA_OK) return st;
   out6[0] = p.n_splits;
   out6[1] = p.units_per_split;
@@ -2439,8 +1692,10 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   for (int i = 0; i < 5; ++i)
     if (meta_seq_stride[i] < 0) return TSFA_ERR_INVALID_ARGUMENT;
 
+  // one snapshot of the TSFA_* switches for the whole call
+  const Config cfg = config();
   Plan p;
-  st = device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, kv.paged(), &p);
+  st = device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, kv.paged(), cfg, &p);
   if (st != TSFA_OK) return st;
   p.tree_key_limit = (int)std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
   if (workspace == nullptr || workspace_bytes < p.ws_acc_bytes + p.ws_ml_bytes) return TSFA_ERR_WORKSPACE;
@@ -2477,7 +1732,7 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
     sa.page_shift = shift;
     // the 32-bit-offset kernel when every byte offset it forms from a kv
     // head's base fits (TSFA_PAGED32=0 keeps the 64-bit kernel)
-    sa.cache32 = (config().paged32 != 0 && paged_offsets_fit_32(kv.n_pages, kv.cache_strides[0], kv.cache_strides[2],
+    sa.cache32 = (cfg.paged32 != 0 && paged_offsets_fit_32(kv.n_pages, kv.cache_strides[0], kv.cache_strides[2],
                                                                  kv.page_size, head_dim))
                      ? 1 : 0;
     sa.cps_b32 = (uint32_t)(kv.cache_strides[0] * 2);
@@ -2526,17 +1781,15 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   sa.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
   // Non-temporal K/V loads when little L2 reuse is at stake (TSFA_KV_NT=0/1
   // forces them off/on).
-  const int kv_nt = config().kv_nt;
+  const int kv_nt = cfg.kv_nt;
   sa.kv_nt = kv_nt >= 0 ? (kv_nt != 0) : (p.n_chunks <= 2);
   // Prefix runs first when the grid has at most 4 rounds (TSFA_ITEM_ORDER=0/1/2
   // forces natural / prefix first / tree first).
   int cus = 256;
   if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
-  const int order = config().item_order;
+  const int order = cfg.item_order;
   sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
   sa.fold_tree = p.fold_tree;
-  sa.os_first = config().os_first;
-  sa.rot_step = config().rot;
   // folded: the last run of each chunk carries the tree units, the longest
   // items, so those go first (longest first)
   if (p.fold_tree && order < 0) sa.item_order = sa.item_order ? 2 : 0;
@@ -2550,10 +1803,7 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   // skipped (the 16-sequence decode shape: its ~5 us combine of ~55 us).
   const bool o_dense = o_strides[3] == 1 && o_strides[2] == head_dim && o_strides[1] == (int64_t)q_len * head_dim &&
                        o_strides[0] == (int64_t)num_heads * q_len * head_dim;
-  sa.direct_out = p.n_slots == 1 && !p.wide && lse == nullptr && o_dense && config().direct_out != 0 &&
-                         config().pipe != 0
-                     ? 1
-                     : 0;
+  sa.direct_out = p.n_slots == 1 && lse == nullptr && o_dense && cfg.direct_out != 0 ? 1 : 0;
 
   CombineArgs ca;
   ca.o = o;
@@ -2574,11 +1824,11 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   const bool bf = dtype == TSFA_DTYPE_BF16, d128 = head_dim == 128;
   if (kv.paged()) {
-    if (bf) return d128 ? launch_all<__bf16, 128, true>(sa, ca, p, stream) : launch_all<__bf16, 64, true>(sa, ca, p, stream);
-    return d128 ? launch_all<_Float16, 128, true>(sa, ca, p, stream) : launch_all<_Float16, 64, true>(sa, ca, p, stream);
+    if (bf) return d128 ? launch_all<__bf16, 128, true>(sa, ca, p, cfg, stream) : launch_all<__bf16, 64, true>(sa, ca, p, cfg, stream);
+    return d128 ? launch_all<_Float16, 128, true>(sa, ca, p, cfg, stream) : launch_all<_Float16, 64, true>(sa, ca, p, cfg, stream);
   }
-  if (bf) return d128 ? launch_all<__bf16, 128, false>(sa, ca, p, stream) : launch_all<__bf16, 64, false>(sa, ca, p, stream);
-  return d128 ? launch_all<_Float16, 128, false>(sa, ca, p, stream) : launch_all<_Float16, 64, false>(sa, ca, p, stream);
+  if (bf) return d128 ? launch_all<__bf16, 128, false>(sa, ca, p, cfg, stream) : launch_all<__bf16, 64, false>(sa, ca, p, cfg, stream);
+  return d128 ? launch_all<_Float16, 128, false>(sa, ca, p, cfg, stream) : launch_all<_Float16, 64, false>(sa, ca, p, cfg, stream);
 }
 
 }  // namespace

@@ -34,17 +34,13 @@ int env_int(const char* name, int dflt) {
 
 Config read_config() {
   Config c;
-  c.wide = env_int("TSFA_WIDE", -1);
   c.streams = env_int("TSFA_STREAMS", 0);
   c.prefix_units = env_int("TSFA_PREFIX_UNITS_PER_SPLIT", 0);
   c.fold_tree = env_int("TSFA_FOLD_TREE", -1);
-  c.pipe = env_int("TSFA_PIPE", 1);
   c.fast_ring = env_int("TSFA_FAST_RING", 1);
   c.direct_out = env_int("TSFA_DIRECT_OUT", 1);
   c.kv_nt = env_int("TSFA_KV_NT", -1);
   c.item_order = env_int("TSFA_ITEM_ORDER", -1);
-  c.os_first = env_int("TSFA_OS_FIRST", 64);
-  c.rot = env_int("TSFA_ROT", 0);
   c.paged32 = env_int("TSFA_PAGED32", 1);
   c.meta_small = env_int("TSFA_META_SMALL", 1);
   c.bwd_concurrent = env_int("TSFA_BWD_CONCURRENT", 1);
@@ -54,18 +50,16 @@ Config read_config() {
 }
 
 std::mutex g_config_mu;
-std::atomic<bool> g_config_loaded{false};
+bool g_config_loaded = false;  // guarded by g_config_mu
 Config g_config;
 
 }  // namespace
 
-const Config& config() {
-  if (!g_config_loaded.load(std::memory_order_acquire)) {
-    std::lock_guard<std::mutex> lock(g_config_mu);
-    if (!g_config_loaded.load(std::memory_order_relaxed)) {
-      g_config = read_config();
-      g_config_loaded.store(true, std::memory_order_release);
-    }
+Config config() {
+  std::lock_guard<std::mutex> lock(g_config_mu);
+  if (!g_config_loaded) {
+    g_config = read_config();
+    g_config_loaded = true;
   }
   return g_config;
 }
@@ -75,7 +69,7 @@ void config_reload() {
   const int gen = g_config.generation + 1;
   g_config = read_config();
   g_config.generation = gen;
-  g_config_loaded.store(true, std::memory_order_release);
+  g_config_loaded = true;
 }
 
 // -------------------------------------------------------------- forward plan
@@ -87,17 +81,13 @@ namespace fwd {
 // with the tree folded in beats 5 splits of 103 on the 1024-token wide tree
 // (338 -> 306 us per call), one 1024-unit run beats 8 of 128 on the 70B
 // shape (1243 -> 1180 us), one 64-unit run beats 2 of 32 on the 16-sequence
-// decode shape (71 -> 66 us; same-box A/B).  The 8-wave kernel: two key
-// streams of 128-row chunks below 1024
-// rows per (batch, kv head), one stream of 256-row chunks from 1024 rows on
-// (TSFA_STREAMS=1/2 forces one or two).  One stream loads each K/V unit once
-// for 256 rows, halving the loads per MFMA and leaving six units in flight
-// instead of two per stream: the 1024-token wide tree 391 -> 377 us, the 70B
-// shape 1463 (wide kernel) -> 1355 us per call.  Two streams fill the grid
-// where rows are few (the 8B decode shape: 22.9 -> 19.3 us; 16 sequences:
-// 75.1 -> 70.3 us).  TSFA_WIDE=2 selects the wide kernel (256-row chunks, one
-// wave per SIMD), TSFA_WIDE=1 selects it above 128 rows per (batch, kv head);
-// paged calls run the wide plan on the 8-wave kernel.
+// decode shape (71 -> 66 us; same-box A/B).  Key streams: two, with
+// 128-row chunks, below 1024 rows per (batch, kv head); one, with 256-row
+// chunks, from 1024 rows on (TSFA_STREAMS=1/2 forces one or two).  One stream
+// loads each K/V unit once for 256 rows, halving the loads per MFMA and
+// leaving six units in flight instead of two per stream (the 1024-token wide
+// tree 391 -> 377 us per call); two streams fill the grid where rows are few
+// (the 8B decode shape: 22.9 -> 19.3 us; 16 sequences: 75.1 -> 70.3 us).
 int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len, int head_dim,
               bool paged, int cus, int max_lds, const Config& cfg, Plan* p) {
   (void)paged;
@@ -107,8 +97,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   const int G = num_heads / num_kv_heads;
   const int64_t TG = (int64_t)q_len * G;
   if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
-  p->wide = cfg.wide == 2 || (cfg.wide == 1 && TG > kMaxRows / 2);
-  p->streams = p->wide || cfg.streams == 1 || (cfg.streams != 2 && TG >= 1024) ? 1 : 2;
+  p->streams = cfg.streams == 1 || (cfg.streams != 2 && TG >= 1024) ? 1 : 2;
   p->rows_per_chunk = kMaxRows / p->streams;
   p->n_chunks = (int)((TG + p->rows_per_chunk - 1) / p->rows_per_chunk);
   p->n_pu = ceil_div(prefix_len, kUnitKeys);
@@ -125,7 +114,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
       // full rounds, the last partial round of runs and the (shorter) tree
       // items share the CUs.  A tree item runs only its visible units,
       // estimated as 60 % of the tree's.
-      const double t_step = (p->wide ? 1.4 : 1.15) * head_dim / 128.0, t_fixed = 5.0;
+      const double t_step = 1.15 * head_dim / 128.0, t_fixed = 5.0;
       const double part_bytes = (double)batch * num_heads * q_len * (2.0 * head_dim + 8.0);
       const int64_t tree_units = ceil_div(std::max(0, kv_len - prefix_len), kUnitKeys);
       const double c_tree =
@@ -318,12 +307,15 @@ int make_bwd_plan(int batch, int num_kv_heads, int q_len, int kv_len, int prefix
   p->nqbc_max = std::min(ceil_div(q_len, block_m), toks / block_m + 2);
   if ((int64_t)p->nqbc_max * n_tree_blocks > kMaxStateInts || p->nqbc_max + 1 > 72) return TSFA_ERR_UNSUPPORTED;
   const int64_t rows = (int64_t)batch * num_kv_heads;
+  // the grid (rows x key blocks) and the workspace sizes stay far from
+  // int64 overflow: every product below is checked by division first
+  const int64_t kblocks = (int64_t)p->n_pb + p->n_tb;
+  if (kblocks > 0 && rows > ((int64_t)INT32_MAX / 2) / kblocks) return TSFA_ERR_UNSUPPORTED;
+  if (rows > ((int64_t)1 << 40) / ((int64_t)p->n_tiles * kTileRows * head_dim * 4)) return TSFA_ERR_UNSUPPORTED;
+  if ((int64_t)n_trees * p->n_tiles * p->n_tkeys > ((int64_t)1 << 28)) return TSFA_ERR_UNSUPPORTED;
   p->rowstat_bytes = align256((size_t)rows * p->n_tiles * kTileRows * 8);
   p->dq_bytes = align256((size_t)rows * p->n_tiles * kTileRows * head_dim * 4);
   p->vis_bytes = align256((size_t)n_trees * p->n_tiles * p->n_tkeys * 4 + 16);
-  const int64_t items = rows * (p->n_pb + p->n_tb);
-  if (items > (int64_t)INT32_MAX / 2 || (int64_t)n_trees * p->n_tiles * p->n_tkeys > ((int64_t)1 << 28))
-    return TSFA_ERR_UNSUPPORTED;
   return TSFA_OK;
 }
 

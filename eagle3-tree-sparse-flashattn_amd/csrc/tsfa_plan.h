@@ -38,26 +38,27 @@ TSFA_HD inline uint32_t fdiv(uint32_t n, const FastDiv& f) {
 TSFA_HD inline uint32_t frem(uint32_t n, const FastDiv& f) { return n - fdiv(n, f) * f.d; }
 
 // The TSFA_* environment switches, read once at first use (tsfa_config_reload
-// reads them again).  -1 / 0 mean "the planner decides" where noted.
+// reads them again).  -1 / 0 mean "the planner decides" where noted.  Apart
+// from TSFA_BENCH_HOOKS they select among kernels and plans the planner picks
+// for other shapes anyway, so tests can run each one on any shape.
 struct Config {
-  int wide;            // TSFA_WIDE: 2 wide kernel, 1 above 128 rows, else never (-1)
   int streams;         // TSFA_STREAMS: 1 or 2 key streams, 0 planner
   int prefix_units;    // TSFA_PREFIX_UNITS_PER_SPLIT: > 0 forces the run length
   int fold_tree;       // TSFA_FOLD_TREE: 0/1 forces, -1 planner
-  int pipe;            // TSFA_PIPE: 0 the unpipelined unit loop
   int fast_ring;       // TSFA_FAST_RING: 0 keeps the checked ring steps for full prefix runs
   int direct_out;      // TSFA_DIRECT_OUT: 0 keeps the combine for one-slot plans
   int kv_nt;           // TSFA_KV_NT: 0/1 forces non-temporal K/V loads, -1 planner
   int item_order;      // TSFA_ITEM_ORDER: 0/1/2 forces, -1 planner
-  int os_first;        // TSFA_OS_FIRST: one-shot run units requested with Q
-  int rot;             // TSFA_ROT: prefix-run rotation step per row chunk
   int paged32;         // TSFA_PAGED32: 0 keeps the 64-bit-offset paged kernel
   int meta_small;      // TSFA_META_SMALL: 0 always two metadata launches
   int bwd_concurrent;  // TSFA_BWD_CONCURRENT: 0 keeps the backward on one stream
   int bench_hooks;     // TSFA_BENCH_HOOKS: 1 unlocks tsfa_fwd_set_kernel_mask
   int generation;      // bumped by every reload (keys of memoised plans)
 };
-const Config& config();
+// A copy of the switches, taken under the lock that config_reload holds, so
+// a call that snapshots them once sees one consistent set even while another
+// thread reloads them.
+Config config();
 void config_reload();
 
 namespace fwd {
@@ -79,7 +80,7 @@ inline int64_t chunk_qblocks(int rows, int group, int block_m) {
 }
 
 struct Plan {
-  int wide, streams, rows_per_chunk;
+  int streams, rows_per_chunk;
   int n_chunks, n_pu, units_per_split, n_splits, n_slots, n_items, items_per_xcd, grid, ring_stages, fold_tree;
   int vt_max, tree_key_limit;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;

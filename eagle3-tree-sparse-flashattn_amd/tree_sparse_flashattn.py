@@ -209,7 +209,10 @@ def _masks_u8(tree_masks: torch.Tensor) -> torch.Tensor:
     m = tree_masks
     if m.dtype != torch.bool:
         m = m != 0  # nonzero -> visible, NaN included (tree_sparse_flashattn.py:90)
-    if m.stride(-1) != 1:
+    # the host builder reads rows at least q_len apart (an expanded mask with
+    # row stride 0 is made dense first, as the reference's .contiguous()
+    # does); the device builder reads any row stride
+    if m.stride(-1) != 1 or (m.device.type == "cpu" and m.stride(-2) < m.shape[-1]):
         m = m.contiguous()
     return m.view(torch.uint8)
 

@@ -38,6 +38,7 @@ EXPORTS = (
     "tsfa_config_reload",
     "tsfa_fwd_plan_for_device",
     "tsfa_fwd_workspace_bytes_for_device",
+    "tsfa_device_limits",
     "tsfa_fwd_check_args",
     "tsfa_fwd_workspace_bytes",
     "tsfa_fwd",
@@ -66,6 +67,7 @@ _SIGNATURES = {
     "tsfa_config_reload": (_c_int, []),
     "tsfa_fwd_plan_for_device": (_c_int, [_c_int] * 10 + [ctypes.POINTER(ctypes.c_int32)]),
     "tsfa_fwd_workspace_bytes_for_device": (_c_size, [_c_int] * 9),
+    "tsfa_device_limits": (_c_int, [ctypes.POINTER(ctypes.c_int32)]),
     "tsfa_fwd_check_args": (_c_int, [_c_int] * 13),
     "tsfa_fwd_workspace_bytes": (_c_size, [_c_int] * 7),
     "tsfa_fwd": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -163,4 +165,13 @@ def fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim
     check("tsfa_fwd_plan", load().tsfa_fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
                                                  head_dim, out))
     keys = ("prefix_splits", "units_per_split", "rows_per_chunk", "row_chunks", "workgroups", "ring_stages")
-    return dict(zip(keys, list(out)))
+    plan = dict(zip(keys, list(out)))
+    # the partial slots per row chunk and the folded tree, planned for this device
+    lim = (ctypes.c_int32 * 2)()
+    check("tsfa_device_limits", load().tsfa_device_limits(lim))
+    out8 = (ctypes.c_int32 * 8)()
+    check("tsfa_fwd_plan_for_device", load().tsfa_fwd_plan_for_device(
+        lim[0], lim[1], batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, 0, out8))
+    plan["slots"] = int(out8[6])
+    plan["fold_tree"] = int(out8[7])
+    return plan

@@ -249,6 +249,12 @@ int tsfa_fwd_plan_for_device(int cus, int max_lds, int batch, int num_heads, int
 size_t tsfa_fwd_workspace_bytes_for_device(int cus, int max_lds, int batch, int num_heads, int num_kv_heads,
                                            int q_len, int kv_len, int prefix_len, int head_dim);
 
+/* The current device's compute-unit count and LDS bytes per workgroup, as
+ * the planner reads them: out2[0] = CUs, out2[1] = max LDS per block (the
+ * arguments tsfa_fwd_plan_for_device takes to plan this device).  No
+ * counterpart in the reference. */
+int tsfa_device_limits(int32_t* out2);
+
 /* Re-read the TSFA_* environment switches (read once, at their first use).
  * Not to be called while a forward or backward of this library runs. */
 int tsfa_config_reload(void);

@@ -41,12 +41,17 @@ def _full_mask(tree_mask: torch.Tensor, batch: int, q_len: int, kv_len: int, pre
     return full.unsqueeze(1)
 
 
-def dense_mask_attention(q, k, v, tree_mask, prefix_len: int, *, head_chunk: int | None = None) -> torch.Tensor:
+def dense_mask_attention(q, k, v, tree_mask, prefix_len: int, *, head_chunk: int | None = None,
+                         p_dtype: torch.dtype | None = None) -> torch.Tensor:
     """fp32 CPU restatement of benchmark.py:8-35.  Returns [B, Hq, T, D] float32.
 
     ``head_chunk`` bounds memory by processing that many query heads at a time
     (the scores tensor is [B, chunk, T, KV] fp32); the result does not depend
-    on it.
+    on it.  ``p_dtype`` (default None: plain fp32 softmax) restates the
+    reference kernel's own rounding instead: the probabilities
+    exp(s - rowmax) are rounded to that dtype before the product with V while
+    the row sum takes them unrounded (tree_sparse_flashattn.py:273-278,
+    :321-326: ``l_i += tl.sum(p)`` in fp32, ``tl.dot(p.to(v.dtype), v)``).
     """
     q = q.detach().to("cpu", torch.float32)
     k = k.detach().to("cpu", torch.float32)
@@ -65,7 +70,11 @@ def dense_mask_attention(q, k, v, tree_mask, prefix_len: int, *, head_chunk: int
         ve = v[:, kv_idx]
         scores = torch.matmul(q[:, h0:h1], ke.transpose(-2, -1)) * scale
         scores = scores.masked_fill(~mask, float("-inf"))
-        out[:, h0:h1] = torch.matmul(torch.softmax(scores, dim=-1), ve)
+        if p_dtype is None:
+            out[:, h0:h1] = torch.matmul(torch.softmax(scores, dim=-1), ve)
+        else:
+            p = torch.exp(scores - scores.amax(dim=-1, keepdim=True))  # NaN rows stay NaN (no visible key)
+            out[:, h0:h1] = torch.matmul(p.to(p_dtype).float(), ve) / p.sum(dim=-1, keepdim=True)
     return out
 
 

@@ -11,15 +11,39 @@ from oracle.attn_oracle import dense_mask_attention
 # max_abs_err bars against the fp32 oracle (the named workloads use these alone).
 TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3}
 # Edge cases with few visible keys have |O| up to ~4, where rounding O once to
-# the output dtype already costs up to 2^-9*|O| (bf16) -- 7.8e-3 at |O| = 4,
-# and the reference's own numerics (P rounded to the input dtype before PV,
-# tree_sparse_flashattn.py:278) add about as much again.  Those tests allow
-# TOL + REL * |ref|.  Measured over the 83 such cases of the GPU suite: bf16
-# max_abs_err 1.37e-2 in 13 of 48 cases above the absolute bar, needing at
-# most 2.81e-3*|ref| beyond it (REL = 2^-8 = 3.91e-3, 2 ulp); fp16 max_abs_err
-# 1.18e-3, never above its absolute bar (REL = 0).  Every relaxed comparison
-# prints its max_abs_err and the relative share it needed.
-REL = {torch.bfloat16: 2.0 ** -8, torch.float16: 0.0}
+# the output dtype already costs up to half an ulp of O: 2^-7 = 7.8e-3 at |O|
+# in [2, 4) for bf16, so no bf16-output kernel can meet 8e-3 absolute there
+# once the reference's own rounding (P to the input dtype before P.V,
+# tree_sparse_flashattn.py:278) adds its share.  Those tests allow the
+# storage roundings of the call beyond the bar: |got - ref| <= TOL + n *
+# ulp(got) / 2, ulp in the output dtype (MANT significand bits), n = 1 when
+# the split kernel writes O (a one-slot plan) and n = 2 when the combine
+# merges split-KV partials stored in the input dtype (one rounding of the
+# partial, one of O; the reference has no partials).  Measured on the GPU
+# suite's worst case (P = 1, G = 4, bf16, |O| up to 3.9): the reference's own
+# P rounding moves O by up to 4.4e-3 from the fp32 oracle; the kernel is
+# 1.34e-2 off with one slot (0.69 half-ulps beyond TOL) and 1.37e-2 with two
+# (0.72 to 1.05).  Every such comparison prints its max_abs_err and how many
+# half-ulps of |got| it used beyond TOL.
+MANT = {torch.bfloat16: 8, torch.float16: 11}
+
+
+def storage_roundings(q, k, prefix_len) -> int:
+    """Roundings of O to its dtype in one forward call of this shape: 1 when
+    the plan has one slot (the split kernel writes O), else 2 (partial, then
+    O).  The plan is read under the current TSFA_* switches."""
+    from tsfa import _lib
+
+    b, hq, t, d = q.shape
+    width = 64 if d <= 64 else 128  # narrower head dims run zero-padded
+    plan = _lib.fwd_plan(b, hq, k.shape[1], t, k.shape[2], prefix_len, width)
+    return 1 if plan["slots"] == 1 else 2
+
+
+def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:
+    """Half an ulp of each element of x (values of `dtype` held as fp32), in `dtype`."""
+    _, e = torch.frexp(x.nan_to_num(0.0))  # x = m * 2^e, 0.5 <= |m| < 1
+    return torch.where(x == 0, torch.zeros_like(x), torch.ldexp(torch.ones_like(x), e - MANT[dtype] - 1))
 
 
 def assert_meta_equal(meta, ref: mo.OracleMetadata):
@@ -47,8 +71,9 @@ def oracle_out(q, k, v, mask, prefix_len, heads=None, head_chunk=8):
     return torch.cat(outs, dim=1)
 
 
-def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None, relative=False):
-    """max |out - ref| <= TOL[dtype] (+ REL[dtype]*|ref| when `relative`); NaN where ref is NaN."""
+def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None, half_ulps=0):
+    """max |out - ref| <= TOL[dtype] (+ half_ulps halves of an ulp of out in
+    `dtype`: the storage roundings of the call); NaN exactly where ref is NaN."""
     got = out.float().cpu()
     if heads is not None:
         got = got[:, list(heads)]
@@ -58,16 +83,17 @@ def assert_close_to_oracle(out, ref, dtype, heads=None, atol=None, relative=Fals
     diff = (got - ref).abs()
     diff[nan_ref] = 0
     err = float(diff.max()) if diff.numel() else 0.0
-    if relative:
-        mag = ref.abs().nan_to_num(0.0)
-        bound = tol + REL[dtype] * mag
-        excess = float((diff - bound).max()) if diff.numel() else 0.0
-        # the relative share the worst element needed beyond the absolute bar
-        over = (diff - tol).clamp(min=0) / mag.clamp(min=1e-30)
-        need = float(over.max()) if diff.numel() else 0.0
-        print(f"[err] relative bar: max_abs_err {err:.3e} (absolute bar {tol:.0e}); relative part needed "
-              f"{need:.2e} of |ref|, allowed {REL[dtype]:.2e}", flush=True)
-        assert excess <= 0, f"max_abs_err {err:.3e} exceeds {tol:.1e} + {REL[dtype]:.1e}*|ref|"
+    if half_ulps > 0:
+        hu = half_ulp(got, dtype)
+        excess = float((diff - tol - half_ulps * hu).max()) if diff.numel() else 0.0
+        # the storage roundings the worst element used beyond the absolute bar
+        used = ((diff - tol).clamp(min=0) / hu.clamp(min=1e-30))
+        need = float(used.max()) if diff.numel() else 0.0
+        print(f"[err] max_abs_err {err:.3e} (absolute bar {tol:.0e}); beyond it {need:.2f} half-ulp of |got| "
+              f"(allowed {half_ulps})", flush=True)
+        assert excess <= 0, (f"max_abs_err {err:.3e} exceeds {tol:.1e} + {half_ulps} * ulp(got)/2 "
+                             f"(used {need:.2f} half-ulps)")
     else:
+        print(f"[err] max_abs_err {err:.3e} (bar {tol:.0e})", flush=True)
         assert err <= tol, f"max_abs_err {err:.3e} > {tol:.1e}"
     return err

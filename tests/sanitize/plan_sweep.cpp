@@ -74,7 +74,6 @@ static void sweep_fwd_plan() {
     const int D = uni(0, 1) ? 64 : 128;
     const int cus = cus_list[uni(0, 4)];
     const int max_lds = uni(0, 3) ? 163840 : 65536;
-    cfg.wide = (int)uni(-1, 2);
     cfg.streams = (int)uni(0, 2);
     cfg.prefix_units = uni(0, 5) ? 0 : (int)uni(-3, 300);
     cfg.fold_tree = (int)uni(-1, 1);
@@ -111,7 +110,7 @@ static void sweep_fwd_plan() {
   }
   // invalid shapes come back as errors, never as plans
   fwd::Plan p;
-  const Config& c0 = config();
+  const Config c0 = config();
   EXPECT(fwd::make_plan(0, 4, 2, 8, 8, 0, 128, false, 256, 163840, c0, &p) != TSFA_OK, "batch 0");
   EXPECT(fwd::make_plan(1, 5, 2, 8, 8, 0, 128, false, 256, 163840, c0, &p) != TSFA_OK, "heads not a multiple of kv heads");
   EXPECT(fwd::make_plan(1, 4, 2, 8, 4, 8, 128, false, 256, 163840, c0, &p) != TSFA_OK, "kv < prefix");

@@ -93,3 +93,27 @@ def test_host_builder_rejects_like_the_reference():
         tsf.prepare_tree_sparse_metadata(torch.ones(4, 4), 0, 0, 16)
     with pytest.raises(ValueError):
         tsf.prepare_tree_sparse_metadata(torch.ones(4, 5), 0, 16, 16)
+
+
+@pytest.mark.parametrize("view", ["row_stride_0", "transposed", "batched_expand"])
+def test_host_builder_takes_overlapping_and_strided_masks(view):
+    # views whose rows overlap or are not contiguous: the reference makes
+    # them dense (.contiguous()); the host builder sees the dense copy
+    rng = np.random.default_rng(5)
+    if view == "row_stride_0":
+        row = torch.from_numpy(rng.random(24) < 0.5)
+        m = row.unsqueeze(0).expand(24, 24)
+        assert m.stride(-2) == 0
+    elif view == "transposed":
+        m = torch.from_numpy(trees.ancestor_mask(trees.random_parents(40, rng))).t()
+    else:
+        one = torch.from_numpy(trees.ancestor_mask(trees.random_parents(32, rng)))
+        m = one.unsqueeze(0).expand(3, 32, 32)
+    dense = m.contiguous().numpy()
+    if m.ndim == 2:
+        meta = tsf.prepare_tree_sparse_metadata(m, 7, 16, 16)
+        assert_meta_equal(meta, mo.build_metadata(dense, 7, 16, 16))
+    else:
+        bm = tsf.prepare_tree_sparse_metadata_batched(m, 7, 16, 16)
+        for b in range(m.shape[0]):
+            assert_meta_equal(bm.sequence(b), mo.build_metadata(dense[b], 7, 16, 16))

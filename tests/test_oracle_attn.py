@@ -98,3 +98,37 @@ def test_scale_is_inverse_sqrt_head_dim():
     s = (q[0, 0] @ k[0, 0].T) / math.sqrt(16)
     ref = torch.softmax(s, -1) @ v[0, 0]
     torch.testing.assert_close(out[0, 0], ref, atol=1e-6, rtol=1e-6)
+
+
+@pytest.mark.parametrize("p_dtype", [torch.bfloat16, torch.float16])
+def test_reference_p_rounding_matches_a_per_row_loop(p_dtype):
+    # the reference's own numerics (p rounded to the input dtype before P.V,
+    # the row sum from unrounded p; tree_sparse_flashattn.py:273-278): against
+    # a float64 loop that gathers each row's visible keys and rounds each p
+    # explicitly, and within 2^-(mantissa+1) * sum(p|v|) / l of the plain oracle
+    b, hq, hkv, t, p, d = 2, 4, 2, 11, 6, 8
+    q, k, v = _inputs(b, hq, hkv, t, p, d, seed=3)
+    q = q * 3  # wide score spread: most p far from 1
+    rng = np.random.default_rng(4)
+    masks = torch.from_numpy(np.stack([trees.ancestor_mask(trees.random_parents(t, rng)) for _ in range(b)]))
+    out = dense_mask_attention(q, k, v, masks, p, p_dtype=p_dtype)
+    plain = dense_mask_attention(q, k, v, masks, p)
+    np.testing.assert_allclose(dense_mask_attention(q, k, v, masks, p, p_dtype=torch.float32).numpy(),
+                               plain.numpy(), atol=1e-6, rtol=1e-6)
+    ref = np.empty(out.shape)
+    bound = np.empty(out.shape)
+    mant = 8 if p_dtype == torch.bfloat16 else 11
+    for bi in range(b):
+        for h in range(hq):
+            kv = h // (hq // hkv)
+            for r in range(t):
+                keys = list(range(p)) + [p + j for j in range(t) if masks[bi, r, j]]
+                s = np.array([float(q[bi, h, r].double() @ k[bi, kv, j].double()) for j in keys]) / math.sqrt(d)
+                pe = np.exp(s - s.max())
+                pr = torch.from_numpy(pe).float().to(p_dtype).double().numpy()
+                vv = v[bi, kv, keys].double().numpy()
+                ref[bi, h, r] = pr @ vv / pe.sum()
+                bound[bi, h, r] = 2.0 ** -mant * (pe @ np.abs(vv)) / pe.sum()
+    np.testing.assert_allclose(out.numpy(), ref, atol=2e-6, rtol=1e-5)
+    assert np.all(np.abs(out.numpy() - plain.numpy()) <= bound + 2e-6)
+    assert np.abs(out.numpy() - plain.numpy()).max() > 0  # the rounding is visible

@@ -1,7 +1,8 @@
 """tsfa_fwd_noalloc -- the forward without a workspace argument, its split-KV
 partials in the library's per-GPU device array -- against tsfa_fwd with a
 caller workspace, called through the C-ABI: identical O on two calls in a
-row, the second on a smaller input, and the size refusal."""
+row, the second on a smaller input; the same under HIP graph capture on a
+non-default stream (the use the entry point is for); and the size refusal."""
 
 import pytest
 import torch
@@ -80,3 +81,34 @@ def test_noalloc_refuses_calls_past_its_array():
                               w.prefix_len, nqb, ntb, w.q_heads // w.kv_heads, w.block_m, w.block_n, w.head_dim,
                               _lib.dtype_code(w.dtype), None)
     assert st == _lib.TSFA_ERR_WORKSPACE
+
+
+def test_noalloc_captured_in_a_graph_on_a_side_stream():
+    # tsfa_fwd_noalloc captured into a HIP graph on a non-default stream and
+    # replayed three times, with eager work between the replays (the array
+    # keeps the last call's contents): every replay equals tsfa_fwd's O
+    q, k, v, meta = _inputs("llama3-8b-eagle64-p4096")
+    ref = tsf.tree_sparse_attention_fwd(q, k, v, meta)
+    out = torch.full_like(q, float("nan"))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _lib.check("tsfa_fwd_noalloc", _noalloc(q, k, v, meta, out))  # takes the array's address
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            _lib.check("tsfa_fwd_noalloc", _noalloc(q, k, v, meta, out))
+    torch.cuda.synchronize()
+    small = _inputs(small=True)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"[noalloc] graph replay {rep}", flush=True)
+        assert torch.equal(out.isnan(), ref.isnan())
+        assert torch.equal(out.nan_to_num(0.0), ref.nan_to_num(0.0)), f"replay {rep} differs from tsfa_fwd"
+        # an eager call on another shape between replays overwrites the array
+        tmp = torch.empty_like(small[0])
+        _lib.check("tsfa_fwd_noalloc", _noalloc(*small, tmp))
+        torch.cuda.synchronize()
