@@ -58,7 +58,6 @@ namespace fwd {
 // kWaves, kMaxRows, kUnitKeys, kRingBytes, kMaskWords, kMaxTreeUnits and
 // kMiscInts come from tsfa_plan.h (the planner sizes the grid and LDS by them)
 constexpr float kRescaleLog2 = 8.0f;
-constexpr int kOneShotSync = 2;  // steps between the barriers of a one-shot prefix run
 
 // Per-workgroup timestamps for timeline measurements: compiled in only with
 // -DTSFA_STAMPS (a separate measurement build); TSFA_STAMP is empty otherwise.
@@ -539,22 +538,9 @@ void split_kernel(const SplitArgs a) {
   unsigned char* sring = ring + ks * RB;
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
   const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
-  // One-shot prefix runs (contiguous K/V, two streams): unit i
-  // of a run of at most NOS units sits in stage i of the ring followed by the
-  // mask area (a prefix run does not use it), Q in the last two stages; every
-  // unit is requested up front (the two behind Q once Q is read) and the loop
-  // only waits.  Latency under load is ~2.5 us, so a ring that requests a
-  // unit two steps ahead stalls every step on short runs.
-  constexpr int NOS = (kRingBytes + kMaskWords * 4) / SB;
   constexpr bool RING2 = NS >= 8;  // ring loop meets every other step
-  static_assert(S == 1 || QS == 1, "one-shot Q staging: one stage per stream");
-  static_assert(NOS <= 32 && (NOS - S) * LPU < 64, "one-shot geometry");
-  // LDS address of the stage of the stream's unit j: ring stage j % NS, or
-  // stage ks + S*j of the one-shot layout
-  bool oneshot = false;
-  uint32_t st_base = sring_lds, st_step = SB;
-  int st_mask = NS - 1;
-  auto stage = [&](int j) { return st_base + (uint32_t)((j & st_mask) * st_step); };
+  // LDS address of the ring stage of the stream's unit j
+  auto stage = [&](int j) { return sring_lds + (uint32_t)((j & (NS - 1)) * SB); };
   TSFA_CYC_DECL
 
   // The stream's RG waves move equal shares of each unit: the first half of
@@ -658,9 +644,9 @@ void split_kernel(const SplitArgs a) {
   // prologue need not wait for Q before filling the ring.  Rows past the end
   // repeat the last row (their outputs are never stored).
   // Q stage of the stream holding chunk rows [s*QROWS, (s+1)*QROWS): the last
-  // QS stages of its ring, or stage NOS - S + s in one-shot runs.
-  auto q_stage = [&](int s, bool os) { return os ? ring + (NOS - S + s) * SB : ring + s * RB + (NS - QS) * SB; };
-  auto issue_q = [&](bool os) {
+  // QS stages of its ring.
+  auto q_stage = [&](int s) { return ring + s * RB + (NS - QS) * SB; };
+  auto issue_q = [&]() {
     constexpr int RPL = 1024 / ROWB, CPR = D / 8;
     constexpr int QL = ROWS / RPL / kWaves;  // 1 KB loads per wave
 #pragma unroll
@@ -672,11 +658,11 @@ void split_kernel(const SplitArgs a) {
       const int g = R - t * G;
       const T* src = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm +
                      ((pos ^ swz_k<D>(tr)) << 3);
-      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(q_stage(l0 / QROWS, os) + (l0 % QROWS) * ROWB)));
+      dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(q_stage(l0 / QROWS) + (l0 % QROWS) * ROWB)));
     }
   };
-  auto read_q = [&](bool os) {
-    const unsigned char* qs = q_stage(rg * 32 / QROWS, os) + ((rg * 32) % QROWS) * ROWB;
+  auto read_q = [&]() {
+    const unsigned char* qs = q_stage(rg * 32 / QROWS) + ((rg * 32) % QROWS) * ROWB;
 #pragma unroll
     for (int kk = 0; kk < KSTEPS; ++kk)
       qf[kk] = *reinterpret_cast<const i16x8*>(qs + ln * ROWB + (((2 * kk + lh) ^ swz_k<D>(ln)) << 4)) ^ qsgn;
@@ -880,13 +866,7 @@ void split_kernel(const SplitArgs a) {
   auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
-    if (oneshot) {
-      // units [0, pre) requested with Q; the rest go into Q's stages once
-      // every wave has read Q (the barrier below)
-      if (mine > 0) wait_units<LPU, NOS - S>(pre - 1);  // unit 0 landed
-      sync_lds();
-      for (int j = pre; j < mine; ++j) issue_of(stage(j), ks + S * j);
-    } else {
+    {
       // RING2: NS-2 units ahead, two issued at every other step
       constexpr int AHEAD = RING2 ? NS - 2 : NS - 1;
       for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(sring_lds + j * SB, ks + S * j);
@@ -903,19 +883,12 @@ void split_kernel(const SplitArgs a) {
       s_cur = qk(kf);
     }
     // Ring: unit j+1 landed for every wave of the stream; ring stage
-    // (j-1)%NS is free.  One-shot: no stage is reused, so the waves meet
-    // every kOneShotSync steps only, each time for the units of those steps
-    // (units up to j + kOneShotSync landed); fewer barriers let the two
-    // waves of a SIMD drift apart.
+    // (j-1)%NS is free.
     // RING2 (rings of at least 8 stages): the same with the waves meeting
     // every other step, units up to j+2 landed and stages (j-2)%NS and
     // (j-1)%NS refilled at even steps j.
     auto ring_step = [&](int j) {
-      if (oneshot) {
-        if (j % kOneShotSync != 0) return;
-        const int last = min(j + kOneShotSync, mine - 1);
-        if (j + 1 < mine) wait_units<LPU, NOS - S>(mine - 1 - last);
-      } else if constexpr (RING2) {
+      if constexpr (RING2) {
         if (j & 1) return;
         if constexpr (decltype(fast_c)::value) {
           // steady state (both refill units exist): fixed wait, unchecked
@@ -959,13 +932,11 @@ void split_kernel(const SplitArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       if (j < 40) TSFA_STAMP(3 + j);
       TSFA_CYC(2);
-      if (!oneshot) {
-        if constexpr (RING2) {
-          if (j + NS - 2 < mine) issue_of(sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
-          if (j + NS - 1 < mine) issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
-        } else if (j + NS - 1 < mine) {
-          issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
-        }
+      if constexpr (RING2) {
+        if (j + NS - 2 < mine) issue_of(sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
+        if (j + NS - 1 < mine) issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+      } else if (j + NS - 1 < mine) {
+        issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
       }
       if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
       __builtin_amdgcn_sched_barrier(0);
@@ -979,7 +950,7 @@ void split_kernel(const SplitArgs a) {
       // the scheduling fences keep the two iterations' registers apart (the
       // 2x unrolled body spills without them).  1024-token wide tree -2 %,
       // 70B shape -3 to -6 % (same-call A/B).
-      if (!oneshot && active) {
+      if (active) {
         for (; j0 + NS - 1 < mine; j0 += 2) {
           vm_wait<(NS - 5) * LPU>();
           __builtin_amdgcn_sched_barrier(0);
@@ -1000,7 +971,7 @@ void split_kernel(const SplitArgs a) {
       }
     } else if constexpr (decltype(fast_c)::value) {
       // the same for rings that meet and refill at every step
-      if (!oneshot && active) {
+      if (active) {
         for (; j0 + NS < mine; j0 += 2) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -1044,21 +1015,16 @@ void split_kernel(const SplitArgs a) {
     // run plus one product (the general path rebuilds it from the key with
     // 64-bit scalar arithmetic and range checks, on the scalar unit the
     // workgroup's waves share); units reaching past kv_len take that path.
-    // (Set up for ring runs only: a one-shot run issues its few units in the
-    // prologue, where the setup would delay Q.)
-    int64_t unit_bytes = 0;
-    const char* run_rows = nullptr;
-    int n_fast = 0;
-    uint32_t m0_off = 0;
+    const int64_t unit_bytes = (int64_t)kUnitKeys * dstride * (int64_t)sizeof(T);
+    const char* run_rows =
+        reinterpret_cast<const char*>(dbase + ((int64_t)u_lo * kUnitKeys + dma_u0 * DRPL) * dstride);
+    const int n_fast = rows_fast ? max(0, min(n, a.kv_len / kUnitKeys - u_lo)) : 0;
+    const uint32_t m0_off = dlds + (uint32_t)dma_u0 * 1024u;
     auto issue_prefix = [&](uint32_t sb, int i) {
-      const int ri = i;
       if constexpr (FM != 0 && !PAGED) {
-        // one-shot runs (two streams only) issue by the general path: their
-        // run base is not set up, to keep Q's request first
-        if (!(S == 2 && oneshot)) dma_rows<LPU, FM == 2>(run_rows + (int64_t)ri * unit_bytes, doff, sb + m0_off);
-        else issue_at(sb, key0_of(i));
-      } else if (!PAGED && !oneshot && ri < n_fast) {
-        const char* rowp = run_rows + ri * unit_bytes;
+        dma_rows<LPU, FM == 2>(run_rows + (int64_t)i * unit_bytes, doff, sb + m0_off);
+      } else if (!PAGED && i < n_fast) {
+        const char* rowp = run_rows + i * unit_bytes;
         if (kv_nt) dma_rows<LPU, true>(rowp, doff, sb + m0_off);
         else dma_rows<LPU, false>(rowp, doff, sb + m0_off);
       } else {
@@ -1068,39 +1034,22 @@ void split_kernel(const SplitArgs a) {
     // Q and the first NS-QS units of each stream leave together; wait for Q
     // only (loads complete in order), then every wave reads its fragments.
     // With QS > 1 the ring prologue reuses Q stages: one more barrier first.
+    // A run requests at most NS - 1 units of its stream ahead: requesting a
+    // short run's units all at once (every run of the Llama-3-8B decode
+    // shape fits in LDS) lets Q and the first units queue behind the rest in
+    // HBM (Q landed 3.6 against 2.8 us after the workgroups start; 16.0
+    // against 15.4-15.6 us per call, same-box A/B).
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
-    int pre;
-    if (!PAGED && S == 2 && n <= NOS) {
-      // one-shot: Q in the last S stages, run units below NOS - S with it
-      oneshot = true;
-      st_base = ring_lds + ks * SB;
-      st_step = S * SB;
-      st_mask = 31;
-      const int early = min(n, NOS - S);
-      pre = early > ks ? (early - ks + S - 1) / S : 0;
-      TSFA_STAMP(62);
-      issue_q(true);
-      for (int j = 0; j < pre; ++j) issue_prefix(stage(j), ks + S * j);
-      TSFA_STAMP(60);
-      wait_units<LPU, NOS - S>(pre);  // Q landed (loads complete in order)
-      TSFA_STAMPW(35);
-      sync_lds();
-      TSFA_STAMP(1);
-      read_q(true);
-    } else {
-      pre = min(mine, NS - QS);
-      issue_q(false);
-      unit_bytes = (int64_t)kUnitKeys * dstride * (int64_t)sizeof(T);
-      run_rows = reinterpret_cast<const char*>(dbase + ((int64_t)u_lo * kUnitKeys + dma_u0 * DRPL) * dstride);
-      n_fast = rows_fast ? max(0, min(n, a.kv_len / kUnitKeys - u_lo)) : 0;
-      m0_off = dlds + (uint32_t)dma_u0 * 1024u;
-      for (int j = 0; j < pre; ++j) issue_prefix(sring_lds + j * SB, ks + S * j);
-      wait_units<LPU, NS - QS>(pre);
-      sync_lds();
-      TSFA_STAMP(1);
-      read_q(false);
-      if (QS > 1) sync_lds();
-    }
+    const int pre = min(mine, NS - QS);
+    TSFA_STAMP(62);
+    issue_q();
+    for (int j = 0; j < pre; ++j) issue_prefix(sring_lds + j * SB, ks + S * j);
+    TSFA_STAMP(60);
+    wait_units<LPU, NS - QS>(pre);
+    sync_lds();
+    TSFA_STAMP(1);
+    read_q();
+    if (QS > 1) sync_lds();
     // Steady refills (FAST, rotation off): the next unit's row pointer and
     // ring stage advance by S units and one stage per refill.
     const char* seq_rows = nullptr;
@@ -1134,11 +1083,6 @@ void split_kernel(const SplitArgs a) {
         },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix,
         FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next});
-    // a folded tree phase runs on the rings
-    oneshot = false;
-    st_base = sring_lds;
-    st_step = SB;
-    st_mask = NS - 1;
   }
   if (do_tree) {
     // after a prefix run: its ring reads and loads done (the block states
@@ -1443,8 +1387,11 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
     const float lse2 = (l > 0.f) ? mx * a.scale_log2 + __log2f(l) : -INFINITY;
     a.lse[((int64_t)b * a.num_heads + h) * a.q_len + t] = lse2 * 0.69314718055994531f;
   }
+  // O leaves by non-temporal stores: no dirty O lines stay in the L2 for the
+  // end-of-kernel write-back (the Llama-3-8B decode shape: 16.5-16.9 ->
+  // 16.2-16.5 us per call, same-box A/B; the combine alone is unchanged)
   T* dst = static_cast<T*>(a.o) + b * a.sob + (int64_t)h * a.soh + (int64_t)t * a.som + part * kEpt;
-  *reinterpret_cast<TV*>(dst) = out;
+  __builtin_nontemporal_store(out, reinterpret_cast<TV*>(dst));
 }
 
 // Merge the n_slots partials of every row and write O.  Threads walk the

@@ -163,11 +163,10 @@ def test_cases_other_kernels(case, kernel, monkeypatch):
 
 # A prefix whose length is a multiple of 32 takes the kernel with unchecked
 # prefix ring steps (one key stream or two; with two, its non-temporal
-# flavour too).  The runs here are 24, 24 and 16 units (a shorter last run;
-# with two streams and D = 64 the last one is a one-shot run), so the steady
-# ring steps and the checked tail both run; the result must equal the checked
-# kernel's bit for bit (the same arithmetic in the same order) and match the
-# oracle.
+# flavour too).  The runs here are 24, 24 and 16 units (a shorter last run),
+# so the steady ring steps and the checked tail both run; the result must
+# equal the checked kernel's bit for bit (the same arithmetic in the same
+# order) and match the oracle.
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("streams,nt", [("1", "0"), ("2", "0"), ("2", "1")])
 def test_fast_ring_matches_checked_steps(d, streams, nt, monkeypatch):
