@@ -215,9 +215,12 @@ def eager_call_timing(w, qd, ks, vs, mask_dev, meta, reps: int = 100, batches: i
     with metadata built once.  us_per_call: wall time per call over `reps`
     calls with one synchronisation at the end (host cost and device time
     overlap); host_us_per_call: time for the call to return (launch path).
-    Each is the median of `batches` batches: a rare stall of the host process
-    (one call of 40 ms among 200 has been seen) moves one batch, not the
-    figure."""
+    Each is the median of `batches` batches.  The slowest single call of each
+    form is logged with its position, beside the Python garbage collector's
+    pauses over the same batches (gc.callbacks): a rare stall of the host
+    process moves one batch, and the log says whether it was a collection."""
+    import gc
+
     import torch
 
     import eagle_tree_sparse_bridge as bridge
@@ -230,25 +233,50 @@ def eager_call_timing(w, qd, ks, vs, mask_dev, meta, reps: int = 100, batches: i
         "forward_with_metadata": lambda i: tsf.tree_sparse_attention_fwd(qd, ks[i % len(ks)], vs[i % len(vs)], meta,
                                                                          out=out),
     }
+    gc_pauses = []
+    gc_t0 = [0.0]
+
+    def on_gc(phase, info):
+        if phase == "start":
+            gc_t0[0] = time.perf_counter()
+        else:
+            gc_pauses.append((info.get("generation", -1), (time.perf_counter() - gc_t0[0]) * 1e6))
+
     res = {}
     for name, fn in forms.items():
         for i in range(10):
             fn(i)
         torch.cuda.synchronize()
         walls, hosts = [], []
-        for _ in range(batches):
-            host = 0.0
-            t0 = time.perf_counter()
-            for i in range(reps):
-                h0 = time.perf_counter()
-                fn(i)
-                host += time.perf_counter() - h0
-            torch.cuda.synchronize()
-            walls.append((time.perf_counter() - t0) / reps * 1e6)
-            hosts.append(host / reps * 1e6)
+        slowest = (0.0, -1, -1)
+        gc_pauses.clear()
+        gc.callbacks.append(on_gc)
+        try:
+            for bi in range(batches):
+                host = 0.0
+                t0 = time.perf_counter()
+                for i in range(reps):
+                    h0 = time.perf_counter()
+                    fn(i)
+                    dh = time.perf_counter() - h0
+                    host += dh
+                    if dh > slowest[0]:
+                        slowest = (dh, bi, i)
+                torch.cuda.synchronize()
+                walls.append((time.perf_counter() - t0) / reps * 1e6)
+                hosts.append(host / reps * 1e6)
+        finally:
+            gc.callbacks.remove(on_gc)
+        by_gen = {}
+        for gen, us in gc_pauses:
+            n, mx = by_gen.get(gen, (0, 0.0))
+            by_gen[gen] = (n + 1, max(mx, us))
         res[name] = {"us_per_call": round(sorted(walls)[batches // 2], 2),
                      "host_us_per_call": round(sorted(hosts)[batches // 2], 2),
-                     "batches_us_per_call": [round(x, 2) for x in walls]}
+                     "batches_us_per_call": [round(x, 2) for x in walls],
+                     "slowest_call": {"host_us": round(slowest[0] * 1e6, 1), "batch": slowest[1], "index": slowest[2]},
+                     "gc_collections": {f"gen{g}": {"count": n, "max_pause_us": round(mx, 1)}
+                                        for g, (n, mx) in sorted(by_gen.items())}}
     res["sample"] = (f"{batches} batches of {reps} eager calls each (median batch), cycling the cold K/V copies; "
                      "one synchronisation per batch")
     return res

@@ -1798,6 +1798,103 @@ extern "C" int tsfa_fwd(const void* q, const void* k, const void* v, void* o, co
                   workspace, workspace_bytes, stream_);
 }
 
+// ------------------------------------- metadata build + forward in one call
+// run_tree_sparse_kernel(q, k, v, tree_mask) as one C call: the device
+// metadata builder (tsfa_meta_build) writes the capacity-layout tree record
+// into the front of the workspace and the forward reads it there, in stream
+// order, with no host synchronisation.  Workspace layout (each section
+// 256-byte aligned): row_ptr, col_idx, blk_type, payload, offset, counts of
+// n_masks trees, the builder's scratch, the forward's split-KV partials.
+namespace {
+
+struct TreeCallLayout {
+  size_t off[8];  // row_ptr col_idx blk_type payload offset counts meta_ws fwd_ws
+  size_t total, fwd_bytes;
+  int nqb, ntb, words;
+  int64_t cap;
+};
+
+int tree_call_layout(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int n_masks,
+                     int block_m, int block_n, int head_dim, TreeCallLayout* L) {
+  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || kv_len < q_len ||
+      (n_masks != 1 && n_masks != batch))
+    return TSFA_ERR_INVALID_ARGUMENT;
+  const int st = tsfa_meta_check_args(n_masks, q_len, block_m, block_n);
+  if (st != TSFA_OK) return st;
+  meta::MetaGeom g;
+  if (!meta::meta_geom(q_len, block_m, block_n, &g)) return TSFA_ERR_UNSUPPORTED;
+  L->nqb = g.nqb;
+  L->ntb = g.ntb;
+  L->words = g.words;
+  L->cap = g.cap;
+  const size_t n = (size_t)n_masks;
+  const size_t sizes[7] = {n * (g.nqb + 1) * 4, n * g.cap * 4, n * g.cap, n * g.cap * g.words * 4, n * g.cap * 4,
+                           n * 2 * 4, tsfa_meta_workspace_bytes(n_masks, q_len, block_m, block_n)};
+  size_t at = 0;
+  for (int i = 0; i < 7; ++i) {
+    L->off[i] = at;
+    at += align256(std::max<size_t>(sizes[i], 1));
+  }
+  L->off[7] = at;
+  L->fwd_bytes = tsfa_fwd_workspace_bytes(batch, num_heads, num_kv_heads, q_len, kv_len, kv_len - q_len, head_dim);
+  if (L->fwd_bytes == 0) return TSFA_ERR_UNSUPPORTED;
+  L->total = at + L->fwd_bytes;
+  return TSFA_OK;
+}
+
+}  // namespace
+
+extern "C" size_t tsfa_tree_attention_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len,
+                                                      int kv_len, int n_masks, int block_m, int block_n,
+                                                      int head_dim) {
+  TreeCallLayout L;
+  if (tree_call_layout(batch, num_heads, num_kv_heads, q_len, kv_len, n_masks, block_m, block_n, head_dim, &L) !=
+      TSFA_OK)
+    return 0;
+  return L.total;
+}
+
+extern "C" int tsfa_tree_attention(const void* q, const void* k, const void* v, void* o, const uint8_t* mask,
+                                   int64_t mask_seq_stride, int64_t mask_row_stride, int n_masks,
+                                   const int64_t* strides, float sm_scale, int batch, int num_heads,
+                                   int num_kv_heads, int q_len, int kv_len, int block_m, int block_n, int head_dim,
+                                   int dtype, void* workspace, size_t workspace_bytes, tsfa_stream_t stream) {
+  if (kv_len < q_len) return TSFA_ERR_INVALID_ARGUMENT;  // eagle_tree_sparse_bridge.py:91-93
+  if (batch == 0) return TSFA_OK;
+  TreeCallLayout L;
+  int st = tree_call_layout(batch, num_heads, num_kv_heads, q_len, kv_len, n_masks, block_m, block_n, head_dim, &L);
+  if (st != TSFA_OK) return st;
+  const int prefix_len = kv_len - q_len;
+  // the forward's own checks first: nothing is launched for a call it refuses
+  st = tsfa_fwd_check_args(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, L.nqb, L.ntb,
+                           num_heads / num_kv_heads, block_m, block_n, head_dim, dtype);
+  if (st != TSFA_OK) return st;
+  if (mask == nullptr || strides == nullptr || mask_row_stride < 1 || mask_seq_stride < 0)
+    return TSFA_ERR_INVALID_ARGUMENT;
+  if (q == nullptr || o == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
+  st = check_strides(q, strides, o, strides + 12);
+  if (st == TSFA_OK) st = check_kv_strides(k, strides + 4, v, strides + 8);
+  if (st != TSFA_OK) return st;
+  if (workspace == nullptr || workspace_bytes < L.total || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return TSFA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  int32_t* row_ptr = reinterpret_cast<int32_t*>(ws + L.off[0]);
+  int32_t* col_idx = reinterpret_cast<int32_t*>(ws + L.off[1]);
+  int8_t* blk_type = reinterpret_cast<int8_t*>(ws + L.off[2]);
+  int32_t* payload = reinterpret_cast<int32_t*>(ws + L.off[3]);
+  int32_t* offset = reinterpret_cast<int32_t*>(ws + L.off[4]);
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + L.off[5]);
+  st = tsfa_meta_build(mask, mask_seq_stride, mask_row_stride, n_masks, q_len, block_m, block_n, row_ptr, col_idx,
+                       blk_type, payload, offset, counts, ws + L.off[6], L.off[7] - L.off[6], stream);
+  if (st != TSFA_OK) return st;
+  // one tree for the batch: stride 0; one per sequence: the capacity layout
+  const int64_t ms[5] = {n_masks > 1 ? (int64_t)L.nqb + 1 : 0, n_masks > 1 ? L.cap : 0, n_masks > 1 ? L.cap : 0,
+                         n_masks > 1 ? L.cap * L.words : 0, n_masks > 1 ? L.cap : 0};
+  return tsfa_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, ms, strides, sm_scale, batch, num_heads,
+                  num_kv_heads, q_len, kv_len, prefix_len, L.nqb, L.ntb, num_heads / num_kv_heads, block_m, block_n,
+                  head_dim, dtype, ws + L.off[7], L.fwd_bytes, stream);
+}
+
 // ------------------------------------------------- allocation-free forward
 // The split-KV partials of tsfa_fwd_noalloc live in this file-scope device
 // array: each GPU the library runs on holds its own copy (kNoAllocBytes) until

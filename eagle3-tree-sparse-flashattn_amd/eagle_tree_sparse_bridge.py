@@ -31,9 +31,12 @@ import torch
 
 from tree_sparse_flashattn import (
     BatchedTreeSparseMetadata,
+    _check_qkv,
+    _layout_ok,
     prepare_tree_sparse_metadata_batched,
     tree_sparse_attention_fwd,
 )
+from tsfa import _lib
 
 
 def build_tree_metadata(tree_mask: torch.Tensor, prefix_len: int, block_m: int,
@@ -152,6 +155,9 @@ def run_tree_sparse_kernel(
     if metadata is None:
         if tree_mask is None:
             raise ValueError("run_tree_sparse_kernel needs a tree_mask or prebuilt metadata")
+        out = _tree_call(query_states, key_states, value_states, tree_mask, block_m, block_n)
+        if out is not None:
+            return out
         metadata = build_tree_metadata(tree_mask.to(device=query_states.device), prefix_len, block_m, block_n)
     else:
         nqb = (q_len + block_m - 1) // block_m
@@ -160,6 +166,75 @@ def run_tree_sparse_kernel(
                 metadata.n_tree_blocks) != (prefix_len, block_m, block_n, nqb, ntb):
             raise ValueError("metadata was built for another prefix_len, q_len or block size")
     return tree_sparse_attention_fwd(query_states, key_states, value_states, metadata)
+
+
+# Launch arguments of the one-call path (tsfa_tree_attention: the metadata
+# built from the device mask, then the forward, in one C call) per geometry;
+# False marks a geometry that takes the general path.
+_TREE_CALLS: dict = {}
+
+
+def _tree_call_plan(q, k, v, mask, block_m, block_n):
+    """Launch arguments of tsfa_tree_attention for this geometry, or False when
+    the call needs the general path (a mask that is not a bool device tensor
+    with unit column stride, head dims the kernels pad, layouts they copy)."""
+    _check_qkv(q, k, v)
+    bsz, n_heads, q_len, head_dim = q.shape
+    _, n_kv_heads, kv_len, _ = k.shape
+    if head_dim not in (64, 128) or not all(_layout_ok(t) for t in (q, k, v)):
+        return False
+    if mask.dim() == 2:
+        n_masks, seq_stride = 1, 0
+    elif mask.dim() == 3 and mask.shape[0] in (1, bsz):
+        n_masks, seq_stride = mask.shape[0], mask.stride(0)
+    else:
+        return False
+    if tuple(mask.shape[-2:]) != (q_len, q_len) or mask.stride(-1) != 1 or mask.stride(-2) < 1:
+        return False
+    probe = torch.empty_like(q)  # the strides empty_like gives O for this q layout
+    if not _layout_ok(probe):
+        return False
+    lib = _lib.load()
+    ws_bytes = lib.tsfa_tree_attention_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, n_masks, block_m,
+                                                        block_n, head_dim)
+    if ws_bytes == 0:
+        return False
+    strides = _lib.i64_array((*q.stride(), *k.stride(), *v.stride(), *probe.stride()))
+    ints = (bsz, n_heads, n_kv_heads, q_len, kv_len, block_m, block_n, head_dim, _lib.dtype_code(q.dtype))
+    return (strides, ints, ws_bytes, 1.0 / math.sqrt(head_dim), n_masks, seq_stride, mask.stride(-2))
+
+
+def _tree_call(q, k, v, mask, block_m, block_n):
+    """run_tree_sparse_kernel on a device mask in one C call, or None."""
+    if mask.dtype != torch.bool or mask.device != q.device or q.dtype != k.dtype or q.dtype != v.dtype:
+        return None
+    key = (q.shape, q.stride(), k.shape, k.stride(), v.stride(), q.dtype, mask.shape, mask.stride(), block_m,
+           block_n, q.device, (q.data_ptr() | k.data_ptr() | v.data_ptr()) & 15)
+    entry = _TREE_CALLS.get(key)
+    if entry is None:
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            entry = False
+        else:
+            entry = _tree_call_plan(q, k, v, mask, block_m, block_n)
+        if len(_TREE_CALLS) >= 64:
+            _TREE_CALLS.clear()
+        _TREE_CALLS[key] = entry
+    if entry is False:
+        return None
+    strides, ints, ws_bytes, scale, n_masks, seq_stride, row_stride = entry
+    dev = q.device
+    out = torch.empty_like(q)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
+    lib = _lib.load()
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(), seq_stride, row_stride, n_masks,
+            strides, scale, *ints, ws.data_ptr(), ws_bytes)
+    if dev.index == torch.cuda.current_device():
+        st = lib.tsfa_tree_attention(*args, torch.cuda.current_stream().cuda_stream)
+    else:
+        with torch.cuda.device(dev):
+            st = lib.tsfa_tree_attention(*args, torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check("run_tree_sparse_kernel", st)
+    return out
 
 
 # ------------------------------------------------------------ model shims

@@ -44,6 +44,8 @@ EXPORTS = (
     "tsfa_fwd",
     "tsfa_fwd_lse",
     "tsfa_fwd_noalloc",
+    "tsfa_tree_attention",
+    "tsfa_tree_attention_workspace_bytes",
     "tsfa_bwd",
     "tsfa_bwd_workspace_bytes",
     "tsfa_fwd_paged",
@@ -77,6 +79,9 @@ _SIGNATURES = {
                      + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
     "tsfa_fwd_noalloc": (_c_int, [_c_vp] * 9 + [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                          + [_c_int] * 13 + [_c_vp]),
+    "tsfa_tree_attention": (_c_int, [_c_vp] * 5 + [_c_i64, _c_i64, _c_int, ctypes.POINTER(_c_i64), _c_float]
+                            + [_c_int] * 9 + [_c_vp, _c_size, _c_vp]),
+    "tsfa_tree_attention_workspace_bytes": (_c_size, [_c_int] * 9),
     "tsfa_bwd_workspace_bytes": (_c_size, [_c_int] * 10),
     "tsfa_bwd": (_c_int, [_c_vp] * 14 + [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),

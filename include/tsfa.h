@@ -16,6 +16,8 @@
  *                     (argument list: tree_sparse_flashattn.py:164-203,
  *                      call sites eagle_tree_sparse_bridge.py:119-158,
  *                      benchmark.py:183-194)
+ *   tsfa_tree_attention  run_tree_sparse_kernel            eagle_tree_sparse_bridge.py:76-159
+ *                     (metadata build + forward in one call)
  */
 #ifndef TSFA_H_
 #define TSFA_H_
@@ -218,6 +220,28 @@ int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr
                    int n_q_blocks, int n_tree_blocks, int gqa_group_size,
                    int block_m, int block_n, int head_dim, int dtype,
                    void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
+
+/* run_tree_sparse_kernel(q, k, v, tree_mask) in one call
+ * (eagle_tree_sparse_bridge.py:76-159: metadata from the tree mask, then the
+ * forward with prefix_len = kv_len - q_len, eagle_tree_sparse_bridge.py:91-117):
+ * tsfa_meta_build on the device mask into the front of `workspace`, then
+ * tsfa_fwd reading that record, both on `stream`, no host synchronisation.
+ * mask      uint8 (nonzero = visible) device memory: n_masks trees of
+ *           [q_len, q_len] rows mask_row_stride apart, trees mask_seq_stride
+ *           apart; n_masks = 1 (one tree for the batch, as the reference) or
+ *           batch (one tree per sequence)
+ * strides, dtype, sm_scale, o: as tsfa_fwd.
+ * workspace of tsfa_tree_attention_workspace_bytes, 256-byte aligned.
+ * Errors as tsfa_fwd / tsfa_meta_build; kv_len < q_len is
+ * TSFA_ERR_INVALID_ARGUMENT (the reference's ValueError).  The forward's
+ * checks run before anything is launched. */
+size_t tsfa_tree_attention_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                                           int n_masks, int block_m, int block_n, int head_dim);
+int tsfa_tree_attention(const void* q, const void* k, const void* v, void* o, const uint8_t* mask,
+                        int64_t mask_seq_stride, int64_t mask_row_stride, int n_masks,
+                        const int64_t* strides, float sm_scale, int batch, int num_heads,
+                        int num_kv_heads, int q_len, int kv_len, int block_m, int block_n, int head_dim,
+                        int dtype, void* workspace, size_t workspace_bytes, tsfa_stream_t stream);
 
 /* tsfa_fwd without the workspace argument, for callers that cannot allocate
  * device memory (code under graph capture, tight serving loops, harnesses

@@ -143,3 +143,18 @@ def _paged_call(page_size=16, n_pages=8, n_indices=16, pt_stride=4, indptr=None,
 ])
 def test_fwd_paged_rejects_on_host(kw, status):
     assert _paged_call(**kw) == status
+
+
+@needs_full_library
+def test_tree_attention_rejects_on_the_host():
+    # kv_len < q_len is the reference's ValueError (eagle_tree_sparse_bridge.py:91-93),
+    # refused before any device query; a null mask or strides likewise
+    lib = _lib.load()
+    strides = (ctypes.c_int64 * 16)(*([1] * 16))
+    args = dict(batch=1, num_heads=8, num_kv_heads=2, q_len=40, kv_len=30, block_m=16, block_n=32, head_dim=128,
+                dtype=_lib.TSFA_DTYPE_BF16)
+    st = lib.tsfa_tree_attention(None, None, None, None, None, 0, 40, 1, strides, ctypes.c_float(0.1),
+                                 *args.values(), None, 0, None)
+    assert st == _lib.TSFA_ERR_INVALID_ARGUMENT
+    assert lib.tsfa_tree_attention_workspace_bytes(1, 8, 2, 40, 30, 1, 16, 32, 128) == 0
+    assert lib.tsfa_tree_attention_workspace_bytes(2, 8, 2, 40, 100, 3, 16, 32, 128) == 0  # n_masks not 1 or B

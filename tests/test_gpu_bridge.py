@@ -172,3 +172,42 @@ def test_cache_hidden_verify_uses_the_tree_kernel_with_gqa_heads():
     assert err <= TOL[torch.bfloat16] + 1e-2, err
     assert all(torch.equal(a, c) for a, c in zip(ch_got[0], ch_want[0]))
     assert ch_got[0][0].shape[1] == heads  # the cache still holds the repeat_kv copies
+
+
+@pytest.mark.parametrize("case", ["shared", "per-sequence", "strided", "fp16-d64", "float-mask"])
+def test_one_call_path_matches_the_metadata_path(case):
+    # run_tree_sparse_kernel(q, k, v, tree_mask) on a device bool mask runs
+    # tsfa_tree_attention (metadata build + forward in one C call); its O must
+    # equal the general path (device metadata record, then tsfa_fwd) bit for
+    # bit, and a float mask (nonzero = visible) takes the general path
+    print(f"[bridge] one-call path {case}", flush=True)
+    dtype, d = (torch.float16, 64) if case == "fp16-d64" else (torch.bfloat16, 128)
+    q, k, v, mask = _inputs(b=3, hq=8, hkv=2, t=40, p=200, d=d, dtype=dtype, seed=11)
+    if case == "per-sequence":
+        rng = np.random.default_rng(12)
+        mask = torch.from_numpy(np.stack([trees.ancestor_mask(trees.random_parents(40, rng)) for _ in range(3)]))
+    qd, kd, vd, md = q.cuda(), k.cuda(), v.cuda(), mask.cuda()
+    if case == "strided":
+        # [B, N, H, D] storage viewed as [B, H, N, D], as benchmark.py:182-194 passes it
+        qd = qd.transpose(1, 2).contiguous().transpose(1, 2)
+        kd = kd.transpose(1, 2).contiguous().transpose(1, 2)
+        vd = vd.transpose(1, 2).contiguous().transpose(1, 2)
+    if case == "float-mask":
+        md = md.float()
+    bridge._TREE_CALLS.clear()
+    out = bridge.run_tree_sparse_kernel(qd, kd, vd, md, block_m=16, block_n=32)
+    took_one_call = any(e is not False for e in bridge._TREE_CALLS.values())
+    assert took_one_call == (case != "float-mask")
+    meta = bridge.build_tree_metadata(md.bool() if case == "float-mask" else md, k.shape[2] - q.shape[2], 16, 32)
+    ref = tsf.tree_sparse_attention_fwd(qd, kd, vd, meta)
+    torch.cuda.synchronize()
+    assert torch.equal(out.isnan(), ref.isnan())
+    assert torch.equal(out.nan_to_num(0.0), ref.nan_to_num(0.0))
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, k.shape[2] - q.shape[2]), dtype)
+
+
+def test_one_call_path_refuses_kv_shorter_than_q():
+    q, k, v, mask = _inputs(b=1, t=40, p=0)
+    with pytest.raises(ValueError):
+        bridge.run_tree_sparse_kernel(q.cuda(), k[:, :, :30].cuda(), v[:, :, :30].cuda(), mask.cuda(),
+                                      block_m=16, block_n=32)
