@@ -912,6 +912,9 @@ extern "C" int tsfa_bwd(const void* q, const void* k, const void* v, const void*
   int st = tsfa_fwd_check_args(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
                                n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype);
   if (st != TSFA_OK) return st;
+  // the backward kernels: 16-bit inputs, head_dim 64 or 128
+  if ((dtype != TSFA_DTYPE_FP16 && dtype != TSFA_DTYPE_BF16) || (head_dim != 64 && head_dim != 128))
+    return TSFA_ERR_UNSUPPORTED;
   if (batch == 0 || q_len == 0) return TSFA_OK;
   if (strides == nullptr || meta_seq_stride == nullptr) return TSFA_ERR_INVALID_ARGUMENT;
   const void* ptrs[9] = {q, k, v, o, dout, dq, dk, dv, lse};

@@ -1306,7 +1306,7 @@ constexpr int kCombineThreads = 128;
 // group 0 writes the row: GR times the threads for the same 16-byte loads,
 // 1/GR of the conversions and multiply-adds per thread (the combine is bound
 // by those VALU instructions at one or two waves per SIMD, not by its loads).
-template <typename T, int D, int NB, int GR = 1>
+template <typename T, int D, int NB, int GR = 1, typename PT = T>
 __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int part, int half = 0) {
   const int64_t TG = (int64_t)a.q_len * a.group;
   const int t = R / a.group, g = R - t * a.group;
@@ -1314,9 +1314,10 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
   const int h = kvh * a.group + g;
   const int64_t r0 = bk * a.n_slots * TG + R;
   const float2* ml = a.ws_ml + r0;
-  const T* src = static_cast<const T*>(a.ws_o) + r0 * D + part * kEpt;
+  const PT* src = static_cast<const PT*>(a.ws_o) + r0 * D + part * kEpt;
   const int64_t slot_stride = TG * D;
   typedef T TV __attribute__((ext_vector_type(kEpt)));
+  typedef PT PV __attribute__((ext_vector_type(kEpt)));
 
   // Running merge over batches of slots: a batch's (m, l) pairs and partial
   // vectors are loaded together, then folded into (M, L, acc) with the same
@@ -1329,12 +1330,12 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
   for (int s0 = half; s0 < a.n_slots; s0 += SS * NB) {
     const int nb = min(NB, (a.n_slots - s0 + SS - 1) / SS);
     float2 v[NB];
-    TV x[NB];
+    PV x[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int s = s0 + SS * min(i, nb - 1);  // duplicates of the last slot get weight 0 below
       v[i] = ml[s * TG];
-      x[i] = *reinterpret_cast<const TV*>(src + s * slot_stride);
+      x[i] = *reinterpret_cast<const PV*>(src + s * slot_stride);
     }
     float bm = mx;
 #pragma unroll
@@ -1396,7 +1397,7 @@ __device__ inline void merge_row(const CombineArgs& a, int64_t bk, int R, int pa
 
 // Merge the n_slots partials of every row and write O.  Threads walk the
 // workspace rows in order (coalesced partial loads).
-template <typename T, int D, int NB, int GR = 1>
+template <typename T, int D, int NB, int GR = 1, typename PT = T>
 __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineArgs a) {
   constexpr int TPR = D / kEpt;
   static_assert(GR * TPR <= 64 && kCombineThreads % (GR * TPR) == 0, "a row's groups share one wave");
@@ -1407,7 +1408,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const CombineA
   // (a whole row's threads leave together: its groups exchange within it)
   if (row >= a.xcd_row[x + 1]) return;
   const int64_t bk = row / TG;
-  merge_row<T, D, NB, GR>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR), (int)(threadIdx.x / TPR) % GR);
+  merge_row<T, D, NB, GR, PT>(a, bk, (int)(row - bk * TG), (int)(threadIdx.x % TPR), (int)(threadIdx.x / TPR) % GR);
 }
 
 template <typename T, int D, int S, bool PAGED, bool C32 = false, int FAST = 0>
@@ -1529,6 +1530,304 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
+// ------------------------------------------------------------ generic kernel
+// Head dims above 128 (bf16 / fp16) and fp32 inputs.  The same semantics as
+// split_kernel (tree_sparse_flashattn.py:211-339) with a simpler structure:
+// a workgroup is 4 waves of 32 packed query rows (a 128-row chunk, r = t*G +
+// g) over one split of the key axis in units of 32 keys; each unit's K and V
+// go through LDS, prefix keys are visible, tree keys by the CSR record of the
+// row's q-block (FULL, or the MIXED bit).  S^T = K Q^T and O^T += V^T P^T on
+// v_mfma_f32_32x32x16_{bf16,f16} (V^T from ds_read_b64_tr_b16) or
+// v_mfma_f32_32x32x2_f32, with the key order of the P V product permuted so
+// that P^T comes straight from the S^T accumulator.  Every split writes an
+// fp32 partial (O / l and (m, l)) that combine_kernel merges.
+struct GenArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* row_ptr;
+  const int32_t* col_idx;
+  const int8_t* blk_type;
+  const int32_t* payload;
+  const int32_t* offset;
+  int64_t ms[5];  // per-sequence strides of the five metadata arrays (0: one tree)
+  int64_t sqb, sqh, sqm, skb, skh, skn, svb, svh, svn;
+  float scale_log2;  // |sm_scale| * log2(e), never 0
+  int neg_q;         // sm_scale < 0: Q enters negated
+  int num_kv_heads, group, q_len, kv_len, prefix_len, block_m, block_n;
+  int n_chunks, n_units, units_per_split, n_slots;
+  float* ws_o;     // [B*Hkv][n_slots][q_len*G][D] fp32 partial O / l
+  float2* ws_ml;   // [B*Hkv][n_slots][q_len*G] (m, l)
+};
+
+constexpr int kGenWaves = 4;
+constexpr int kGenRows = 32 * kGenWaves;
+
+template <typename T, int D>
+__global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int ROWB = D * (int)sizeof(T);  // bytes of one key row
+  constexpr int TILE = 32 * ROWB;           // bytes of one unit's K (or V)
+  constexpr int DT = D / 32;
+  constexpr int KS = F32 ? D / 2 : D / 16;  // k-steps of S^T
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  unsigned char* kt = smem;
+  unsigned char* vt = smem + TILE;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 31, lh = lane >> 5;
+  const int chunk = blockIdx.x % a.n_chunks;
+  const int rest = blockIdx.x / a.n_chunks;
+  const int slot = rest % a.n_slots, bk = rest / a.n_slots;
+  const int b = bk / a.num_kv_heads, kvh = bk % a.num_kv_heads;
+  const int G = a.group, TG = a.q_len * G;
+  const int r = chunk * kGenRows + wave * 32 + ln;  // the lane's packed row
+  const bool row_ok = r < TG;
+  const int R = min(r, TG - 1);
+  const int t = R / G, g = R - t * G;
+  const float sl2 = a.scale_log2;
+
+  const T* kbase = static_cast<const T*>(a.k) + b * a.skb + kvh * a.skh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.svb + kvh * a.svh;
+  const T* qrow = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm;
+
+  // Q^T operand: 16-bit, lane (ln, lh) holds d = 16kk + 8lh + [0, 8) of its
+  // row; fp32, d = 2kk + lh.  Q is negated for a negative scale.
+  typedef typename std::conditional<F32, float, i16x8>::type QF;
+  QF qf[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    if constexpr (F32) {
+      qf[kk] = a.neg_q ? -qrow[2 * kk + lh] : qrow[2 * kk + lh];
+    } else {
+      qf[kk] = *reinterpret_cast<const i16x8*>(qrow + 16 * kk + 8 * lh) ^ (short)(a.neg_q ? 0x8000 : 0);
+    }
+  }
+
+  // The lane's row in the tree record: token t, q-block t / BM.
+  const int32_t* rp = a.row_ptr + b * a.ms[0];
+  const int32_t* ci = a.col_idx + b * a.ms[1];
+  const int8_t* bt = a.blk_type + b * a.ms[2];
+  const int32_t* pl = a.payload + b * a.ms[3];
+  const int32_t* of = a.offset + b * a.ms[4];
+  const int qb = t / a.block_m, tl = t - qb * a.block_m;
+  const int e_lo = rp[qb], e_hi = rp[qb + 1];
+  // Visibility of keys k0 .. k0+31 for the lane's row: prefix keys, then the
+  // tree keys of the row's FULL and MIXED blocks (tree_sparse_flashattn.py:
+  // 266-270, :307-318); keys past kv_len are not visible.
+  auto vis_word = [&](int k0) {
+    const int P = a.prefix_len, BN = a.block_n;
+    const int np = min(max(P - k0, 0), 32);
+    uint32_t w = np >= 32 ? 0xffffffffu : ((1u << np) - 1u);
+    const int c_lo = max(k0, P) - P, c_hi = min(k0 + 32, a.kv_len) - P;  // tree columns of the unit
+    if (c_lo < c_hi) {
+      for (int e = e_lo; e < e_hi; ++e) {
+        const int cb = ci[e] * BN;
+        const int lo = max(cb, c_lo), hi = min(cb + BN, c_hi);
+        if (lo >= hi) continue;
+        const bool full = bt[e] == TSFA_FULL_BLOCK;
+        const int off = full ? 0 : of[e];
+        for (int c = lo; c < hi; ++c) {
+          const int flat = tl * BN + (c - cb);
+          const uint32_t bit = full ? 1u : (((uint32_t)pl[off + (flat >> 5)] >> (flat & 31)) & 1u);
+          w |= bit << (c + P - k0);
+        }
+      }
+    }
+    return w;
+  };
+
+  f32x16 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int u_lo = slot * a.units_per_split;
+  const int u_hi = min(u_lo + a.units_per_split, a.n_units);
+  for (int u = u_lo; u < u_hi; ++u) {
+    const int k0 = u * 32;
+    // K and V of the unit into LDS (rows past kv_len repeat the last key;
+    // those keys are not visible)
+    __syncthreads();
+    for (int c = tid; c < 2 * TILE / 16; c += kGenWaves * 64) {
+      const int half = c / (TILE / 16), cc = c % (TILE / 16);
+      const int row = cc / (ROWB / 16), col = cc % (ROWB / 16);
+      const int key = min(k0 + row, a.kv_len - 1);
+      const T* src = (half ? vbase + (int64_t)key * a.svn : kbase + (int64_t)key * a.skn) + col * (16 / (int)sizeof(T));
+      *reinterpret_cast<uint4*>(smem + half * TILE + row * ROWB + col * 16) = *reinterpret_cast<const uint4*>(src);
+    }
+    __syncthreads();
+    // S^T: MFMA row = key, column = query row; lane (ln, lh) element i is key
+    // 8*(i/4) + 4*lh + i%4 of row ln
+    f32x16 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      if constexpr (F32) {
+        const float kv = *reinterpret_cast<const float*>(kt + ln * ROWB + (2 * kk + lh) * 4);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv, qf[kk], s, 0, 0, 0);
+      } else {
+        const i16x8 kf = *reinterpret_cast<const i16x8*>(kt + ln * ROWB + (16 * kk + 8 * lh) * 2);
+        s = Mma<T>::run(bit_cast<typename Mma<T>::vec8>(kf), bit_cast<typename Mma<T>::vec8>(qf[kk]), s);
+      }
+    }
+    // mask, online softmax (tree_sparse_flashattn.py:272-279, :320-327)
+    const uint32_t w = row_ok ? vis_word(k0) : 0u;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (!((w >> (8 * (i >> 2) + 4 * lh + (i & 3))) & 1u)) s[i] = -INFINITY;
+      mx = fmaxf(mx, s[i]);
+    }
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    const float rmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const float m_new = fmaxf(m_run, rmax);
+    // alpha = 1 while both are -inf; a first finite max scales the (zero) sums by 0
+    const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sl2);
+    m_run = m_new;
+    // p = 2^((s - m) * scale): exactly 1 at the row's maximum (a single
+    // visible key gives O = V bit for bit, fp32 included); 0 for masked keys
+    // and while no key is visible
+    float p[16], ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[i] = (m_new == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f((s[i] - m_new) * sl2);
+      ps += p[i];
+    }
+    l_run = l_run * alpha + ps;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    // O^T += V^T P^T, P rounded to the input dtype (tree_sparse_flashattn.py:278)
+    if constexpr (F32) {
+      // k-step i: keys 8*(i/4) + 4*k + i%4 (k = 0, 1), lane (ln, lh) gives its
+      // element i of P^T and V[key 8*(i/4) + 4*lh + i%4][32*dt + ln] of V^T
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = 8 * (i >> 2) + 4 * lh + (i & 3);
+          const float vv = *reinterpret_cast<const float*>(vt + key * ROWB + (32 * dt + ln) * 4);
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, p[i], o[dt], 0, 0, 0);
+        }
+    } else {
+      typedef typename Mma<T>::vec8 V8;
+      V8 pb[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pb[i >> 3][i & 7] = (T)p[i];
+      // V^T fragments by the transposing LDS read: lane i of 16-lane group x
+      // gets keys 16*s2 + 8*jj + 4*(x>>1) + [0,4) of d = 32*dt + 16*(x&1) + i
+      const int vx = lane >> 4, vi = lane & 15;
+      const int vrow = 4 * (vx >> 1) + (vi >> 2);
+      const int vcol = 2 * (16 * (vx & 1) + 4 * (vi & 3));
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (TSFA_LDS i16x4*)(vt + (16 * s2 + vrow) * ROWB + 64 * dt + vcol));
+          const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (TSFA_LDS i16x4*)(vt + (16 * s2 + 8 + vrow) * ROWB + 64 * dt + vcol));
+          const i16x8 vf = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+          o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
+        }
+    }
+  }
+
+  // partial of the lane's row: O / l in fp32 and (m, l); a split that saw no
+  // key stores O = 0 with m = -inf (weight 0 in the combine)
+  const float lt = pair_sum(l_run);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  const int64_t prow = ((int64_t)bk * a.n_slots + slot) * TG + r;
+  if (row_ok) {
+    float* dst = a.ws_o + prow * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<f32x4*>(dst + 32 * dt + 8 * j + 4 * lh) =
+            f32x4{o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv};
+    if (lh == 0) a.ws_ml[prow] = make_float2(m_run, lt);
+  }
+}
+
+// The generic kernel's plan: 128-row chunks, the key axis cut into n_slots
+// splits of whole 32-key units so that the grid holds about two workgroups
+// per compute unit.
+struct GenPlan {
+  int n_chunks, n_units, units_per_split, n_slots, grid;
+  size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
+};
+
+inline bool gen_path(int head_dim, int dtype) { return head_dim > 128 || dtype == TSFA_DTYPE_FP32; }
+
+inline int gen_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int head_dim, int dtype,
+                    int cus, GenPlan* p) {
+  if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || kv_len < 1 || cus <= 0)
+    return TSFA_ERR_INVALID_ARGUMENT;
+  const int64_t TG = (int64_t)q_len * (num_heads / num_kv_heads);
+  if (TG > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
+  p->n_chunks = (int)((TG + kGenRows - 1) / kGenRows);
+  p->n_units = ceil_div(kv_len, 32);
+  const int64_t groups = (int64_t)batch * num_kv_heads * p->n_chunks;
+  const int64_t want = std::max<int64_t>(1, (2 * (int64_t)cus + groups - 1) / groups);
+  const int slots = (int)std::min<int64_t>(p->n_units, want);
+  p->units_per_split = ceil_div(p->n_units, slots);
+  p->n_slots = ceil_div(p->n_units, p->units_per_split);
+  const int64_t grid = groups * p->n_slots;
+  if (grid > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
+  p->grid = (int)grid;
+  const size_t es = dtype == TSFA_DTYPE_FP32 ? 4 : 2;
+  p->lds_bytes = 2 * 32 * (size_t)head_dim * es;
+  const size_t rows = (size_t)batch * num_heads * q_len;
+  p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 4);
+  p->ws_ml_bytes = align256(rows * p->n_slots * 8);
+  return TSFA_OK;
+}
+
+template <typename T, int D>
+int launch_gen(const GenArgs& ga, const CombineArgs& ca, const GenPlan& p, hipStream_t stream) {
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (p.lds_bytes > 65536 && (attr_set.load(std::memory_order_acquire) & bit) == 0) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gen_kernel<T, D>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
+      return TSFA_ERR_LAUNCH;
+    attr_set.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  if (g_kernel_mask & 1) {
+    hipLaunchKernelGGL((gen_kernel<T, D>), dim3(p.grid), dim3(kGenWaves * 64), p.lds_bytes, stream, ga);
+    if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+  }
+  if ((g_kernel_mask & 2) == 0) return TSFA_OK;
+  // the fp32 partials of every row merged: rows cut into 8 equal ranges, one
+  // per XCD slot of the combine's block ids (no placement to follow: the
+  // splits of a chunk spread over the grid)
+  CombineArgs c = ca;
+  constexpr int TPR = D / kEpt;
+  const int gr = (ca.n_slots > 4 && 2 * TPR <= 64) ? 2 : 1;
+  const int RPB = kCombineThreads / TPR / gr;
+  const int64_t rows = (int64_t)ca.batch * ca.num_kv_heads * ca.q_len * ca.group;
+  const int64_t per = (rows + 7) / 8;
+  for (int x = 0; x <= 8; ++x) c.xcd_row[x] = std::min<int64_t>(x * per, rows);
+  const int64_t blocks = 8 * ((per + RPB - 1) / RPB);
+  if (blocks > INT32_MAX) return TSFA_ERR_UNSUPPORTED;
+  const int ns = ca.n_slots;
+  if (ns <= 2)
+    hipLaunchKernelGGL((combine_kernel<T, D, 2, 1, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+  else if (ns <= 4)
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 1, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+  else if (gr == 2)
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 2, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+  else
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 1, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+  return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+}
+
 }  // namespace fwd
 }  // namespace tsfa
 
@@ -1571,9 +1870,17 @@ int device_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_le
 
 }  // namespace
 
-extern "C" size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
-                                           int prefix_len, int head_dim) {
+extern "C" size_t tsfa_fwd_workspace_bytes_for_dtype(int batch, int num_heads, int num_kv_heads, int q_len,
+                                                     int kv_len, int prefix_len, int head_dim, int dtype) {
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
+  if (gen_path(head_dim, dtype)) {
+    int cus = 0;
+    GenPlan gp;
+    if (device_cu_count(&cus) != TSFA_OK ||
+        gen_plan(batch, num_heads, num_kv_heads, q_len, kv_len, head_dim, dtype, cus, &gp) != TSFA_OK)
+      return 0;
+    return gp.ws_acc_bytes + gp.ws_ml_bytes;
+  }
   // enough for both the contiguous and the paged plan of the shape
   const Config cfg = config();
   Plan p, pp;
@@ -1581,6 +1888,12 @@ extern "C" size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_
       device_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim, true, cfg, &pp) != TSFA_OK)
     return 0;
   return std::max(p.ws_acc_bytes + p.ws_ml_bytes, pp.ws_acc_bytes + pp.ws_ml_bytes);
+}
+
+extern "C" size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                                           int prefix_len, int head_dim) {
+  return tsfa_fwd_workspace_bytes_for_dtype(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim,
+                                            TSFA_DTYPE_BF16);
 }
 
 extern "C" int tsfa_fwd_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int prefix_len,
@@ -1616,6 +1929,84 @@ struct KvSource {
   bool paged() const { return cache != nullptr; }
 };
 
+// The generic kernel's call (head_dim 256, fp32): contiguous K/V only.
+int gen_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32_t* row_ptr, const int32_t* col_idx,
+             const int8_t* blk_type, const int32_t* payload, const int32_t* offset, const int64_t* meta_seq_stride,
+             const int64_t* o_strides, float sm_scale, int batch, int num_heads, int num_kv_heads, int q_len,
+             int kv_len, int prefix_len, int gqa_group_size, int block_m, int block_n, int head_dim, int dtype,
+             void* workspace, size_t workspace_bytes, hipStream_t stream, const int64_t* q_strides) {
+  if (kv.paged()) return TSFA_ERR_UNSUPPORTED;
+  int cus = 0;
+  if (device_cu_count(&cus) != TSFA_OK) return TSFA_ERR_DEVICE;
+  GenPlan p;
+  int st = gen_plan(batch, num_heads, num_kv_heads, q_len, kv_len, head_dim, dtype, cus, &p);
+  if (st != TSFA_OK) return st;
+  if (workspace == nullptr || workspace_bytes < p.ws_acc_bytes + p.ws_ml_bytes ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+    return TSFA_ERR_WORKSPACE;
+  // fp32 rows are addressed as 16-byte pieces too: q/k/v/o row strides and
+  // bases are multiples of 16 bytes (check_strides asks 8 elements of 2 bytes)
+  GenArgs ga = {};
+  ga.q = q;
+  ga.k = kv.k;
+  ga.v = kv.v;
+  ga.row_ptr = row_ptr;
+  ga.col_idx = col_idx;
+  ga.blk_type = blk_type;
+  ga.payload = payload;
+  ga.offset = offset;
+  for (int i = 0; i < 5; ++i) ga.ms[i] = meta_seq_stride[i];
+  ga.sqb = q_strides[0];
+  ga.sqh = q_strides[1];
+  ga.sqm = q_strides[2];
+  ga.skb = kv.k_strides[0];
+  ga.skh = kv.k_strides[1];
+  ga.skn = kv.k_strides[2];
+  ga.svb = kv.v_strides[0];
+  ga.svh = kv.v_strides[1];
+  ga.svn = kv.v_strides[2];
+  float sl2 = fabsf(sm_scale) * 1.4426950408889634f;
+  if (sl2 == 0.f) sl2 = 1e-30f;
+  ga.scale_log2 = sl2;
+  ga.neg_q = sm_scale < 0.f ? 1 : 0;
+  ga.num_kv_heads = num_kv_heads;
+  ga.group = gqa_group_size;
+  ga.q_len = q_len;
+  ga.kv_len = kv_len;
+  ga.prefix_len = prefix_len;
+  ga.block_m = block_m;
+  ga.block_n = block_n;
+  ga.n_chunks = p.n_chunks;
+  ga.n_units = p.n_units;
+  ga.units_per_split = p.units_per_split;
+  ga.n_slots = p.n_slots;
+  ga.ws_o = static_cast<float*>(workspace);
+  ga.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
+  CombineArgs ca;
+  ca.o = o;
+  ca.lse = lse;
+  ca.sob = o_strides[0];
+  ca.soh = o_strides[1];
+  ca.som = o_strides[2];
+  ca.scale_log2 = sl2;
+  ca.batch = batch;
+  ca.num_heads = num_heads;
+  ca.num_kv_heads = num_kv_heads;
+  ca.group = gqa_group_size;
+  ca.q_len = q_len;
+  ca.n_slots = p.n_slots;
+  ca.ws_o = ga.ws_o;
+  ca.ws_ml = ga.ws_ml;
+  if (dtype == TSFA_DTYPE_FP32) {
+    if (head_dim == 64) return launch_gen<float, 64>(ga, ca, p, stream);
+    if (head_dim == 128) return launch_gen<float, 128>(ga, ca, p, stream);
+    return launch_gen<float, 256>(ga, ca, p, stream);
+  }
+  if (head_dim != 256) return TSFA_ERR_UNSUPPORTED;
+  return dtype == TSFA_DTYPE_BF16 ? launch_gen<__bf16, 256>(ga, ca, p, stream)
+                                  : launch_gen<_Float16, 256>(ga, ca, p, stream);
+}
+
 int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32_t* row_ptr, const int32_t* col_idx,
              const int8_t* blk_type, const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
              const int64_t* meta_seq_stride, const int64_t* q_strides, const int64_t* o_strides, float sm_scale,
@@ -1638,6 +2029,11 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   if (st != TSFA_OK) return st;
   for (int i = 0; i < 5; ++i)
     if (meta_seq_stride[i] < 0) return TSFA_ERR_INVALID_ARGUMENT;
+  if (gen_path(head_dim, dtype))
+    return gen_impl(q, kv, o, lse, row_ptr, col_idx, blk_type, mixed_mask_payload, mixed_mask_offset,
+                    meta_seq_stride, o_strides, sm_scale, batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
+                    gqa_group_size, block_m, block_n, head_dim, dtype, workspace, workspace_bytes,
+                    reinterpret_cast<hipStream_t>(stream_), q_strides);
 
   // one snapshot of the TSFA_* switches for the whole call
   const Config cfg = config();
@@ -1815,7 +2211,7 @@ struct TreeCallLayout {
 };
 
 int tree_call_layout(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len, int n_masks,
-                     int block_m, int block_n, int head_dim, TreeCallLayout* L) {
+                     int block_m, int block_n, int head_dim, int dtype, TreeCallLayout* L) {
   if (batch <= 0 || q_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 || kv_len < q_len ||
       (n_masks != 1 && n_masks != batch))
     return TSFA_ERR_INVALID_ARGUMENT;
@@ -1836,7 +2232,8 @@ int tree_call_layout(int batch, int num_heads, int num_kv_heads, int q_len, int 
     at += align256(std::max<size_t>(sizes[i], 1));
   }
   L->off[7] = at;
-  L->fwd_bytes = tsfa_fwd_workspace_bytes(batch, num_heads, num_kv_heads, q_len, kv_len, kv_len - q_len, head_dim);
+  L->fwd_bytes = tsfa_fwd_workspace_bytes_for_dtype(batch, num_heads, num_kv_heads, q_len, kv_len, kv_len - q_len,
+                                                    head_dim, dtype);
   if (L->fwd_bytes == 0) return TSFA_ERR_UNSUPPORTED;
   L->total = at + L->fwd_bytes;
   return TSFA_OK;
@@ -1846,10 +2243,10 @@ int tree_call_layout(int batch, int num_heads, int num_kv_heads, int q_len, int 
 
 extern "C" size_t tsfa_tree_attention_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len,
                                                       int kv_len, int n_masks, int block_m, int block_n,
-                                                      int head_dim) {
+                                                      int head_dim, int dtype) {
   TreeCallLayout L;
-  if (tree_call_layout(batch, num_heads, num_kv_heads, q_len, kv_len, n_masks, block_m, block_n, head_dim, &L) !=
-      TSFA_OK)
+  if (tree_call_layout(batch, num_heads, num_kv_heads, q_len, kv_len, n_masks, block_m, block_n, head_dim, dtype,
+                       &L) != TSFA_OK)
     return 0;
   return L.total;
 }
@@ -1862,7 +2259,8 @@ extern "C" int tsfa_tree_attention(const void* q, const void* k, const void* v, 
   if (kv_len < q_len) return TSFA_ERR_INVALID_ARGUMENT;  // eagle_tree_sparse_bridge.py:91-93
   if (batch == 0) return TSFA_OK;
   TreeCallLayout L;
-  int st = tree_call_layout(batch, num_heads, num_kv_heads, q_len, kv_len, n_masks, block_m, block_n, head_dim, &L);
+  int st = tree_call_layout(batch, num_heads, num_kv_heads, q_len, kv_len, n_masks, block_m, block_n, head_dim,
+                            dtype, &L);
   if (st != TSFA_OK) return st;
   const int prefix_len = kv_len - q_len;
   // the forward's own checks first: nothing is launched for a call it refuses
@@ -1953,7 +2351,8 @@ extern "C" int tsfa_fwd_noalloc(const void* q, const void* k, const void* v, voi
   const int st = tsfa_fwd_check_args(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks,
                                      n_tree_blocks, gqa_group_size, block_m, block_n, head_dim, dtype);
   if (st != TSFA_OK) return st;
-  if (tsfa_fwd_workspace_bytes(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim) > kNoAllocBytes)
+  if (tsfa_fwd_workspace_bytes_for_dtype(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim,
+                                         dtype) > kNoAllocBytes)
     return TSFA_ERR_WORKSPACE;
   void* ws = nullptr;
   const int sst = noalloc_scratch(reinterpret_cast<hipStream_t>(stream_), &ws);

@@ -218,8 +218,8 @@ int check_args(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len
   if ((int64_t)n_q_blocks != ((int64_t)q_len + block_m - 1) / block_m ||
       (int64_t)n_tree_blocks != ((int64_t)q_len + block_n - 1) / block_n)
     return TSFA_ERR_INVALID_ARGUMENT;
-  if (dtype != TSFA_DTYPE_FP16 && dtype != TSFA_DTYPE_BF16) return TSFA_ERR_UNSUPPORTED;
-  if (head_dim != 64 && head_dim != 128) return TSFA_ERR_UNSUPPORTED;
+  if (dtype != TSFA_DTYPE_FP16 && dtype != TSFA_DTYPE_BF16 && dtype != TSFA_DTYPE_FP32) return TSFA_ERR_UNSUPPORTED;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return TSFA_ERR_UNSUPPORTED;
   if (block_n % 16 != 0) return TSFA_ERR_UNSUPPORTED;
   const int64_t tree_limit = std::min<int64_t>((int64_t)n_tree_blocks * block_n, (int64_t)kv_len - prefix_len);
   if (tree_limit > (int64_t)kMaxTreeUnits * kUnitKeys) return TSFA_ERR_UNSUPPORTED;

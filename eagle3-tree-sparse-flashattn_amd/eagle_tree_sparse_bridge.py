@@ -196,7 +196,7 @@ def _tree_call_plan(q, k, v, mask, block_m, block_n):
         return False
     lib = _lib.load()
     ws_bytes = lib.tsfa_tree_attention_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, n_masks, block_m,
-                                                        block_n, head_dim)
+                                                        block_n, head_dim, _lib.dtype_code(q.dtype))
     if ws_bytes == 0:
         return False
     strides = _lib.i64_array((*q.stride(), *k.stride(), *v.stride(), *probe.stride()))

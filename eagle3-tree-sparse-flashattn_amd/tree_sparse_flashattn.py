@@ -293,8 +293,8 @@ def _workspace(workspace: Optional[torch.Tensor], nbytes: int, dev: torch.device
 def fwd_workspace_bytes(q: torch.Tensor, k: torch.Tensor, meta) -> int:
     """Bytes of the split-KV workspace tree_sparse_attention_fwd(q, k, v, meta) uses."""
     bsz, n_heads, q_len, head_dim = q.shape
-    return int(_lib.load().tsfa_fwd_workspace_bytes(bsz, n_heads, k.shape[1], q_len, k.shape[2], meta.prefix_len,
-                                                    head_dim))
+    return int(_lib.load().tsfa_fwd_workspace_bytes_for_dtype(bsz, n_heads, k.shape[1], q_len, k.shape[2],
+                                                              meta.prefix_len, head_dim, _lib.dtype_code(q.dtype)))
 
 
 def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_strides, strides, sm_scale,
@@ -315,8 +315,8 @@ def _launch_fwd(q, k, v, o, row_ptr, col_idx, blk_type, payload, offset, meta_st
     args = (batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len, n_q_blocks, n_tree_blocks,
             gqa_group_size, block_m, block_n, head_dim, dt)
     _lib.check("block_sparse_tree_fwd_kernel", lib.tsfa_fwd_check_args(*args))
-    ws_bytes = lib.tsfa_fwd_workspace_bytes(batch_size, num_heads, num_kv_heads, q_len, kv_len, prefix_len,
-                                            head_dim)
+    ws_bytes = lib.tsfa_fwd_workspace_bytes_for_dtype(batch_size, num_heads, num_kv_heads, q_len, kv_len,
+                                                      prefix_len, head_dim, dt)
     ws = _workspace(workspace, ws_bytes, dev)
     with torch.cuda.device(dev):
         if lse is None:
@@ -414,7 +414,7 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: Optional[torch.Tensor], **sa
 
 
 # head_dim widths the kernels are built for; narrower dims are zero-padded
-_KERNEL_DIMS = (64, 128)
+_KERNEL_DIMS = (64, 128, 256)
 
 
 def _padded_dim(d: int) -> int:
@@ -522,7 +522,8 @@ def tree_sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             _lib.i64_array(meta_strides), _lib.i64_array(strides),
             (bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks,
              n_heads // n_kv_heads, meta.block_m, meta.block_n, head_dim, _lib.dtype_code(q.dtype)),
-            lib.tsfa_fwd_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, head_dim),
+            lib.tsfa_fwd_workspace_bytes_for_dtype(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len,
+                                                   head_dim, _lib.dtype_code(q.dtype)),
             1.0 / math.sqrt(head_dim))
     return (out, lse) if return_lse else out
 
@@ -749,7 +750,8 @@ def tree_sparse_attention_fwd_paged(q: torch.Tensor, kv_cache: torch.Tensor, kv_
     args = (bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, meta.n_q_blocks, meta.n_tree_blocks,
             n_heads // n_kv_heads, meta.block_m, meta.block_n, head_dim, dt)
     _lib.check("tree_sparse_attention_fwd_paged", lib.tsfa_fwd_check_args(*args))
-    ws_bytes = lib.tsfa_fwd_workspace_bytes(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len, head_dim)
+    ws_bytes = lib.tsfa_fwd_workspace_bytes_for_dtype(bsz, n_heads, n_kv_heads, q_len, kv_len, meta.prefix_len,
+                                                      head_dim, dt)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     lse = torch.empty((bsz, n_heads, q_len), dtype=torch.float32, device=dev) if return_lse else None
     with torch.cuda.device(dev):

@@ -25,6 +25,7 @@ TSFA_ERR_DEVICE = 5
 
 TSFA_DTYPE_FP16 = 0
 TSFA_DTYPE_BF16 = 1
+TSFA_DTYPE_FP32 = 2
 
 EXPORTS = (
     "tsfa_version",
@@ -41,6 +42,7 @@ EXPORTS = (
     "tsfa_device_limits",
     "tsfa_fwd_check_args",
     "tsfa_fwd_workspace_bytes",
+    "tsfa_fwd_workspace_bytes_for_dtype",
     "tsfa_fwd",
     "tsfa_fwd_lse",
     "tsfa_fwd_noalloc",
@@ -72,6 +74,7 @@ _SIGNATURES = {
     "tsfa_device_limits": (_c_int, [ctypes.POINTER(ctypes.c_int32)]),
     "tsfa_fwd_check_args": (_c_int, [_c_int] * 13),
     "tsfa_fwd_workspace_bytes": (_c_size, [_c_int] * 7),
+    "tsfa_fwd_workspace_bytes_for_dtype": (_c_size, [_c_int] * 8),
     "tsfa_fwd": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                           ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
@@ -81,7 +84,7 @@ _SIGNATURES = {
                          + [_c_int] * 13 + [_c_vp]),
     "tsfa_tree_attention": (_c_int, [_c_vp] * 5 + [_c_i64, _c_i64, _c_int, ctypes.POINTER(_c_i64), _c_float]
                             + [_c_int] * 9 + [_c_vp, _c_size, _c_vp]),
-    "tsfa_tree_attention_workspace_bytes": (_c_size, [_c_int] * 9),
+    "tsfa_tree_attention_workspace_bytes": (_c_size, [_c_int] * 10),
     "tsfa_bwd_workspace_bytes": (_c_size, [_c_int] * 10),
     "tsfa_bwd": (_c_int, [_c_vp] * 14 + [ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_float]
                  + [_c_int] * 13 + [_c_vp, _c_size, _c_vp]),
@@ -162,7 +165,9 @@ def dtype_code(dtype: torch.dtype) -> int:
         return TSFA_DTYPE_FP16
     if dtype == torch.bfloat16:
         return TSFA_DTYPE_BF16
-    raise NotImplementedError(f"dtype {dtype} is not supported by the HIP kernels (fp16/bf16 only)")
+    if dtype == torch.float32:
+        return TSFA_DTYPE_FP32
+    raise NotImplementedError(f"dtype {dtype} is not supported by the HIP kernels (fp16/bf16/fp32)")
 
 
 def fwd_plan(batch, num_heads, num_kv_heads, q_len, kv_len, prefix_len, head_dim) -> dict:

@@ -40,7 +40,7 @@ enum tsfa_status {
   TSFA_ERR_DEVICE = 5            /* no usable HIP device / attribute query failed */
 };
 
-enum tsfa_dtype { TSFA_DTYPE_FP16 = 0, TSFA_DTYPE_BF16 = 1 };
+enum tsfa_dtype { TSFA_DTYPE_FP16 = 0, TSFA_DTYPE_BF16 = 1, TSFA_DTYPE_FP32 = 2 };
 
 /* Block codes of blk_type (tree_sparse_flashattn.py:11-12). ZERO blocks are absent. */
 enum { TSFA_FULL_BLOCK = 0, TSFA_MIXED_BLOCK = 1 };
@@ -113,16 +113,25 @@ int tsfa_pack_bits_host(const uint8_t* bits, int64_t n_bits, int32_t* words);
  *           non-zero = one tree per sequence (tsfa_meta_build's layout)
  * o is written in `dtype` (one rounding of the fp32 result; the reference
  * stores through float16, tree_sparse_flashattn.py:339).
- * Supported: dtype fp16/bf16, head_dim 64 or 128, block_n a positive
- * multiple of 16, block_m >= 1, num_heads % num_kv_heads == 0 with
- * gqa_group_size == num_heads / num_kv_heads <= 256, q_len >= 1,
- * kv_len >= prefix_len >= 0, 16-byte aligned q/k/v/o rows.
+ * Supported: dtype fp16/bf16 with head_dim 64, 128 or 256, fp32 with head_dim
+ * 64, 128 or 256 (the reference's tl.dot takes fp32, tree_sparse_flashattn.py:
+ * 269, :278); block_n a positive multiple of 16, block_m >= 1, num_heads %
+ * num_kv_heads == 0 with gqa_group_size == num_heads / num_kv_heads <= 256,
+ * q_len >= 1, kv_len >= prefix_len >= 0, 16-byte aligned q/k/v/o rows.
+ * head_dim 256 and fp32 run a simpler kernel with fp32 split-KV partials
+ * (contiguous K/V only: tsfa_fwd_paged and tsfa_bwd refuse them with
+ * TSFA_ERR_UNSUPPORTED); size their workspace with
+ * tsfa_fwd_workspace_bytes_for_dtype.
  */
 int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                         int prefix_len, int n_q_blocks, int n_tree_blocks, int gqa_group_size,
                         int block_m, int block_n, int head_dim, int dtype);
 size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                 int prefix_len, int head_dim);
+/* tsfa_fwd_workspace_bytes for inputs of `dtype` (tsfa_fwd_workspace_bytes
+ * sizes 16-bit inputs; fp32 partials need more).  No reference counterpart. */
+size_t tsfa_fwd_workspace_bytes_for_dtype(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
+                                          int prefix_len, int head_dim, int dtype);
 int tsfa_fwd(const void* q, const void* k, const void* v, void* o,
              const int32_t* row_ptr, const int32_t* col_idx, const int8_t* blk_type,
              const int32_t* mixed_mask_payload, const int32_t* mixed_mask_offset,
@@ -236,7 +245,7 @@ int tsfa_fwd_paged(const void* q, const void* kv_cache, const int32_t* kv_indptr
  * TSFA_ERR_INVALID_ARGUMENT (the reference's ValueError).  The forward's
  * checks run before anything is launched. */
 size_t tsfa_tree_attention_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
-                                           int n_masks, int block_m, int block_n, int head_dim);
+                                           int n_masks, int block_m, int block_n, int head_dim, int dtype);
 int tsfa_tree_attention(const void* q, const void* k, const void* v, void* o, const uint8_t* mask,
                         int64_t mask_seq_stride, int64_t mask_row_stride, int n_masks,
                         const int64_t* strides, float sm_scale, int batch, int num_heads,

@@ -9,7 +9,11 @@ from oracle import meta_oracle as mo
 from oracle.attn_oracle import dense_mask_attention
 
 # max_abs_err bars against the fp32 oracle (the named workloads use these alone).
-TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3}
+TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3, torch.float32: 1e-4}
+# fp32 inputs (fp32 MFMA, P not rounded): the north_star bars cover 16-bit
+# inputs only; fp32 is held to 1e-4, well inside what the reference's fp32
+# tl.dot (TF32 by default on its own hardware, tree_sparse_flashattn.py:269)
+# could meet.
 # Edge cases with few visible keys have |O| up to ~4, where rounding O once to
 # the output dtype already costs up to half an ulp of O: 2^-7 = 7.8e-3 at |O|
 # in [2, 4) for bf16, so no bf16-output kernel can meet 8e-3 absolute there
@@ -25,7 +29,7 @@ TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3}
 # 1.34e-2 off with one slot (0.69 half-ulps beyond TOL) and 1.37e-2 with two
 # (0.72 to 1.05).  Every such comparison prints its max_abs_err and how many
 # half-ulps of |got| it used beyond TOL.
-MANT = {torch.bfloat16: 8, torch.float16: 11}
+MANT = {torch.bfloat16: 8, torch.float16: 11, torch.float32: 24}
 
 
 def storage_roundings(q, k, prefix_len) -> int:
@@ -35,6 +39,8 @@ def storage_roundings(q, k, prefix_len) -> int:
     from tsfa import _lib
 
     b, hq, t, d = q.shape
+    if d > 128 or q.dtype == torch.float32:
+        return 1  # the generic kernel: fp32 partials, O rounded once
     width = 64 if d <= 64 else 128  # narrower head dims run zero-padded
     plan = _lib.fwd_plan(b, hq, k.shape[1], t, k.shape[2], prefix_len, width)
     return 1 if plan["slots"] == 1 else 2

@@ -156,5 +156,5 @@ def test_tree_attention_rejects_on_the_host():
     st = lib.tsfa_tree_attention(None, None, None, None, None, 0, 40, 1, strides, ctypes.c_float(0.1),
                                  *args.values(), None, 0, None)
     assert st == _lib.TSFA_ERR_INVALID_ARGUMENT
-    assert lib.tsfa_tree_attention_workspace_bytes(1, 8, 2, 40, 30, 1, 16, 32, 128) == 0
-    assert lib.tsfa_tree_attention_workspace_bytes(2, 8, 2, 40, 100, 3, 16, 32, 128) == 0  # n_masks not 1 or B
+    assert lib.tsfa_tree_attention_workspace_bytes(1, 8, 2, 40, 30, 1, 16, 32, 128, 1) == 0
+    assert lib.tsfa_tree_attention_workspace_bytes(2, 8, 2, 40, 100, 3, 16, 32, 128, 1) == 0  # n_masks not 1 or B

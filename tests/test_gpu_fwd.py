@@ -362,7 +362,7 @@ def test_head_dims_below_a_kernel_width(d):
 
 
 def test_head_dim_above_the_widest_kernel_raises():
-    q, k, v = (x.cuda() for x in _qkv(1, 2, 2, 8, 8, 256, torch.bfloat16))
+    q, k, v = (x.cuda() for x in _qkv(1, 2, 2, 8, 8, 512, torch.bfloat16))
     with pytest.raises(NotImplementedError):
         _run(q, k, v, torch.eye(8, dtype=torch.bool), 16, 16)
 
@@ -377,7 +377,7 @@ def test_repeat_calls_are_deterministic():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32])
+@pytest.mark.parametrize("dtype", [torch.float64])
 def test_unsupported_dtype_raises(dtype):
     q, k, v = _qkv(1, 2, 2, 8, 8, 64, dtype)
     with pytest.raises(NotImplementedError):
