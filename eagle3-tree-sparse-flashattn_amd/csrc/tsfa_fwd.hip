@@ -747,17 +747,32 @@ void split_kernel(const SplitArgs a) {
     return need;
   };
   // Unit j of the stream (u: its index in the run; s_in: its S^T; s_out:
-  // S^T of unit j+1 when NEXT): mask and statistics, group 1 when NEXT (the
-  // S^T MFMAs of unit j+1 with the exponentials and rounded P of unit j
-  // between them), the O re-base, group 2 (O^T += V^T P^T of unit j, V^T read
-  // two MFMAs ahead, the row sum between them).
+  // S^T of unit j+1 when NEXT): the first KA K fragments of unit j+1
+  // requested, mask and statistics, group 1 when NEXT (the S^T MFMAs of unit
+  // j+1 with the exponentials and rounded P of unit j between them), the O
+  // re-base, group 2 (O^T += V^T P^T of unit j, V^T read VA MFMAs ahead, the
+  // row sum between them).  Requesting K at the top, fenced so the compiler
+  // cannot sink it behind the statistics, lets the first S^T MFMA wait for
+  // one LDS read instead of the scheduler's last-moment two (and VA = 4
+  // instead of 2 the same for group 2): 1 % at the 8B decode shape and the
+  // 1024-token tree, same-box A/B.
   auto pipe_iter = [&](int j, int u, auto next_c, f32x16& s_in, f32x16& s_out, auto masked_of, auto mask_of) {
     constexpr bool NEXT = decltype(next_c)::value;
     constexpr int NPV = 2 * DT;  // P V MFMAs
     i16x4 vh[DT][2][2];
     float p[16];
     V8 pb[2];
+    constexpr int KA = KSTEPS < 4 ? KSTEPS : 4;  // K fragments requested before the statistics
+    constexpr int VA = NPV < 4 ? NPV : 4;        // P V MFMAs whose V^T is read ahead
     const uint32_t vb = stage(j) + (uint32_t)(HALF + v_off0);
+    i16x8 kf[KSTEPS];
+    const uint32_t kb = stage(j + 1) + (uint32_t)k_off0;
+    auto rk = [&](int kk) { return lds_ld<i16x8>(kb ^ (uint32_t)(kk << 5)); };
+    if constexpr (NEXT) {
+#pragma unroll
+      for (int kk = 0; kk < KA; ++kk) kf[kk] = rk(kk);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     auto rv = [&](int idx) {  // V^T fragment idx = (dt, s2, jj); P V MFMA g reads 2g and 2g+1
       const int dt = idx >> 2, s2 = (idx >> 1) & 1, jj = idx & 1;
       vh[dt][s2][jj] = lds_tr((vb ^ (uint32_t)(dt << 6)) + (uint32_t)((16 * s2 + 8 * jj) * ROWB));
@@ -788,29 +803,24 @@ void split_kernel(const SplitArgs a) {
     };
     constexpr int NG1 = 4;  // exponential pairs in group 1 (keys 0-15)
     if constexpr (NEXT) {
-      // group 1 in explicit order: K of unit j+1 read two k-steps ahead of
+      // group 1 in explicit order: K of unit j+1 read KA k-steps ahead of
       // its MFMAs; the statistics above and then the exponentials and
-      // rounded P of unit j between the MFMAs; V^T of the first two P V
+      // rounded P of unit j between the MFMAs; V^T of the first VA P V
       // MFMAs at the end
-      const uint32_t kb = stage(j + 1) + (uint32_t)k_off0;
-      auto rk = [&](int kk) { return lds_ld<i16x8>(kb ^ (uint32_t)(kk << 5)); };
-      i16x8 kf[KSTEPS];
-      kf[0] = rk(0);
-      kf[1] = rk(1);
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_out[i] = 0.f;
       constexpr int K0 = KSTEPS / 4;  // steps that carry the statistics; the exponential pairs spread over the rest
 #pragma unroll
       for (int kk = 0; kk < KSTEPS; ++kk) {
-        if (kk + 2 < KSTEPS) kf[kk + 2] = rk(kk + 2);
+        if (kk + KA < KSTEPS) kf[kk + KA] = rk(kk + KA);
         s_out = Mma<T>::run(bit_cast<V8>(kf[kk]), bit_cast<V8>(qf[kk]), s_out);
         if (kk >= K0) {
 #pragma unroll
           for (int pr = (kk - K0) * NG1 / (KSTEPS - K0); pr < (kk - K0 + 1) * NG1 / (KSTEPS - K0); ++pr) expo2(2 * pr);
         }
         if (kk == KSTEPS - 1) {
-          rv2(0);
-          rv2(1);
+#pragma unroll
+          for (int g = 0; g < VA; ++g) rv2(g);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -820,8 +830,8 @@ void split_kernel(const SplitArgs a) {
       asm volatile("" : "+v"(pb[0]));
       TSFA_CYC(0);
     } else {
-      rv2(0);
-      rv2(1);
+#pragma unroll
+      for (int g = 0; g < VA; ++g) rv2(g);
 #pragma unroll
       for (int pr = 0; pr < NG1; ++pr) expo2(2 * pr);
     }
@@ -832,12 +842,12 @@ void split_kernel(const SplitArgs a) {
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
     if constexpr (NEXT) TSFA_CYC(3);
-    // group 2 in explicit order: MFMA g with V^T of MFMA g+2 read behind it,
+    // group 2 in explicit order: MFMA g with V^T of MFMA g+VA read behind it,
     // the remaining exponentials under the k-step-0 MFMAs and the row sum
     // of unit j under the k-step-1 MFMAs
 #pragma unroll
     for (int g = 0; g < NPV; ++g) {
-      if (g + 2 < NPV) rv2(g + 2);
+      if (g + VA < NPV) rv2(g + VA);
       const int dt = pv_dt(g), s2 = pv_s2(g);
       const i16x8 vf = __builtin_shufflevector(vh[dt][s2][0], vh[dt][s2][1], 0, 1, 2, 3, 4, 5, 6, 7);
       o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
@@ -979,6 +989,8 @@ void split_kernel(const SplitArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             sync_lds();
             __builtin_amdgcn_sched_barrier(0);
+            if (j0 + h < 32) TSFA_STAMP(3 + j0 + h);
+            TSFA_CYC(2);
             fast_c.next(mine);  // unit j0 + h + NS - 1 of the stream
             __builtin_amdgcn_sched_barrier(0);
             pipe_iter(j0 + h, ks + S * (j0 + h), std::true_type{}, s_cur, s_next, masked_of, mask_of);
@@ -1089,6 +1101,7 @@ void split_kernel(const SplitArgs a) {
     // reuse the ring), Q already in registers
     if (is_tree) load_q();
     else sync_all();
+    TSFA_STAMP(43);
     const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
     const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
     const int ntok = tok_hi - tok_lo + 1;
@@ -1116,6 +1129,7 @@ void split_kernel(const SplitArgs a) {
       sync_lds();
     };
     build_state();
+    TSFA_STAMP(44);
     // Tree units holding a key some row of the chunk can see, compacted.
     const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
     for (int i = tid; i < n_tu; i += kWaves * 64) vis[i] = 0;
@@ -1141,6 +1155,7 @@ void split_kernel(const SplitArgs a) {
       if (lane == 0) misc[0] = nv;
     }
     sync_lds();
+    TSFA_STAMP(45);
     const int n_vis = misc[0];
     for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
       const int nb = min(a.vt_max, n_vis - vb0);
@@ -1169,11 +1184,13 @@ void split_kernel(const SplitArgs a) {
         reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
       }
       sync_lds();
+      TSFA_STAMP(46);
       auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
       units(
           nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
           [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{});
       sync_all();  // ring and masks free for the next batch
+      TSFA_STAMP(47);
     }
   }
 
