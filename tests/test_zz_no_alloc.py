@@ -62,6 +62,27 @@ def test_noalloc_matches_tsfa_fwd_on_two_calls():
             f"{label}: max diff {float((out.float() - ref.float()).nan_to_num(0).abs().max()):.3e}"
 
 
+def test_noalloc_matches_tsfa_fwd_on_the_generic_kernel():
+    # head_dim 256 and fp32 run the generic kernel with fp32 partials, whose
+    # size the entry point checks against its array by dtype
+    g = torch.Generator().manual_seed(11)
+    for dtype, head_dim in ((torch.float32, 128), (torch.bfloat16, 256), (torch.float32, 64)):
+        q = torch.randn(2, 8, 29, head_dim, generator=g).to(dtype).cuda()
+        k = torch.randn(2, 4, 29 + 300, head_dim, generator=g).to(dtype).cuda()
+        v = torch.randn(2, 4, 29 + 300, head_dim, generator=g).to(dtype).cuda()
+        mask = torch.tril(torch.ones(29, 29, dtype=torch.bool))
+        mask[7, :7] = False
+        meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), 300, 16, 16)
+        print(f"[noalloc] generic {dtype} head_dim {head_dim}", flush=True)
+        assert tsf.fwd_workspace_bytes(q, k, meta) <= NOALLOC_MAX_BYTES
+        ref = tsf.tree_sparse_attention_fwd(q, k, v, meta)
+        out = torch.full_like(q, float("nan"))
+        _lib.check("tsfa_fwd_noalloc", _noalloc(q, k, v, meta, out))
+        torch.cuda.synchronize()
+        assert torch.equal(out.isnan(), ref.isnan())
+        assert torch.equal(out.nan_to_num(0.0), ref.nan_to_num(0.0)), f"{dtype} {head_dim}"
+
+
 def test_noalloc_refuses_calls_past_its_array():
     # the 70B layout at 32 sequences: its partials (at least one slot of
     # 32*64*256 rows) exceed the array, so the call is refused on the host
