@@ -74,6 +74,7 @@ for _p in (ROOT, PKG):
 
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense bf16 / fp16
+MFMA_PEAK_TFLOPS_FP32 = 157.3  # dense fp32 MFMA
 RIDGE_FLOP_PER_BYTE = MFMA_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBPS * 1e9)
 METRIC = "tree-attn fwd µs + achieved HBM TB/s, 8B shape, 4k prefix, 64-node tree"
 
@@ -283,11 +284,24 @@ def eager_call_timing(w, qd, ks, vs, mask_dev, meta, reps: int = 100, batches: i
 
 
 def workload_by_name(name: str):
-    """A named workload, or `name@BMxBN`: the same workload at other block sizes."""
+    """A named workload; `name@BMxBN`: the same workload at other block sizes;
+    `name+d256` / `name+fp32`: at another head_dim / in fp32 (the generic
+    kernel's shapes)."""
+    import dataclasses
+
+    import torch
     from tsfa import configs
 
     base, _, blocks = name.partition("@")
+    base, *mods = base.split("+")
     w = configs.WORKLOADS[base]
+    for m in mods:
+        if m.startswith("d") and m[1:].isdigit():
+            w = dataclasses.replace(w, head_dim=int(m[1:]), name=f"{w.name}+{m}")
+        elif m == "fp32":
+            w = dataclasses.replace(w, dtype=torch.float32, name=f"{w.name}+{m}")
+        else:
+            raise SystemExit(f"unknown workload modifier +{m} in {name}")
     if blocks:
         bm, bn = (int(x) for x in blocks.lower().split("x"))
         w = w.with_blocks(bm, bn)
@@ -319,7 +333,12 @@ def workload_timing(name: str, steps: int, cold_mib: int, cpu_seconds: float = 0
     meta = build(mask.to(dev), w.prefix_len, w.block_m, w.block_n)
     out = torch.empty_like(qd)
     lib = _lib.load()
-    plan = _lib.fwd_plan(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len, w.head_dim)
+    # head_dim above 128 and fp32 run the generic kernel (its own plan, one
+    # region: the split-plan report and the combine-only hook are the split
+    # kernel's)
+    generic = w.head_dim > 128 or w.dtype == torch.float32
+    plan = ({"kernel": "gen_kernel + combine_kernel"} if generic else
+            _lib.fwd_plan(w.batch, w.q_heads, w.kv_heads, w.tree_len, w.kv_len, w.prefix_len, w.head_dim))
 
     def call(i):
         tsf.tree_sparse_attention_fwd(qd, ks[i % copies], vs[i % copies], meta, out=out)
@@ -328,7 +347,7 @@ def workload_timing(name: str, steps: int, cold_mib: int, cpu_seconds: float = 0
         call(i)
     torch.cuda.synchronize()
     secs = {"combine": 0.0}
-    regions = (("full", 3), ("combine", 2)) if plan["slots"] > 1 else (("full", 3),)
+    regions = (("full", 3), ("combine", 2)) if not generic and plan["slots"] > 1 else (("full", 3),)
     for region, kmask in regions:
         g = torch.cuda.CUDAGraph()
         s = torch.cuda.Stream()
@@ -362,17 +381,20 @@ def workload_timing(name: str, steps: int, cold_mib: int, cpu_seconds: float = 0
         del g
     split_s = secs["full"] - secs["combine"]
     flops = algorithmic_flops(w, mask)
-    mfma_bound = flops / kvb > RIDGE_FLOP_PER_BYTE
+    peak_tflops = MFMA_PEAK_TFLOPS_FP32 if w.dtype == torch.float32 else MFMA_PEAK_TFLOPS
+    mfma_bound = flops / kvb > peak_tflops * 1e12 / (HBM_PEAK_GBPS * 1e9)
     tflops, gbps = flops / split_s / 1e12, kvb / split_s / 1e9
     del ks, vs
     torch.cuda.empty_cache()
     res = {"us_per_call": round(secs["full"] * 1e6, 2), "split_kernel_us": round(split_s * 1e6, 2),
            "combine_kernel_us": round(secs["combine"] * 1e6, 2), "bound": "mfma" if mfma_bound else "hbm",
-           "frac": round(tflops / MFMA_PEAK_TFLOPS if mfma_bound else gbps / HBM_PEAK_GBPS, 4),
+           "frac": round(tflops / peak_tflops if mfma_bound else gbps / HBM_PEAK_GBPS, 4),
            "achieved": round(tflops, 1) if mfma_bound else round(gbps, 1),
            "unit": "TFLOP/s" if mfma_bound else "GB/s", "algorithmic_flops": flops, "algorithmic_bytes": kvb,
            "block_m": w.block_m, "block_n": w.block_n, "steps": steps, "kv_copies_cycled": copies, "plan": plan,
            "tokens_per_s": round(w.batch * w.tree_len / secs["full"], 1), "cpu_baseline": None}
+    if generic:
+        res["note"] = "generic kernel: gen_kernel and its combine timed as one region (split_kernel_us is both)"
     if cpu_seconds > 0:
         cache = {} if cpu_cache is None else cpu_cache
         if base not in cache:

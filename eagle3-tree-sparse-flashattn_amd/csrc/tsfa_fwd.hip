@@ -1551,13 +1551,25 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
 // Head dims above 128 (bf16 / fp16) and fp32 inputs.  The same semantics as
 // split_kernel (tree_sparse_flashattn.py:211-339) with a simpler structure:
 // a workgroup is 4 waves of 32 packed query rows (a 128-row chunk, r = t*G +
-// g) over one split of the key axis in units of 32 keys; each unit's K and V
-// go through LDS, prefix keys are visible, tree keys by the CSR record of the
-// row's q-block (FULL, or the MIXED bit).  S^T = K Q^T and O^T += V^T P^T on
+// g) over one split of the key axis in units of 32 keys; prefix keys are
+// visible, tree keys by the CSR record of the row's q-block (FULL, or the
+// MIXED bit).  S^T = K Q^T and O^T += V^T P^T on
 // v_mfma_f32_32x32x16_{bf16,f16} (V^T from ds_read_b64_tr_b16) or
 // v_mfma_f32_32x32x2_f32, with the key order of the P V product permuted so
 // that P^T comes straight from the S^T accumulator.  Every split writes an
 // fp32 partial (O / l and (m, l)) that combine_kernel merges.
+// Units stream HBM -> LDS through a ring of kGenStages(stage bytes) stages
+// (global_load_lds, NSTG - 1 units ahead).  In the 16-bit instances 16-byte
+// chunk c of key row k sits at chunk position c ^ (k & 15) in the K tile and
+// c ^ ((k & 3) << 2) in the V tile, so the 16 key rows of a K operand read
+// and the 4 rows x 4 chunks of a transposing V^T read spread over the LDS
+// banks (a 512-byte row stride maps every row to the same banks; XOR with
+// k & 15 on V only permutes chunks inside their group of 4, which measured
+// bank conflicts on half of the LDS cycles).  The fp32 instances keep
+// rows unswizzled: their 4-byte operand reads then use immediate offsets
+// (with the XOR, one address register per read spills the head_dim 256
+// instance), and their 32x32x2 MFMAs, at 1/16 of the 16-bit rate, bound
+// the loop anyway.
 struct GenArgs {
   const void* q;
   const void* k;
@@ -1577,28 +1589,58 @@ struct GenArgs {
   float2* ws_ml;   // [B*Hkv][n_slots][q_len*G] (m, l)
 };
 
-constexpr int kGenWaves = 4;
-constexpr int kGenRows = 32 * kGenWaves;
+// 128-row chunks: 4 row groups of 32.  The 16-bit instances (head_dim 256)
+// run 8 waves, waves w and w + 4 sharing row group w % 4 and each owning
+// half of O's columns: both compute the group's S^T and softmax (1.5x the
+// MFMAs of one wave per group), but a wave then holds 64 O accumulators
+// instead of 128 and everything fits the 256 VGPRs, two waves per SIMD
+// (with 128 accumulators, Q and the temporaries the compiler parked O in
+// AGPRs and copied all of it to VGPRs on every unit).  fp32 keeps 4 waves.
+constexpr int kGenRows = 128;
+template <typename T> constexpr int gen_waves() { return sizeof(T) == 2 ? 8 : 4; }
+// Tree units per split whose visibility words the prologue builds into LDS
+// (kGenTreeUnits x 128 rows x 4 bytes after the ring).  Splits with more take
+// the gen_kernel<..., TW = false> instance, which builds each unit's words in
+// the loop: its global loads then make the compiler wait for every vector
+// load in flight (vmcnt(0), which counts the ring's DMA) on every unit, so
+// the ring drains each step.
+constexpr int kGenTreeUnits = 32;
+constexpr size_t kGenTreeBytes = (size_t)kGenTreeUnits * kGenRows * 4;
+// Ring stages for a stage of K+V bytes: as many as fit 128 KB, at least 2,
+// at most 4 (head_dim 256 and fp32 head_dim 128 hold one workgroup per CU by
+// their registers; fp32 head_dim 64 fits two at 64 KB each).
+constexpr int kGenStages(int stage_bytes) {
+  return 131072 / stage_bytes < 2 ? 2 : (131072 / stage_bytes > 4 ? 4 : 131072 / stage_bytes);
+}
 
-template <typename T, int D>
-__global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
+template <typename T, int D, bool TW>
+__global__ __launch_bounds__(gen_waves<T>() * 64) void gen_kernel(const GenArgs a) {
   constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int NW = gen_waves<T>();  // waves
+  constexpr int DS = NW / 4;          // column parts of O (waves per row group)
   constexpr int ROWB = D * (int)sizeof(T);  // bytes of one key row
+  constexpr int CPR = ROWB / 16;            // 16-byte chunks per row
   constexpr int TILE = 32 * ROWB;           // bytes of one unit's K (or V)
-  constexpr int DT = D / 32;
+  constexpr int SB = 2 * TILE;              // ring stage: K then V
+  constexpr int NSTG = kGenStages(SB);
+  constexpr int LPW = SB / 1024 / NW;  // 1 KB loads per wave per unit
+  constexpr int DT = D / 32 / DS;      // O d-tiles of a wave
   constexpr int KS = F32 ? D / 2 : D / 16;  // k-steps of S^T
+  // chunk c of row k at c ^ (k & SWZ) in K, c ^ ((k & SWV) << 2) in V
+  constexpr int SWZ = F32 ? 0 : 15, SWV = F32 ? 0 : 3;
+  static_assert(CPR >= 16 && LPW >= 1 && LPW * (NSTG - 2) < 64 && SB % (1024 * NW) == 0, "generic ring");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  unsigned char* kt = smem;
-  unsigned char* vt = smem + TILE;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, lh = lane >> 5;
+  const int rg = wave % 4, dh = wave / 4;  // row group; O columns [dh * D/DS, (dh+1) * D/DS)
   const int chunk = blockIdx.x % a.n_chunks;
   const int rest = blockIdx.x / a.n_chunks;
   const int slot = rest % a.n_slots, bk = rest / a.n_slots;
   const int b = bk / a.num_kv_heads, kvh = bk % a.num_kv_heads;
   const int G = a.group, TG = a.q_len * G;
-  const int r = chunk * kGenRows + wave * 32 + ln;  // the lane's packed row
+  const int r = chunk * kGenRows + rg * 32 + ln;  // the lane's packed row
   const bool row_ok = r < TG;
   const int R = min(r, TG - 1);
   const int t = R / G, g = R - t * G;
@@ -1609,13 +1651,16 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
   const T* qrow = static_cast<const T*>(a.q) + b * a.sqb + (int64_t)(kvh * G + g) * a.sqh + (int64_t)t * a.sqm;
 
   // Q^T operand: 16-bit, lane (ln, lh) holds d = 16kk + 8lh + [0, 8) of its
-  // row; fp32, d = 2kk + lh.  Q is negated for a negative scale.
+  // row; fp32, d = 2kk + lh (16-byte loads, the lane keeps its two words of
+  // each).  Q is negated for a negative scale.
   typedef typename std::conditional<F32, float, i16x8>::type QF;
   QF qf[KS];
 #pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
+  for (int kk = 0; kk < KS; kk += (F32 ? 2 : 1)) {
     if constexpr (F32) {
-      qf[kk] = a.neg_q ? -qrow[2 * kk + lh] : qrow[2 * kk + lh];
+      const f32x4 x = *reinterpret_cast<const f32x4*>(qrow + 2 * kk);
+      qf[kk] = a.neg_q ? -(lh ? x[1] : x[0]) : (lh ? x[1] : x[0]);
+      qf[kk + 1] = a.neg_q ? -(lh ? x[3] : x[2]) : (lh ? x[3] : x[2]);
     } else {
       qf[kk] = *reinterpret_cast<const i16x8*>(qrow + 16 * kk + 8 * lh) ^ (short)(a.neg_q ? 0x8000 : 0);
     }
@@ -1644,70 +1689,149 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
         if (lo >= hi) continue;
         const bool full = bt[e] == TSFA_FULL_BLOCK;
         const int off = full ? 0 : of[e];
-        for (int c = lo; c < hi; ++c) {
-          const int flat = tl * BN + (c - cb);
-          const uint32_t bit = full ? 1u : (((uint32_t)pl[off + (flat >> 5)] >> (flat & 31)) & 1u);
-          w |= bit << (c + P - k0);
+        // columns lo .. hi-1 are flat bits f0 .. f1-1 of the block's row-major
+        // bitset: one payload word per run of bits inside a word
+        const int f0 = tl * BN + (lo - cb), f1 = tl * BN + (hi - cb);
+        for (int f = f0; f < f1;) {
+          const int b0 = f & 31, nb = min(32 - b0, f1 - f);
+          const uint32_t word = full ? 0xffffffffu : (uint32_t)pl[off + (f >> 5)];
+          const uint32_t bits = (word >> b0) & (nb == 32 ? 0xffffffffu : ((1u << nb) - 1u));
+          w |= bits << (cb + (f - tl * BN) + P - k0);
+          f += nb;
         }
       }
     }
     return w;
   };
 
+  // The wave's DMA share of a unit: the first NW/2 waves move the K tile,
+  // the others the V tile (LPW loads of 1 KB each, NW/2 * LPW KB = one
+  // tile).  Load i of wave w moves tile chunks x = ((w % (NW/2))*LPW + i)*64
+  // + lane, landing at tile + 16x: key row x / CPR, chunk position x % CPR,
+  // which holds the row's chunk (x % CPR) ^ (row & SWZ) (K) or
+  // (x % CPR) ^ ((row & SWV) << 2) (V).  Rows past kv_len repeat the last
+  // key (never visible).
+  constexpr int HW = NW / 2;
+  static_assert(HW * LPW * 1024 == TILE, "one tile per half of the waves");
+  const bool dma_v = wave >= HW;
+  const T* dbase = dma_v ? vbase : kbase;
+  const int64_t dstride = dma_v ? a.svn : a.skn;
+  const uint32_t ring = lds_addr(smem);
+  const int u_lo = slot * a.units_per_split;
+  const int n = min(a.units_per_split, a.n_units - u_lo);
+  auto issue = [&](int j) {  // run unit j into stage j % NSTG
+    const int k0 = (u_lo + j) * 32;
+    const uint32_t st = ring + (uint32_t)((j % NSTG) * SB + (dma_v ? TILE : 0) + (wave % HW) * LPW * 1024);
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int x = ((wave % HW) * LPW + i) * 64 + lane;
+      const int row = x / CPR;
+      const int col = ((x % CPR) ^ (dma_v ? (row & SWV) << 2 : (row & SWZ))) * (16 / (int)sizeof(T));
+      const int64_t key = min(k0 + row, a.kv_len - 1);
+      dma16(dbase + key * dstride + col, st + (uint32_t)i * 1024u);
+    }
+  };
+  // LDS byte offset of chunk c (16 B) of key row k within the K / V tile
+  auto swz = [](int k, int c) { return k * ROWB + ((c ^ (k & SWZ)) << 4); };
+  auto swv = [](int k, int c) { return k * ROWB + ((c ^ ((k & SWV) << 2)) << 4); };
+
   f32x16 o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = -INFINITY, m_lim = -INFINITY, l_run = 0.f;
+  const float thr_raw = kRescaleLog2 / sl2;  // re-base past 2^8 growth
 
-  const int u_lo = slot * a.units_per_split;
-  const int u_hi = min(u_lo + a.units_per_split, a.n_units);
-  for (int u = u_lo; u < u_hi; ++u) {
-    const int k0 = u * 32;
-    // K and V of the unit into LDS (rows past kv_len repeat the last key;
-    // those keys are not visible)
-    __syncthreads();
-    for (int c = tid; c < 2 * TILE / 16; c += kGenWaves * 64) {
-      const int half = c / (TILE / 16), cc = c % (TILE / 16);
-      const int row = cc / (ROWB / 16), col = cc % (ROWB / 16);
-      const int key = min(k0 + row, a.kv_len - 1);
-      const T* src = (half ? vbase + (int64_t)key * a.svn : kbase + (int64_t)key * a.skn) + col * (16 / (int)sizeof(T));
-      *reinterpret_cast<uint4*>(smem + half * TILE + row * ROWB + col * 16) = *reinterpret_cast<const uint4*>(src);
+  // Units holding a tree column: u >= P / 32 (the unit at P / 32 may also
+  // hold prefix keys).  TW: their visibility words of the chunk's rows,
+  // built once below into tw[unit - ut0][row].
+  const int ut0 = max(u_lo, a.prefix_len / 32);
+  const int nt = max(0, u_lo + n - ut0);
+  uint32_t* tw = reinterpret_cast<uint32_t*>(smem + NSTG * SB);
+
+  // ring prologue: Q (compiler-tracked loads, consumed here so the compiler's
+  // own waits never count the ring's), the first NSTG - 1 units, and with TW
+  // the tree words (their loads land behind the units')
+  for (int j = 0; j < NSTG - 1 && j < n; ++j) issue(j);
+  if constexpr (TW) {
+    for (int i = 0; i < nt; ++i) {
+      const uint32_t w = row_ok ? vis_word((ut0 + i) * 32) : 0u;
+      if (lh == 0 && dh == 0) tw[i * kGenRows + rg * 32 + ln] = w;
     }
-    __syncthreads();
+  }
+  vm_wait<0>();
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) asm volatile("" : : "v"(qf[kk]));
+  for (int j = 0; j < n; ++j) {
+    // unit j landed for every wave; stage (j - 1) % NSTG is free
+    wait_units<LPW, NSTG - 2>(min(n - 1 - j, NSTG - 2));
+    sync_lds();
+    if (j + NSTG - 1 < n) issue(j + NSTG - 1);
+    const unsigned char* kt = smem + (j % NSTG) * SB;
+    const unsigned char* vt = kt + TILE;
+    const int k0 = (u_lo + j) * 32;
     // S^T: MFMA row = key, column = query row; lane (ln, lh) element i is key
     // 8*(i/4) + 4*lh + i%4 of row ln
+    // (K read KA k-steps ahead of its MFMA, fenced: left to itself the
+    // scheduler reads one step ahead and every MFMA waits an LDS latency)
     f32x16 s;
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    constexpr int KA = F32 ? 8 : 4;
+    typedef typename std::conditional<F32, float, i16x8>::type KF;
+    KF kf[KS];
+    auto rk = [&](int kk) {
+      if constexpr (F32) {
+        const int wd = 2 * kk + lh;  // word of the row
+        kf[kk] = *reinterpret_cast<const float*>(kt + swz(ln, wd >> 2) + (wd & 3) * 4);
+      } else {
+        kf[kk] = *reinterpret_cast<const i16x8*>(kt + swz(ln, 2 * kk + lh));
+      }
+    };
+#pragma unroll
+    for (int kk = 0; kk < KA; ++kk) rk(kk);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
+      if (kk + KA < KS) rk(kk + KA);
       if constexpr (F32) {
-        const float kv = *reinterpret_cast<const float*>(kt + ln * ROWB + (2 * kk + lh) * 4);
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv, qf[kk], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[kk], qf[kk], s, 0, 0, 0);
       } else {
-        const i16x8 kf = *reinterpret_cast<const i16x8*>(kt + ln * ROWB + (16 * kk + 8 * lh) * 2);
-        s = Mma<T>::run(bit_cast<typename Mma<T>::vec8>(kf), bit_cast<typename Mma<T>::vec8>(qf[kk]), s);
+        s = Mma<T>::run(bit_cast<typename Mma<T>::vec8>(kf[kk]), bit_cast<typename Mma<T>::vec8>(qf[kk]), s);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // mask, online softmax (tree_sparse_flashattn.py:272-279, :320-327)
-    const uint32_t w = row_ok ? vis_word(k0) : 0u;
+    // mask (units with a tree column only: every key of the others is a
+    // visible prefix key), online softmax (tree_sparse_flashattn.py:272-279,
+    // :320-327)
+    if (u_lo + j >= ut0) {
+      uint32_t w;
+      if constexpr (TW) w = tw[(u_lo + j - ut0) * kGenRows + rg * 32 + ln];
+      else w = row_ok ? vis_word(k0) : 0u;
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (!((w >> (8 * (i >> 2) + 4 * lh + (i & 3))) & 1u)) s[i] = -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (!((w >> (8 * (i >> 2) + 4 * lh + (i & 3))) & 1u)) s[i] = -INFINITY;
-      mx = fmaxf(mx, s[i]);
-    }
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     const float rmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    const float m_new = fmaxf(m_run, rmax);
-    // alpha = 1 while both are -inf; a first finite max scales the (zero) sums by 0
-    const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sl2);
+    // The reference point m_run moves only when a score passes it by more
+    // than 2^kRescaleLog2 (or on the row's first visible key: m_lim is -inf
+    // until then), so p <= 2^8 and O is rescaled on few units: with 32 rows
+    // per wave some row's exact maximum moves on almost every unit, and each
+    // rescale moves the D / 2 accumulators of a lane through the VALU.
+    // Exact for any consistent reference point (tree_sparse_flashattn.py:
+    // 272-279 rescales at every block); a row that sees one key still gets
+    // p = 2^0 = 1, O = V bit for bit.
+    const bool need = rmax > m_lim;
+    const float m_new = need ? rmax : m_run;
+    // alpha = 0 on the first visible key (O and l are still 0)
+    const float alpha = need ? __builtin_amdgcn_exp2f((m_run - m_new) * sl2) : 1.f;
     m_run = m_new;
-    // p = 2^((s - m) * scale): exactly 1 at the row's maximum (a single
-    // visible key gives O = V bit for bit, fp32 included); 0 for masked keys
-    // and while no key is visible
+    m_lim = m_new + thr_raw;
+    // p = 2^((s - m_run) * scale); 0 for masked keys and while no key is visible
     float p[16], ps = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -1715,8 +1839,10 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
       ps += p[i];
     }
     l_run = l_run * alpha + ps;
+    if (__ballot(need) != 0) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
     // O^T += V^T P^T, P rounded to the input dtype (tree_sparse_flashattn.py:278)
     if constexpr (F32) {
       // k-step i: keys 8*(i/4) + 4*k + i%4 (k = 0, 1), lane (ln, lh) gives its
@@ -1726,7 +1852,8 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = 8 * (i >> 2) + 4 * lh + (i & 3);
-          const float vv = *reinterpret_cast<const float*>(vt + key * ROWB + (32 * dt + ln) * 4);
+          const int wd = 32 * (dh * DT + dt) + ln;
+          const float vv = *reinterpret_cast<const float*>(vt + swv(key, wd >> 2) + (wd & 3) * 4);
           o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, p[i], o[dt], 0, 0, 0);
         }
     } else {
@@ -1735,21 +1862,32 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) pb[i >> 3][i & 7] = (T)p[i];
       // V^T fragments by the transposing LDS read: lane i of 16-lane group x
-      // gets keys 16*s2 + 8*jj + 4*(x>>1) + [0,4) of d = 32*dt + 16*(x&1) + i
+      // gets keys 16*s2 + 8*jj + 4*(x>>1) + [0,4) of d = 32*gt + 16*(x&1) + i,
+      // gt = dh*DT + dt the d-tile (bytes 64*gt + 2*(16*(x&1) + 4*(i&3)) of the
+      // key row: chunk 4*gt + 2*(x&1) + (i&3)/2, 8-byte half (i&3)&1)
       const int vx = lane >> 4, vi = lane & 15;
       const int vrow = 4 * (vx >> 1) + (vi >> 2);
-      const int vcol = 2 * (16 * (vx & 1) + 4 * (vi & 3));
+      const int vch = 2 * (vx & 1) + ((vi & 3) >> 1), vhalf = 8 * (vi & 1);
+      // P V MFMA g = (dt, s2) = (g / 2, g % 2), its V^T read VA MFMAs ahead
+      constexpr int NPV = 2 * DT, VA = 3;
+      i16x4 vh[NPV][2];
+      auto rv = [&](int g) {
+        const int dt = g >> 1, s2 = g & 1;
+        const int k0r = 16 * s2 + vrow, k1r = 16 * s2 + 8 + vrow;
+        vh[g][0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (TSFA_LDS i16x4*)(vt + swv(k0r, 4 * (dh * DT + dt) + vch) + vhalf));
+        vh[g][1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (TSFA_LDS i16x4*)(vt + swv(k1r, 4 * (dh * DT + dt) + vch) + vhalf));
+      };
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int g = 0; g < VA && g < NPV; ++g) rv(g);
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-          const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (TSFA_LDS i16x4*)(vt + (16 * s2 + vrow) * ROWB + 64 * dt + vcol));
-          const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (TSFA_LDS i16x4*)(vt + (16 * s2 + 8 + vrow) * ROWB + 64 * dt + vcol));
-          const i16x8 vf = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-          o[dt] = Mma<T>::run(bit_cast<V8>(vf), pb[s2], o[dt]);
-        }
+      for (int g = 0; g < NPV; ++g) {
+        if (g + VA < NPV) rv(g + VA);
+        const i16x8 vf = __builtin_shufflevector(vh[g][0], vh[g][1], 0, 1, 2, 3, 4, 5, 6, 7);
+        o[g >> 1] = Mma<T>::run(bit_cast<V8>(vf), pb[g & 1], o[g >> 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
@@ -1759,20 +1897,23 @@ __global__ __launch_bounds__(kGenWaves * 64) void gen_kernel(const GenArgs a) {
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   const int64_t prow = ((int64_t)bk * a.n_slots + slot) * TG + r;
   if (row_ok) {
-    float* dst = a.ws_o + prow * D;
+    float* dst = a.ws_o + prow * D + 32 * DT * dh;  // the wave's columns
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         *reinterpret_cast<f32x4*>(dst + 32 * dt + 8 * j + 4 * lh) =
             f32x4{o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv};
-    if (lh == 0) a.ws_ml[prow] = make_float2(m_run, lt);
+    if (lh == 0 && dh == 0) a.ws_ml[prow] = make_float2(m_run, lt);
   }
 }
 
 // The generic kernel's plan: 128-row chunks, the key axis cut into n_slots
-// splits of whole 32-key units so that the grid holds about two workgroups
-// per compute unit.
+// splits of whole 32-key units: about one workgroup per compute unit, with
+// the fp32 partials (written once, read once by the combine) held to at most
+// the K/V bytes or 8 MB, whichever is larger (the 8B decode shape at
+// head_dim 256: 16 splits, 36.8 us per call, against 40.5 with half the
+// K/V bytes (8 splits, half the CUs idle); twice the K/V bytes: the same 16).
 struct GenPlan {
   int n_chunks, n_units, units_per_split, n_slots, grid;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
@@ -1789,36 +1930,48 @@ inline int gen_plan(int batch, int num_heads, int num_kv_heads, int q_len, int k
   p->n_chunks = (int)((TG + kGenRows - 1) / kGenRows);
   p->n_units = ceil_div(kv_len, 32);
   const int64_t groups = (int64_t)batch * num_kv_heads * p->n_chunks;
-  const int64_t want = std::max<int64_t>(1, (2 * (int64_t)cus + groups - 1) / groups);
-  const int slots = (int)std::min<int64_t>(p->n_units, want);
+  const size_t es = dtype == TSFA_DTYPE_FP32 ? 4 : 2;
+  const double kv_bytes = 2.0 * batch * num_kv_heads * (double)kv_len * head_dim * es;
+  const double slot_bytes = (double)batch * num_heads * q_len * (4.0 * head_dim + 8.0);
+  const int64_t want = std::max<int64_t>(1, ((int64_t)cus + groups - 1) / groups);
+  const int64_t cap = std::max<int64_t>(1, (int64_t)(std::max(kv_bytes, 8.0 * (1 << 20)) / slot_bytes));
+  const int slots = (int)std::min<int64_t>(p->n_units, std::min(want, cap));
   p->units_per_split = ceil_div(p->n_units, slots);
   p->n_slots = ceil_div(p->n_units, p->units_per_split);
   const int64_t grid = groups * p->n_slots;
   if (grid > INT32_MAX / 2) return TSFA_ERR_UNSUPPORTED;
   p->grid = (int)grid;
-  const size_t es = dtype == TSFA_DTYPE_FP32 ? 4 : 2;
-  p->lds_bytes = 2 * 32 * (size_t)head_dim * es;
+  const int stage = 2 * 32 * head_dim * (int)es;
+  p->lds_bytes = (size_t)kGenStages(stage) * stage + kGenTreeBytes;
   const size_t rows = (size_t)batch * num_heads * q_len;
   p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 4);
   p->ws_ml_bytes = align256(rows * p->n_slots * 8);
   return TSFA_OK;
 }
 
-template <typename T, int D>
-int launch_gen(const GenArgs& ga, const CombineArgs& ca, const GenPlan& p, hipStream_t stream) {
+template <typename T, int D, bool TW>
+int launch_gen_kernel(const GenArgs& ga, const GenPlan& p, hipStream_t stream) {
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return TSFA_ERR_DEVICE;
   const uint64_t bit = 1ull << (dev & 63);
   if (p.lds_bytes > 65536 && (attr_set.load(std::memory_order_acquire) & bit) == 0) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gen_kernel<T, D>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&gen_kernel<T, D, TW>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds_bytes) != hipSuccess)
       return TSFA_ERR_LAUNCH;
     attr_set.fetch_or(bit, std::memory_order_acq_rel);
   }
+  hipLaunchKernelGGL((gen_kernel<T, D, TW>), dim3(p.grid), dim3(gen_waves<T>() * 64), p.lds_bytes, stream, ga);
+  return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
+}
+
+template <typename T, int D>
+int launch_gen(const GenArgs& ga, const CombineArgs& ca, const GenPlan& p, hipStream_t stream) {
   if (g_kernel_mask & 1) {
-    hipLaunchKernelGGL((gen_kernel<T, D>), dim3(p.grid), dim3(kGenWaves * 64), p.lds_bytes, stream, ga);
-    if (hipGetLastError() != hipSuccess) return TSFA_ERR_LAUNCH;
+    // tree units of the fullest split: their words fit the LDS table?
+    const bool tw = std::min(p.units_per_split, p.n_units - ga.prefix_len / 32) <= kGenTreeUnits;
+    const int st = tw ? launch_gen_kernel<T, D, true>(ga, p, stream) : launch_gen_kernel<T, D, false>(ga, p, stream);
+    if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0) return TSFA_OK;
   // the fp32 partials of every row merged: rows cut into 8 equal ranges, one

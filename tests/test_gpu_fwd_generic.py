@@ -102,6 +102,22 @@ def test_generic_cases(case):
                            half_ulps=storage_roundings(q, k, p) if p < 256 and dtype != torch.float32 else 0)
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 256)])
+def test_long_tree_builds_its_words_in_the_loop(dtype, d):
+    # 1100 tree tokens and no prefix: one split of 35 units, all with tree
+    # columns, more than the prologue's LDS word table holds (32 units), so
+    # the kernel instance that builds each unit's words in the loop runs
+    t = 1100
+    print(f"[gen] long tree {dtype} head_dim {d}", flush=True)
+    rng = np.random.default_rng(d)
+    mask = torch.from_numpy(_tree("depth", t, rng))
+    q, k, v = _qkv(1, 4, 2, t, 0, d, dtype, seed=d + 1)
+    out = _run_nan_filled(q, k, v, mask, 0, 64, 64)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, 0), dtype,
+                           half_ulps=1 if dtype != torch.float32 else 0)
+
+
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 128)])
 def test_per_sequence_trees_and_lse(dtype, d):
     b, hq, hkv, t, p = 3, 8, 2, 40, 150
