@@ -550,9 +550,9 @@ def main():
                     help="also time the paged-cache forward at this page size (0: skip)")
     ap.add_argument("--workloads", default="batched-decode-b16-p2048:100,wide-tree-1024-p16384:10,"
                     "llama3-70b-b4-p32768:5,llama3-70b-b4-p32768@64x32:5,llama3-70b-b4-p32768@64x128:5,"
-                    "llama3-70b-b4-p32768@16x64:5",
-                    help="other forward workloads timed into the `workloads` object, as name[@BMxBN]:steps "
-                         "('' skips)")
+                    "llama3-70b-b4-p32768@16x64:5,llama3-8b-eagle64-p4096+d256:100,tiny-random-tree-fp32:100",
+                    help="other forward workloads timed into the `workloads` object, as "
+                         "name[+d<head_dim>|+fp32][@BMxBN]:steps ('' skips)")
     ap.add_argument("--workload-cpu-seconds", type=float, default=6.0,
                     help="CPU baseline sample per other workload (0 skips)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
