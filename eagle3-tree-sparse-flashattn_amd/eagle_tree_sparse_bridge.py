@@ -229,10 +229,10 @@ def _tree_call(q, k, v, mask, block_m, block_n):
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), mask.data_ptr(), seq_stride, row_stride, n_masks,
             strides, scale, *ints, ws.data_ptr(), ws_bytes)
     if dev.index == torch.cuda.current_device():
-        st = lib.tsfa_tree_attention(*args, torch.cuda.current_stream().cuda_stream)
+        st = lib.tsfa_tree_attention(*args, _lib.stream_handle(dev))
     else:
         with torch.cuda.device(dev):
-            st = lib.tsfa_tree_attention(*args, torch.cuda.current_stream(dev).cuda_stream)
+            st = lib.tsfa_tree_attention(*args, _lib.stream_handle(dev))
     _lib.check("run_tree_sparse_kernel", st)
     return out
 

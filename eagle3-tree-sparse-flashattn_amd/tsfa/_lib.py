@@ -151,7 +151,17 @@ def ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
 
 
+# torch's raw current-stream accessor (an int, no Stream object: ~0.2 us
+# against ~1.8 us for current_stream(dev).cuda_stream per eager call)
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device) -> int:
+    """The hipStream_t of torch's current stream on `device` (the capture
+    stream under graph capture)."""
+    if _RAW_STREAM is not None:
+        idx = device.index if isinstance(device, torch.device) else device
+        return _RAW_STREAM(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 
