@@ -1587,6 +1587,9 @@ struct GenArgs {
   int n_chunks, n_units, units_per_split, n_slots;
   float* ws_o;     // [B*Hkv][n_slots][q_len*G][D] fp32 partial O / l
   float2* ws_ml;   // [B*Hkv][n_slots][q_len*G] (m, l)
+  void* out;       // direct: O [B, Hq, q_len, D] (strides sob, soh, som; d stride 1)
+  int64_t sob, soh, som;
+  int direct;      // one split and no LSE: the kernel writes O, no partials, no combine
 };
 
 // 128-row chunks: 4 row groups of 32.  The 16-bit instances (head_dim 256)
@@ -1891,9 +1894,28 @@ __global__ __launch_bounds__(gen_waves<T>() * 64) void gen_kernel(const GenArgs 
     }
   }
 
+  const float lt = pair_sum(l_run);
+  if (a.direct) {
+    // a one-split plan writes the lane's row of O (token t, head kvh*G + g)
+    // in the input dtype: one rounding of the fp32 result; a row that saw no
+    // key gets NaN (0/0, as the reference and the combine give)
+    if (row_ok) {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      const float inv_o = lt > 0.f ? 1.f / lt : __builtin_nanf("");
+      T* dst = static_cast<T*>(a.out) + b * a.sob + (int64_t)(kvh * G + g) * a.soh + (int64_t)t * a.som +
+               32 * DT * dh;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<T4*>(dst + 32 * dt + 8 * j + 4 * lh) =
+              T4{(T)(o[dt][4 * j] * inv_o), (T)(o[dt][4 * j + 1] * inv_o), (T)(o[dt][4 * j + 2] * inv_o),
+                 (T)(o[dt][4 * j + 3] * inv_o)};
+    }
+    return;
+  }
   // partial of the lane's row: O / l in fp32 and (m, l); a split that saw no
   // key stores O = 0 with m = -inf (weight 0 in the combine)
-  const float lt = pair_sum(l_run);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   const int64_t prow = ((int64_t)bk * a.n_slots + slot) * TG + r;
   if (row_ok) {
@@ -1973,7 +1995,7 @@ int launch_gen(const GenArgs& ga, const CombineArgs& ca, const GenPlan& p, hipSt
     const int st = tw ? launch_gen_kernel<T, D, true>(ga, p, stream) : launch_gen_kernel<T, D, false>(ga, p, stream);
     if (st != TSFA_OK) return st;
   }
-  if ((g_kernel_mask & 2) == 0) return TSFA_OK;
+  if ((g_kernel_mask & 2) == 0 || ga.direct) return TSFA_OK;
   // the fp32 partials of every row merged: rows cut into 8 equal ranges, one
   // per XCD slot of the combine's block ids (no placement to follow: the
   // splits of a chunk spread over the grid)
@@ -2152,6 +2174,13 @@ int gen_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   ga.n_slots = p.n_slots;
   ga.ws_o = static_cast<float*>(workspace);
   ga.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
+  // One split and no LSE: the kernel writes O itself (TSFA_DIRECT_OUT=0
+  // keeps the partials and the combine)
+  ga.out = o;
+  ga.sob = o_strides[0];
+  ga.soh = o_strides[1];
+  ga.som = o_strides[2];
+  ga.direct = (config().direct_out != 0 && p.n_slots == 1 && lse == nullptr) ? 1 : 0;
   CombineArgs ca;
   ca.o = o;
   ca.lse = lse;

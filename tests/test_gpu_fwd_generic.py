@@ -118,6 +118,32 @@ def test_long_tree_builds_its_words_in_the_loop(dtype, d):
                            half_ulps=1 if dtype != torch.float32 else 0)
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 64)])
+def test_one_split_plans_write_o_directly(dtype, d, monkeypatch):
+    # 16 sequences x 8 kv heads x 2 row chunks = 256 groups: one split, so
+    # the kernel writes O itself; TSFA_DIRECT_OUT=0 keeps the fp32 partial
+    # and the combine, whose one-slot merge (l * x) / l may move x by an
+    # fp32 ulp: the two agree within one ulp of the output dtype
+    b, hq, hkv, t, p = 16, 32, 8, 64, 200
+    print(f"[gen] one split {dtype} head_dim {d}", flush=True)
+    rng = np.random.default_rng(d + 3)
+    masks = torch.from_numpy(np.stack([_tree("eagle", t, rng) for _ in range(b)]))
+    masks[3, 5, :] = False  # a row with no visible tree key (the prefix still shows)
+    q, k, v = _qkv(b, hq, hkv, t, p, d, dtype, seed=d + 5)
+    outs = {}
+    for direct in ("1", "0"):
+        monkeypatch.setenv("TSFA_DIRECT_OUT", direct)
+        outs[direct] = _run_nan_filled(q, k, v, masks, p, 16, 32)
+        torch.cuda.synchronize()
+    ref = oracle_out(q, k, v, masks, p)
+    for direct, out in outs.items():
+        assert_close_to_oracle(out, ref, dtype)
+    a, c = outs["1"].float().cpu(), outs["0"].float().cpu()
+    assert torch.equal(a.isnan(), c.isnan())
+    from tests.gpu_util import half_ulp
+    assert ((a - c).abs().nan_to_num(0) <= 2 * half_ulp(c, dtype) + 1e-30).all()
+
+
 @pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 256), (torch.float32, 128)])
 def test_per_sequence_trees_and_lse(dtype, d):
     b, hq, hkv, t, p = 3, 8, 2, 40, 150
