@@ -206,6 +206,22 @@ def test_reference_grid_launch_in_fp32_with_strided_views():
     assert_close_to_oracle(o, oracle_out(q.cpu(), k.cpu(), v.cpu(), mask, P), torch.float32)
 
 
+@pytest.mark.parametrize("dtype,d", [(torch.bfloat16, 160), (torch.float16, 200), (torch.float32, 96)])
+def test_head_dims_between_kernel_widths_run_zero_padded(dtype, d):
+    # 160 / 200 run the head_dim 256 kernel, fp32 96 the fp32 128 one, on
+    # zero-padded copies (zeros add nothing to q.k and give zero columns of O)
+    print(f"[gen] padded {dtype} head_dim {d}", flush=True)
+    rng = np.random.default_rng(d)
+    mask = torch.from_numpy(_tree("eagle", 40, rng))
+    q, k, v = _qkv(2, 8, 4, 40, 150, d, dtype, seed=d)
+    out = tsf.tree_sparse_attention_fwd(q.cuda(), k.cuda(), v.cuda(),
+                                        tsf.prepare_tree_sparse_metadata(mask.cuda(), 150, 16, 32))
+    torch.cuda.synchronize()
+    assert out.shape == q.shape
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, 150), dtype,
+                           half_ulps=1 if dtype != torch.float32 else 0)
+
+
 def test_paged_and_backward_refuse_the_generic_shapes():
     q, k, v = (x.cuda() for x in _qkv(1, 4, 2, 16, 32, 256, torch.bfloat16))
     meta = tsf.prepare_tree_sparse_metadata(torch.eye(16, dtype=torch.bool).cuda(), 32, 16, 16)
