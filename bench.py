@@ -560,7 +560,7 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}); "
+        print(f"bench.py measures one GPU: the library has no multi-GPU path (got --gpus {args.gpus}); "
               "the forward shards by (batch, kv head) with no exchange -- run one process per GPU.",
               file=sys.stderr)
         sys.exit(2)

@@ -74,7 +74,7 @@ __device__ unsigned long long g_stamps[4096 * 64];
       g_stamps[(size_t)blockIdx.x * 64 + (k) + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 // Per-wave cycle sums of loop phases (s_memtime deltas; each reading waits
-// for the wave's outstanding LDS/scalar loads, so this build perturbs the loop).
+// for the wave's outstanding LDS/scalar loads, so the instrumented library perturbs the loop).
 __device__ unsigned long long g_cyc[4096 * 32];
 #define TSFA_CYC_DECL unsigned long long cyc_prev = __builtin_amdgcn_s_memtime(), cyc_acc[4] = {0, 0, 0, 0};
 #define TSFA_CYC(k)                                              \

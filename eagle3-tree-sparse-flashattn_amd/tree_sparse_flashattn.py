@@ -421,7 +421,7 @@ def _padded_dim(d: int) -> int:
     for w in _KERNEL_DIMS:
         if d <= w:
             return w
-    raise NotImplementedError(f"head_dim {d} is above this build's widest kernel ({_KERNEL_DIMS[-1]})")
+    raise NotImplementedError(f"head_dim {d} is above the widest kernel ({_KERNEL_DIMS[-1]})")
 
 
 def _strided(t: torch.Tensor, size, stride) -> torch.Tensor:

@@ -34,7 +34,7 @@ typedef struct ihipStream_t* tsfa_stream_t; /* a hipStream_t; NULL = default str
 enum tsfa_status {
   TSFA_OK = 0,
   TSFA_ERR_INVALID_ARGUMENT = 1, /* shapes/values the reference rejects (ValueError / assert) */
-  TSFA_ERR_UNSUPPORTED = 2,      /* valid for the reference, outside this build's kernels */
+  TSFA_ERR_UNSUPPORTED = 2,      /* valid for the reference, outside this library's kernels */
   TSFA_ERR_WORKSPACE = 3,        /* workspace missing or smaller than *_workspace_bytes() */
   TSFA_ERR_LAUNCH = 4,           /* the HIP runtime refused a launch */
   TSFA_ERR_DEVICE = 5            /* no usable HIP device / attribute query failed */

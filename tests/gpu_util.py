@@ -10,7 +10,7 @@ from oracle.attn_oracle import dense_mask_attention
 
 # max_abs_err bars against the fp32 oracle (the named workloads use these alone).
 TOL = {torch.bfloat16: 8e-3, torch.float16: 2e-3, torch.float32: 1e-4}
-# fp32 inputs (fp32 MFMA, P not rounded): the north_star bars cover 16-bit
+# fp32 inputs (fp32 MFMA, P not rounded): the stated bars cover 16-bit
 # inputs only; fp32 is held to 1e-4, well inside what the reference's fp32
 # tl.dot (TF32 by default on its own hardware, tree_sparse_flashattn.py:269)
 # could meet.

@@ -4,7 +4,7 @@ fp32 dense+mask oracle.
 The reference takes any power-of-two BLOCK_D (tree_sparse_flashattn.py:
 200-202, README.md:190) and any dtype tl.dot takes (fp32 included,
 tree_sparse_flashattn.py:269, :278).  Bars: 8e-3 (bf16) / 2e-3 (fp16) as
-north_star states them, 1e-4 for fp32 (tests/gpu_util.py); O and the
+the forward's parity bar states them, 1e-4 for fp32 (tests/gpu_util.py); O and the
 workspace start NaN-filled so an unwritten row fails.
 """
 
