@@ -1043,16 +1043,20 @@ void split_kernel(const SplitArgs a) {
         issue_at(sb, key0_of(i));
       }
     };
-    // Q and the first NS-QS units of each stream leave together; wait for Q
-    // only (loads complete in order), then every wave reads its fragments.
+    // Q and the first two units of each stream leave together; wait for Q
+    // only (loads complete in order), then every wave reads its fragments
+    // and the ring prologue requests the rest of its NS - 1 units ahead.
     // With QS > 1 the ring prologue reuses Q stages: one more barrier first.
-    // A run requests at most NS - 1 units of its stream ahead: requesting a
-    // short run's units all at once (every run of the Llama-3-8B decode
-    // shape fits in LDS) lets Q and the first units queue behind the rest in
-    // HBM (Q landed 3.6 against 2.8 us after the workgroups start; 16.0
-    // against 15.4-15.6 us per call, same-box A/B).
+    // Every workgroup starts at once, so the opening requests of the whole
+    // grid queue in HBM together: the fewer units beside Q, the sooner every
+    // CU's Q and unit 0 arrive.  Requesting a short run's units all at once
+    // (every run of the Llama-3-8B decode shape fits in LDS) measured 16.0
+    // against 15.4-15.6 us per call; two units with Q instead of NS - QS
+    // (3 with two streams, 4 with one): the 8B shape 15.6 -> 15.3 us, the
+    // 16-sequence shape 49.7 -> 47.8-48.3 us, the 1024-token tree unchanged
+    // (same-box A/B; one unit: in between).
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
-    const int pre = min(mine, NS - QS);
+    const int pre = min(mine, min(NS - QS, 2));
     TSFA_STAMP(62);
     issue_q();
     for (int j = 0; j < pre; ++j) issue_prefix(sring_lds + j * SB, ks + S * j);
