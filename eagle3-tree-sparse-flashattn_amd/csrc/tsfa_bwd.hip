@@ -767,7 +767,8 @@ __device__ inline void bwd_vis(const VisArgs& a, int tile, int tree, int zc, int
     int qq = 0;
     while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
     const int tb = ci[e];
-    if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] == TSFA_FULL_BLOCK) ? -1 : (of[e] + 1);
+    // a block of any kind but MIXED is FULL (tree_sparse_flashattn.py:313-318)
+    if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
   }
   __syncthreads();
   const int R = r_lo + (lane & 31);
