@@ -1770,8 +1770,8 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
 // MIXED bit).  S^T = K Q^T and O^T += V^T P^T on
 // v_mfma_f32_32x32x16_{bf16,f16} (V^T from ds_read_b64_tr_b16) or
 // v_mfma_f32_32x32x2_f32, with the key order of the P V product permuted so
-// that P^T comes straight from the S^T accumulator.  Every split writes an
-// fp32 partial (O / l and (m, l)) that combine_kernel merges.
+// that P^T comes straight from the S^T accumulator.  Every split writes a
+// partial (O / l in the input dtype, fp32 (m, l)) that combine_kernel merges.
 // Units stream HBM -> LDS through a ring of kGenStages(stage bytes) stages
 // (global_load_lds, NSTG - 1 units ahead).  In the 16-bit instances 16-byte
 // chunk c of key row k sits at chunk position c ^ (k & 15) in the K tile and
@@ -1799,7 +1799,7 @@ struct GenArgs {
   int neg_q;         // sm_scale < 0: Q enters negated
   int num_kv_heads, group, q_len, kv_len, prefix_len, block_m, block_n;
   int n_chunks, n_units, units_per_split, n_slots;
-  float* ws_o;     // [B*Hkv][n_slots][q_len*G][D] fp32 partial O / l
+  void* ws_o;      // [B*Hkv][n_slots][q_len*G][D] partial O / l: the input dtype (fp32 for fp32)
   float2* ws_ml;   // [B*Hkv][n_slots][q_len*G] (m, l)
   void* out;       // direct: O [B, Hq, q_len, D] (strides sob, soh, som; d stride 1)
   int64_t sob, soh, som;
@@ -2128,28 +2128,33 @@ __global__ __launch_bounds__(gen_waves<T>() * 64) void gen_kernel(const GenArgs 
     }
     return;
   }
-  // partial of the lane's row: O / l in fp32 and (m, l); a split that saw no
-  // key stores O = 0 with m = -inf (weight 0 in the combine)
+  // partial of the lane's row: O / l in the input dtype (as the split
+  // kernel's; half the bytes written here and read by the combine of fp32
+  // ones) and (m, l); a split that saw no key stores O = 0 with m = -inf
+  // (weight 0 in the combine)
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   const int64_t prow = ((int64_t)bk * a.n_slots + slot) * TG + r;
   if (row_ok) {
-    float* dst = a.ws_o + prow * D + 32 * DT * dh;  // the wave's columns
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T* dst = static_cast<T*>(a.ws_o) + prow * D + 32 * DT * dh;  // the wave's columns
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        *reinterpret_cast<f32x4*>(dst + 32 * dt + 8 * j + 4 * lh) =
-            f32x4{o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv, o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv};
+        *reinterpret_cast<T4*>(dst + 32 * dt + 8 * j + 4 * lh) =
+            T4{(T)(o[dt][4 * j] * inv), (T)(o[dt][4 * j + 1] * inv), (T)(o[dt][4 * j + 2] * inv),
+               (T)(o[dt][4 * j + 3] * inv)};
     if (lh == 0 && dh == 0) a.ws_ml[prow] = make_float2(m_run, lt);
   }
 }
 
 // The generic kernel's plan: 128-row chunks, the key axis cut into n_slots
 // splits of whole 32-key units: about one workgroup per compute unit, with
-// the fp32 partials (written once, read once by the combine) held to at most
+// the partials (written once, read once by the combine) held to at most
 // the K/V bytes or 8 MB, whichever is larger (the 8B decode shape at
-// head_dim 256: 16 splits, 36.8 us per call, against 40.5 with half the
-// K/V bytes (8 splits, half the CUs idle); twice the K/V bytes: the same 16).
+// head_dim 256 with fp32 partials: 16 splits, 36.8 us per call, against 40.5
+// with half the K/V bytes (8 splits, half the CUs idle); twice the K/V
+// bytes: the same 16).
 struct GenPlan {
   int n_chunks, n_units, units_per_split, n_slots, grid;
   size_t lds_bytes, ws_acc_bytes, ws_ml_bytes;
@@ -2168,7 +2173,7 @@ inline int gen_plan(int batch, int num_heads, int num_kv_heads, int q_len, int k
   const int64_t groups = (int64_t)batch * num_kv_heads * p->n_chunks;
   const size_t es = dtype == TSFA_DTYPE_FP32 ? 4 : 2;
   const double kv_bytes = 2.0 * batch * num_kv_heads * (double)kv_len * head_dim * es;
-  const double slot_bytes = (double)batch * num_heads * q_len * (4.0 * head_dim + 8.0);
+  const double slot_bytes = (double)batch * num_heads * q_len * ((double)es * head_dim + 8.0);
   const int64_t want = std::max<int64_t>(1, ((int64_t)cus + groups - 1) / groups);
   const int64_t cap = std::max<int64_t>(1, (int64_t)(std::max(kv_bytes, 8.0 * (1 << 20)) / slot_bytes));
   const int slots = (int)std::min<int64_t>(p->n_units, std::min(want, cap));
@@ -2180,7 +2185,7 @@ inline int gen_plan(int batch, int num_heads, int num_kv_heads, int q_len, int k
   const int stage = 2 * 32 * head_dim * (int)es;
   p->lds_bytes = (size_t)kGenStages(stage) * stage + kGenTreeBytes;
   const size_t rows = (size_t)batch * num_heads * q_len;
-  p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * 4);
+  p->ws_acc_bytes = align256(rows * p->n_slots * head_dim * es);
   p->ws_ml_bytes = align256(rows * p->n_slots * 8);
   return TSFA_OK;
 }
@@ -2210,7 +2215,7 @@ int launch_gen(const GenArgs& ga, const CombineArgs& ca, const GenPlan& p, hipSt
     if (st != TSFA_OK) return st;
   }
   if ((g_kernel_mask & 2) == 0 || ga.direct) return TSFA_OK;
-  // the fp32 partials of every row merged: rows cut into 8 equal ranges, one
+  // the partials of every row merged: rows cut into 8 equal ranges, one
   // per XCD slot of the combine's block ids (no placement to follow: the
   // splits of a chunk spread over the grid)
   CombineArgs c = ca;
@@ -2224,13 +2229,13 @@ int launch_gen(const GenArgs& ga, const CombineArgs& ca, const GenPlan& p, hipSt
   if (blocks > INT32_MAX) return TSFA_ERR_UNSUPPORTED;
   const int ns = ca.n_slots;
   if (ns <= 2)
-    hipLaunchKernelGGL((combine_kernel<T, D, 2, 1, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+    hipLaunchKernelGGL((combine_kernel<T, D, 2, 1, T>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
   else if (ns <= 4)
-    hipLaunchKernelGGL((combine_kernel<T, D, 4, 1, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 1, T>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
   else if (gr == 2)
-    hipLaunchKernelGGL((combine_kernel<T, D, 4, 2, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 2, T>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
   else
-    hipLaunchKernelGGL((combine_kernel<T, D, 4, 1, float>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
+    hipLaunchKernelGGL((combine_kernel<T, D, 4, 1, T>), dim3((unsigned)blocks), dim3(kCombineThreads), 0, stream, c);
   return hipGetLastError() == hipSuccess ? TSFA_OK : TSFA_ERR_LAUNCH;
 }
 
@@ -2386,7 +2391,7 @@ int gen_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   ga.n_units = p.n_units;
   ga.units_per_split = p.units_per_split;
   ga.n_slots = p.n_slots;
-  ga.ws_o = static_cast<float*>(workspace);
+  ga.ws_o = workspace;
   ga.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) + p.ws_acc_bytes);
   // One split and no LSE: the kernel writes O itself (TSFA_DIRECT_OUT=0
   // keeps the partials and the combine)

@@ -118,9 +118,9 @@ int tsfa_pack_bits_host(const uint8_t* bits, int64_t n_bits, int32_t* words);
  * 269, :278); block_n a positive multiple of 16, block_m >= 1, num_heads %
  * num_kv_heads == 0 with gqa_group_size == num_heads / num_kv_heads <= 256,
  * q_len >= 1, kv_len >= prefix_len >= 0, 16-byte aligned q/k/v/o rows.
- * head_dim 256 and fp32 run a simpler kernel with fp32 split-KV partials
- * (contiguous K/V only: tsfa_fwd_paged and tsfa_bwd refuse them with
- * TSFA_ERR_UNSUPPORTED); size their workspace with
+ * head_dim 256 and fp32 run a simpler kernel whose split-KV partials are in
+ * the input dtype (contiguous K/V only: tsfa_fwd_paged and tsfa_bwd refuse
+ * them with TSFA_ERR_UNSUPPORTED); size their workspace with
  * tsfa_fwd_workspace_bytes_for_dtype.
  */
 int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
@@ -129,7 +129,8 @@ int tsfa_fwd_check_args(int batch, int num_heads, int num_kv_heads, int q_len, i
 size_t tsfa_fwd_workspace_bytes(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                 int prefix_len, int head_dim);
 /* tsfa_fwd_workspace_bytes for inputs of `dtype` (tsfa_fwd_workspace_bytes
- * sizes 16-bit inputs; fp32 partials need more).  No reference counterpart. */
+ * sizes 16-bit inputs; fp32 inputs' fp32 partials need more).  No reference
+ * counterpart. */
 size_t tsfa_fwd_workspace_bytes_for_dtype(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
                                           int prefix_len, int head_dim, int dtype);
 int tsfa_fwd(const void* q, const void* k, const void* v, void* o,

@@ -34,16 +34,39 @@ MANT = {torch.bfloat16: 8, torch.float16: 11, torch.float32: 24}
 
 def storage_roundings(q, k, prefix_len) -> int:
     """Roundings of O to its dtype in one forward call of this shape: 1 when
-    the plan has one slot (the split kernel writes O), else 2 (partial, then
-    O).  The plan is read under the current TSFA_* switches."""
+    the plan has one slot (the kernel writes O, or a one-slot merge returns
+    the partial), else 2 (partial in the input dtype, then O).  fp32 inputs:
+    1 (fp32 partials).  The plan is read under the current TSFA_* switches."""
     from tsfa import _lib
 
     b, hq, t, d = q.shape
-    if d > 128 or q.dtype == torch.float32:
-        return 1  # the generic kernel: fp32 partials, O rounded once
+    if q.dtype == torch.float32:
+        return 1
+    if d > 128:
+        return 1 if generic_slots(q, k, prefix_len) == 1 else 2
     width = 64 if d <= 64 else 128  # narrower head dims run zero-padded
     plan = _lib.fwd_plan(b, hq, k.shape[1], t, k.shape[2], prefix_len, width)
     return 1 if plan["slots"] == 1 else 2
+
+
+def generic_slots(q, k, prefix_len) -> int:
+    """Key splits of the generic kernel's plan for this 16-bit shape, read
+    back from the library's workspace size (partials of rows x slots x D in
+    the input dtype plus fp32 (m, l), each 256-byte aligned)."""
+    from tsfa import _lib
+
+    b, hq, t, d = q.shape
+    rows = b * hq * t
+    ws = int(_lib.load().tsfa_fwd_workspace_bytes_for_dtype(b, hq, k.shape[1], t, k.shape[2], prefix_len, d,
+                                                            _lib.dtype_code(q.dtype)))
+
+    def a256(x):
+        return (x + 255) // 256 * 256
+
+    for ns in range(1, (k.shape[2] + 31) // 32 + 1):
+        if a256(rows * ns * d * 2) + a256(rows * ns * 8) == ws:
+            return ns
+    raise AssertionError(f"no slot count gives a workspace of {ws} bytes")
 
 
 def half_ulp(x: torch.Tensor, dtype) -> torch.Tensor:

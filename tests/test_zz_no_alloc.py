@@ -63,8 +63,9 @@ def test_noalloc_matches_tsfa_fwd_on_two_calls():
 
 
 def test_noalloc_matches_tsfa_fwd_on_the_generic_kernel():
-    # head_dim 256 and fp32 run the generic kernel with fp32 partials, whose
-    # size the entry point checks against its array by dtype
+    # head_dim 256 and fp32 run the generic kernel, whose partials (in the
+    # input dtype, fp32 for fp32 inputs) the entry point sizes against its
+    # array by dtype
     g = torch.Generator().manual_seed(11)
     for dtype, head_dim in ((torch.float32, 128), (torch.bfloat16, 256), (torch.float32, 64)):
         q = torch.randn(2, 8, 29, head_dim, generator=g).to(dtype).cuda()
