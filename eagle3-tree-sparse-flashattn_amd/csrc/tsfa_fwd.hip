@@ -487,6 +487,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 
 void split_kernel(const SplitArgs a) {
   constexpr int FM = FAST & 3;              // unchecked ring steps: 0 off, 1 plain, 2 non-temporal loads
   constexpr bool DIRECT = (FAST & 4) != 0;  // one-slot plan: write O, no combine
+  constexpr bool PTAB = PAGED && FM != 0 && (FAST & 8) != 0;  // paged: steady refills from the LDS page-id table
   typedef typename Mma<T>::vec8 V8;
   constexpr int RG = kWaves / S;             // row groups (waves per stream)
   constexpr int ROWS = 32 * RG;              // rows per chunk
@@ -1112,11 +1113,36 @@ void split_kernel(const SplitArgs a) {
       if (wave == 0 && lane <= nqbc_c) dma4(a.row_ptr + b * a.ms_row_ptr + qb_lo_c + lane, lds_addr(rps_c));
       for (int i = tid; i < a.tree_ntok * n_tu_c; i += kWaves * 64) masks[i] = 0u;
     }
+    // Paged runs of full prefix units: the run's page ids (list positions
+    // pg_lo .. pg_lo + n_pg - 1, clamped like page_entry / clamp_page) leave
+    // HBM with Q into an LDS table, so a steady refill takes its page from
+    // one LDS read a step ahead and a product, instead of the page-table
+    // scalar loads, clamps and 64-bit address checks of the general path.
+    // Each wave clamps the entries it requested once its Q landed; the Q
+    // barrier publishes them.  Its own instance (FAST & 8): the general
+    // path's variables beside the table's spilled SGPRs in the loop of the
+    // two-stream kernels (the Llama-3-8B decode shape's paged call 19.9 ->
+    // 22.3 us with both paths in one instance).
+    int* ptab = misc + kMiscInts;  // kPageTabInts entries (paged instances only)
+    const int pg_lo = PAGED ? (int)(((int64_t)u_lo * kUnitKeys) >> a.page_shift) : 0;
+    const int n_pg = PAGED ? (int)((((int64_t)(u_lo + n) * kUnitKeys - 1) >> a.page_shift) - pg_lo + 1) : 0;
+    // (the host chose the instance: every run within the table, rows_fast;
+    // the table's reads are clamped to it all the same)
+    const bool ptab_ok = PTAB && n > 0;
+    if (ptab_ok) {
+      for (int i0 = wave * 64; i0 < min(n_pg, kPageTabInts); i0 += kWaves * 64)
+        if (i0 + lane < min(n_pg, kPageTabInts))
+          dma4(a.kv_indices + min(max(pt_base + pg_lo + i0 + lane, 0), a.n_indices - 1), lds_addr(ptab + i0));
+    }
     TSFA_STAMP(62);
     issue_q();
     for (int j = 0; j < pre; ++j) issue_prefix(sring_lds + j * SB, ks + S * j);
     TSFA_STAMP(60);
     wait_units<LPU, NS - QS>(pre);
+    if (ptab_ok) {
+      for (int i = wave * 64 + lane; i < min(n_pg, kPageTabInts); i += kWaves * 64)
+        ptab[i] = min(max(ptab[i], 0), a.n_pages - 1);
+    }
     sync_lds();
     TSFA_STAMP(1);
     read_q();
@@ -1258,8 +1284,17 @@ void split_kernel(const SplitArgs a) {
     const char* seq_rows = nullptr;
     uint32_t seq_stage = 0;
     int seq_t = 0;  // paged: the stream's next unit
+    // paged with the LDS page table: the wave's first key of the next unit
+    // and that key's page id, read from the table one refill ahead (its rows
+    // sit in one page: a share of 8 or 16 aligned keys, pages of 16 or more)
+    int seq_kw = 0, seq_pid = 0;
+    const int pmask = PAGED ? (1 << a.page_shift) - 1 : 0;
     auto seq_init = [&](int t) {
-      if constexpr (PAGED) {
+      if constexpr (PTAB) {
+        seq_stage = (uint32_t)(t % NS) * SB;
+        seq_kw = key0_of(ks + S * t) + dma_u0 * DRPL;
+        if (t < mine) seq_pid = ptab[min((seq_kw >> a.page_shift) - pg_lo, kPageTabInts - 1)];
+      } else if constexpr (PAGED) {
         seq_t = t;
       } else {
         seq_rows = run_rows + (int64_t)(ks + S * t) * unit_bytes;
@@ -1267,7 +1302,21 @@ void split_kernel(const SplitArgs a) {
       }
     };
     auto seq_next = [&](int mine_units) {
-      if constexpr (PAGED) {
+      if constexpr (PTAB) {
+        const int pid = __builtin_amdgcn_readfirstlane(seq_pid);
+        const char* rowp;
+        if constexpr (C32)
+          rowp = reinterpret_cast<const char*>(dbase) + ((uint32_t)pid * a.cps_b32 + (uint32_t)(seq_kw & pmask) * a.crs_b32);
+        else
+          rowp = reinterpret_cast<const char*>(dbase + (int64_t)pid * a.cps + (int64_t)(seq_kw & pmask) * a.crs);
+        if (kv_nt) dma_rows<LPU, true>(rowp, doff, sring_lds + seq_stage + m0_off);
+        else dma_rows<LPU, false>(rowp, doff, sring_lds + seq_stage + m0_off);
+        seq_stage = (seq_stage + SB) & (uint32_t)(NS * SB - 1);
+        seq_kw += S * kUnitKeys;
+        // the unit after it (its key is past the run's pages when none follows)
+        if (seq_kw < (u_lo + n) * kUnitKeys) seq_pid = ptab[min((seq_kw >> a.page_shift) - pg_lo, kPageTabInts - 1)];
+        (void)mine_units;
+      } else if constexpr (PAGED) {
         // the page-table path, then the lookup of the unit after it
         issue_prefix(sring_lds + (uint32_t)(seq_t % NS) * SB, ks + S * seq_t);
         ++seq_t;
@@ -1690,6 +1739,22 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   const int fm = fm0 != 0 && sa_in.direct_out ? fm0 | 4 : fm0;
   SplitArgs sa = sa_in;
   if (fm & 4) sa.ws_o = ca.o;
+  // paged, one key stream, head_dim 128, unchecked steps: the instance that
+  // takes the steady refills' pages from an LDS table of the run's page ids
+  // (FAST | 8), when every run spans at most kPageTabInts pages, runs are
+  // long enough to pay for it and the cache's rows take the row-base path
+  bool ptab = false;
+  Plan pt = p;
+  if constexpr (PAGED && D == 128) {
+    int max_lds = 0;
+    // a run starts on a 32-key boundary: page-aligned for pages of 16 or 32
+    // keys, so it spans ceil(keys / page) pages, one more with larger pages
+    const int64_t ps = (int64_t)1 << sa.page_shift;
+    const int64_t run_pages = ((int64_t)p.units_per_split * kUnitKeys + ps - 1) / ps + (ps > kUnitKeys ? 1 : 0);
+    ptab = p.streams == 1 && fm != 0 && p.units_per_split >= kPageTabMinUnits && run_pages <= kPageTabInts &&
+           sa.crs >= D && device_max_lds_per_block(&max_lds) == TSFA_OK && (size_t)max_lds >= kPagedLdsBytes;
+    pt.lds_bytes = kPagedLdsBytes;
+  }
   if (g_kernel_mask & 1) {
     int st;
     // paged: the unchecked steps need only full prefix units (the page-table
@@ -1702,8 +1767,10 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
            : p.streams == 2 ? (fm == 5   ? launch_split<T, D, 2, true, false, 5>(sa, p, stream)
                                : fm == 1 ? launch_split<T, D, 2, true, false, 1>(sa, p, stream)
                                          : launch_split<T, D, 2, true, false>(sa, p, stream))
-                            : (fm == 5   ? launch_split<T, D, 1, true, false, 5>(sa, p, stream)
-                               : fm == 1 ? launch_split<T, D, 1, true, false, 1>(sa, p, stream)
+                            : (fm == 5   ? (ptab ? launch_split<T, D, 1, true, false, D == 128 ? 13 : 5>(sa, pt, stream)
+                                                 : launch_split<T, D, 1, true, false, 5>(sa, p, stream))
+                               : fm == 1 ? (ptab ? launch_split<T, D, 1, true, false, D == 128 ? 9 : 1>(sa, pt, stream)
+                                                 : launch_split<T, D, 1, true, false, 1>(sa, p, stream))
                                          : launch_split<T, D, 1, true, false>(sa, p, stream));
     else
       st = p.streams == 2 ? (fm == 6   ? launch_split<T, D, 2, false, false, 6>(sa, p, stream)

@@ -185,7 +185,7 @@ int make_plan(int batch, int num_heads, int num_kv_heads, int q_len, int kv_len,
   p->n_items = (int)items;
   p->items_per_xcd = ceil_div(p->n_items, 8);
   p->grid = p->items_per_xcd * 8;
-  p->lds_bytes = kSplitLdsBytes;
+  p->lds_bytes = kSplitLdsBytes;  // (the paged page-id table's instances ask for kPagedLdsBytes at launch)
   if (p->lds_bytes > (size_t)max_lds) return TSFA_ERR_UNSUPPORTED;
   p->ring_stages = kRingBytes / p->streams / (2 * kUnitKeys * head_dim * 2);
   p->vt_max = (int)(kMaskWords / chunk_tokens(p->rows_per_chunk, G));
