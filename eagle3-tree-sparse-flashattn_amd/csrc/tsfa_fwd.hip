@@ -1739,10 +1739,11 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   const int fm = fm0 != 0 && sa_in.direct_out ? fm0 | 4 : fm0;
   SplitArgs sa = sa_in;
   if (fm & 4) sa.ws_o = ca.o;
-  // paged, one key stream, head_dim 128, unchecked steps: the instance that
-  // takes the steady refills' pages from an LDS table of the run's page ids
-  // (FAST | 8), when every run spans at most kPageTabInts pages, runs are
-  // long enough to pay for it and the cache's rows take the row-base path
+  // paged, head_dim 128, unchecked steps, one key stream (or two with a
+  // cache below 4 GB): the instance that takes the steady refills' pages
+  // from an LDS table of the run's page ids (FAST | 8), when every run spans
+  // at most kPageTabInts pages, runs are long enough to pay for it and the
+  // cache's rows take the row-base path
   bool ptab = false;
   Plan pt = p;
   if constexpr (PAGED && D == 128) {
@@ -1751,7 +1752,8 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
     // keys, so it spans ceil(keys / page) pages, one more with larger pages
     const int64_t ps = (int64_t)1 << sa.page_shift;
     const int64_t run_pages = ((int64_t)p.units_per_split * kUnitKeys + ps - 1) / ps + (ps > kUnitKeys ? 1 : 0);
-    ptab = p.streams == 1 && fm != 0 && p.units_per_split >= kPageTabMinUnits && run_pages <= kPageTabInts &&
+    ptab = (p.streams == 1 || sa.cache32) && fm != 0 && p.units_per_split >= kPageTabMinUnits &&
+           run_pages <= kPageTabInts &&
            sa.crs >= D && device_max_lds_per_block(&max_lds) == TSFA_OK && (size_t)max_lds >= kPagedLdsBytes;
     pt.lds_bytes = kPagedLdsBytes;
   }
@@ -1761,8 +1763,10 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
     // path serves every refill); FAST 5 also writes O (one-slot plans)
     if constexpr (PAGED)
       st = (sa.cache32 && p.streams == 2)
-               ? (fm == 5   ? launch_split<T, D, 2, true, true, 5>(sa, p, stream)
-                  : fm == 1 ? launch_split<T, D, 2, true, true, 1>(sa, p, stream)
+               ? (fm == 5   ? (ptab ? launch_split<T, D, 2, true, true, D == 128 ? 13 : 5>(sa, pt, stream)
+                                    : launch_split<T, D, 2, true, true, 5>(sa, p, stream))
+                  : fm == 1 ? (ptab ? launch_split<T, D, 2, true, true, D == 128 ? 9 : 1>(sa, pt, stream)
+                                    : launch_split<T, D, 2, true, true, 1>(sa, p, stream))
                             : launch_split<T, D, 2, true, true>(sa, p, stream))
            : p.streams == 2 ? (fm == 5   ? launch_split<T, D, 2, true, false, 5>(sa, p, stream)
                                : fm == 1 ? launch_split<T, D, 2, true, false, 1>(sa, p, stream)
