@@ -1122,7 +1122,7 @@ void split_kernel(const SplitArgs a) {
     // barrier publishes them.  Its own instance (FAST & 8): the general
     // path's variables beside the table's spilled SGPRs in the loop of the
     // two-stream kernels (the Llama-3-8B decode shape's paged call 19.9 ->
-    // 22.3 us with both paths in one instance).
+    // 22.3 us with both paths in one instance; 19.4 -> 19.1 us as its own).
     int* ptab = misc + kMiscInts;  // kPageTabInts entries (paged instances only)
     const int pg_lo = PAGED ? (int)(((int64_t)u_lo * kUnitKeys) >> a.page_shift) : 0;
     const int n_pg = PAGED ? (int)((((int64_t)(u_lo + n) * kUnitKeys - 1) >> a.page_shift) - pg_lo + 1) : 0;
@@ -1742,8 +1742,7 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   // paged, head_dim 128, unchecked steps, one key stream (or two with a
   // cache below 4 GB): the instance that takes the steady refills' pages
   // from an LDS table of the run's page ids (FAST | 8), when every run spans
-  // at most kPageTabInts pages, runs are long enough to pay for it and the
-  // cache's rows take the row-base path
+  // at most kPageTabInts pages and the cache's rows take the row-base path
   bool ptab = false;
   Plan pt = p;
   if constexpr (PAGED && D == 128) {
@@ -1752,8 +1751,7 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
     // keys, so it spans ceil(keys / page) pages, one more with larger pages
     const int64_t ps = (int64_t)1 << sa.page_shift;
     const int64_t run_pages = ((int64_t)p.units_per_split * kUnitKeys + ps - 1) / ps + (ps > kUnitKeys ? 1 : 0);
-    ptab = (p.streams == 1 || sa.cache32) && fm != 0 && p.units_per_split >= kPageTabMinUnits &&
-           run_pages <= kPageTabInts &&
+    ptab = (p.streams == 1 || sa.cache32) && fm != 0 && run_pages <= kPageTabInts &&
            sa.crs >= D && device_max_lds_per_block(&max_lds) == TSFA_OK && (size_t)max_lds >= kPagedLdsBytes;
     pt.lds_bytes = kPagedLdsBytes;
   }

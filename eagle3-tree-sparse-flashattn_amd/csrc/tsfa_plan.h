@@ -73,11 +73,9 @@ constexpr int kMaxTreeUnits = 1024;  // tree keys <= 32768
 constexpr int kMiscInts = 320;       // LDS scalars: visible-unit count, row_ptr window
 // dynamic LDS of the split kernel: ring, mask words, visible-unit list, scalars
 constexpr size_t kSplitLdsBytes = (size_t)kRingBytes + kMaskWords * 4 + (kMaxTreeUnits + kMiscInts) * 4;
-// paged, one key stream: the clamped page ids of a prefix run in LDS (plans
-// whose runs span more pages, or are shorter, read the page table unit by
-// unit)
+// paged: the clamped page ids of a prefix run in LDS (plans whose runs span
+// more pages read the page table unit by unit)
 constexpr int kPageTabInts = 2048;
-constexpr int kPageTabMinUnits = 32;
 constexpr size_t kPagedLdsBytes = kSplitLdsBytes + (size_t)kPageTabInts * 4;
 
 // Tokens a chunk of `rows` consecutive rows can touch, and q-blocks those span.
