@@ -563,6 +563,11 @@ void split_kernel(const SplitArgs a) {
   // units were requested into the stages a previous run left free starts at
   // stage stage_rot; 0, a constant the compiler folds, for the prefix runs)
   int stage_rot = 0;
+  // The folded tree state built during the run (below) is compiled into the
+  // one-slot instances only (DIRECT: where the planner folds the tree by
+  // default): in the others its scalars spill into the run's tail loop
+  // whether or not it runs.
+  constexpr bool TPRE = !RING2 && DIRECT;
   auto stage = [&](int j) { return sring_lds + (uint32_t)(((j + stage_rot) & (NS - 1)) * SB); };
   TSFA_CYC_DECL
 
@@ -1107,7 +1112,7 @@ void split_kernel(const SplitArgs a) {
     const int tok_hi_c = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);
     const int qb_lo_c = tok_lo / tBM, nqbc_c = tok_hi_c / tBM - qb_lo_c + 1;
     const int n_tu_c = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
-    const bool pre_try = !RING2 && do_tree && a.tree_pre != 0 && steps_run >= 3;
+    const bool pre_try = TPRE && do_tree && a.tree_pre != 0 && steps_run >= 3;
     int* rps_c = misc + 8;  // row_ptr[qb_lo .. qb_hi + 1]
     if (pre_try) {
       if (wave == 0 && lane <= nqbc_c) dma4(a.row_ptr + b * a.ms_row_ptr + qb_lo_c + lane, lds_addr(rps_c));
@@ -1446,10 +1451,11 @@ void split_kernel(const SplitArgs a) {
       units(
           nb, pre_tree ? min(mt, NS - 1) : 0, tree_key0, [&](int) { return true; },
           [&](int i) {
-            // (words built here are cut at the tree key limit already)
+            // prebuilt words are payload words, cut here at the tree key
+            // limit; words built after the run are cut already
             const int u = vis[vb0 + i], lim = a.tree_key_limit - u * kUnitKeys;
             const uint32_t w = masks[pre_tree ? u * a.tree_ntok + row_tt : row_tt * a.vt_max + i];
-            return lim < 32 ? w & ((1u << lim) - 1u) : w;
+            return TPRE && lim < 32 ? w & ((1u << lim) - 1u) : w;
           },
           [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [](int) {});
       sync_all();  // ring and masks free for the next batch
@@ -2622,7 +2628,10 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   sa.fold_tree = p.fold_tree;
   // Folded tree units: their state and mask words are built while the run
   // streams when the mask words of every tree unit for the chunk's tokens
-  // fit the mask table (TSFA_TREE_PRE=0 builds them after the run).
+  // fit the mask table (TSFA_TREE_PRE=0 builds them after the run).  Only
+  // the one-slot kernel that writes O (split_kernel<..., FAST | 4>, two key
+  // streams at head_dim 128) carries this path; the other instances ignore
+  // the flag and build the state after the run.
   sa.tree_ntok = (int)chunk_tokens(p.rows_per_chunk, gqa_group_size);
   const int64_t n_tree_units = ((int64_t)std::max(p.tree_key_limit, 0) + kUnitKeys - 1) / kUnitKeys;
   sa.tree_of_dense = meta_seq_stride[4] != 0 && meta_seq_stride[4] == meta_seq_stride[1] ? 1 : 0;

@@ -1,15 +1,16 @@
 """Folded tree units whose state is built while the prefix run streams.
 
-When the last prefix run of a row chunk also runs the chunk's tree units
-(the folded plan) and its rings meet every step (two key streams at head_dim
-128), the chunk's CSR entries, MIXED offsets and payload words are read during
-the run's last three steps and the first tree units are requested into the
-ring stages the run leaves free.  The tree units then run the same unit loop
+When the one prefix run of a row chunk also runs the chunk's tree units (the
+folded one-slot plan, whose kernel writes O) and its rings meet every step
+(two key streams at head_dim 128), the chunk's CSR entries, MIXED offsets and
+payload words are read during the run's last three steps and the first tree
+units are requested into the ring stages the run leaves free.  The tree units then run the same unit loop
 in the same order as when their state is built after the run
 (TSFA_TREE_PRE=0), so the two must agree bit for bit, and both must match the
 fp32 dense+mask oracle.  Chunks whose rows hold more than 64 CSR entries, and
 runs of fewer than three steps, build the state after the run inside the same
-launch.
+launch; so do folded plans of several slots (their kernel does not carry the
+prebuilt path).
 
 Also here: a block kind other than MIXED (1) is FULL, as in the reference
 (tree_sparse_flashattn.py:313-318: only blk_type == 1 reads the bitset), in
@@ -60,6 +61,10 @@ def _fwd_nan_filled(qd, kd, vd, meta):
     return tsf.tree_sparse_attention_fwd(qd, kd, vd, meta, out=out, workspace=ws)
 
 
+# folded tree, two key streams, one prefix run per chunk (more units per run
+# than any prefix here holds): one slot, the kernel that writes O
+ONE_SLOT = {"TSFA_FOLD_TREE": "1", "TSFA_STREAMS": "2", "TSFA_PREFIX_UNITS_PER_SPLIT": "4096"}
+
 CASES = [
     # b, hq, hkv, t, p, dtype, bm, bn, tree, per-sequence trees
     (3, 8, 2, 64, 2048, BF, 16, 64, "eagle", True),   # the 16-sequence decode layout, 3 sequences
@@ -75,12 +80,12 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=[f"t{i}" for i in range(len(CASES))])
 def test_prebuilt_tree_state_matches_state_built_after_the_run(case, monkeypatch):
     b, hq, hkv, t, p, dtype, bm, bn, kind, per_seq = case
-    # runs of 16 prefix units (8 steps) unless the prefix is shorter
-    for key, val in {"TSFA_FOLD_TREE": "1", "TSFA_STREAMS": "2", "TSFA_PREFIX_UNITS_PER_SPLIT": "16"}.items():
+    # one run per chunk over the whole prefix: the one-slot plan
+    for key, val in ONE_SLOT.items():
         monkeypatch.setenv(key, val)
     plan = _lib.fwd_plan(b, hq, hkv, t, p + t, p, 128)
-    # the folded plan with rings that meet every step (4 stages of 2 streams)
-    assert plan["fold_tree"] == 1 and plan["ring_stages"] == 4, plan
+    # the folded one-slot plan with rings that meet every step (4 stages of 2 streams)
+    assert plan["fold_tree"] == 1 and plan["slots"] == 1 and plan["ring_stages"] == 4, plan
     print(f"[prebuilt] case {case} plan {plan}", flush=True)
     rng = np.random.default_rng(t + p + bm)
     if per_seq:
@@ -106,7 +111,7 @@ def test_prebuilt_tree_state_matches_state_built_after_the_run(case, monkeypatch
 def test_prebuilt_tree_state_paged(monkeypatch):
     # the paged kernel takes the same folded path (its tree units through the
     # page table); paged and contiguous agree bit for bit
-    for key, val in {"TSFA_FOLD_TREE": "1", "TSFA_STREAMS": "2", "TSFA_PREFIX_UNITS_PER_SPLIT": "16"}.items():
+    for key, val in ONE_SLOT.items():
         monkeypatch.setenv(key, val)
     b, hq, hkv, t, p, dtype, bm, bn = 3, 8, 2, 64, 2048, BF, 16, 64
     rng = np.random.default_rng(11)
@@ -120,6 +125,28 @@ def test_prebuilt_tree_state_paged(monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(out_p, out_c)
     assert_close_to_oracle(out_p, oracle_out(q, k, v, mask, p), dtype)
+
+
+def test_multi_slot_folded_plans_build_the_state_after_the_run(monkeypatch):
+    # folded plans of several slots run the kernel without the prebuilt path:
+    # the flag changes nothing there, and both match the oracle
+    for key, val in {"TSFA_FOLD_TREE": "1", "TSFA_STREAMS": "2", "TSFA_PREFIX_UNITS_PER_SPLIT": "16"}.items():
+        monkeypatch.setenv(key, val)
+    b, hq, hkv, t, p, dtype, bm, bn = 2, 8, 2, 64, 1024, BF, 16, 64
+    plan = _lib.fwd_plan(b, hq, hkv, t, p + t, p, 128)
+    assert plan["fold_tree"] == 1 and plan["slots"] > 1, plan
+    rng = np.random.default_rng(17)
+    mask = torch.from_numpy(_tree("eagle", t, rng))
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, bm, bn)
+    q, k, v = _qkv(b, hq, hkv, t, p, 128, dtype, seed=17)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    outs = {}
+    for pre in ("1", "0"):
+        monkeypatch.setenv("TSFA_TREE_PRE", pre)
+        outs[pre] = _fwd_nan_filled(qd, kd, vd, meta)
+        torch.cuda.synchronize()
+    assert torch.equal(outs["1"], outs["0"])
+    assert_close_to_oracle(outs["1"], oracle_out(q, k, v, mask, p), dtype)
 
 
 def _with_kind_two(mask, meta, t, bm, bn, n_change, seed):
@@ -152,7 +179,7 @@ def test_block_kind_other_than_mixed_is_full(d, p, bn, fold, monkeypatch):
     if fold is not None:
         monkeypatch.setenv("TSFA_FOLD_TREE", fold)
     if fold == "1":
-        monkeypatch.setenv("TSFA_PREFIX_UNITS_PER_SPLIT", "16")
+        monkeypatch.setenv("TSFA_PREFIX_UNITS_PER_SPLIT", ONE_SLOT["TSFA_PREFIX_UNITS_PER_SPLIT"])
     b, hq, hkv, t, bm, dtype = 1, 8, 2, 64, 16, BF
     rng = np.random.default_rng(d + p)
     mask = torch.from_numpy(_tree("random", t, rng))
