@@ -568,7 +568,10 @@ void split_kernel(const SplitArgs a) {
   // default): in the others its scalars spill into the run's tail loop
   // whether or not it runs.
   constexpr bool TPRE = !RING2 && DIRECT;
-  auto stage = [&](int j) { return sring_lds + (uint32_t)(((j + stage_rot) & (NS - 1)) * SB); };
+  auto stage = [&](int j) -> uint32_t {
+    if constexpr (TPRE) return sring_lds + (uint32_t)(((j + stage_rot) & (NS - 1)) * SB);
+    else return sring_lds + (uint32_t)((j & (NS - 1)) * SB);
+  };
   TSFA_CYC_DECL
 
   // The stream's RG waves move equal shares of each unit: the first half of
@@ -902,15 +905,20 @@ void split_kernel(const SplitArgs a) {
     if constexpr (NEXT) TSFA_CYC(1);
   };
   // tail_hook(j) runs after the barrier of every step j past the unchecked
-  // steady state (each wave, all of them at the same barriers)
+  // steady state (each wave, all of them at the same barriers).  rot_c:
+  // the run starts at ring stage stage_rot (the prebuilt tree units);
+  // otherwise requests address their stages as j * SB / (j % NS) * SB,
+  // forms that leave the paged instances far fewer scalar spills than the
+  // masked one (two-stream paged kernels: 105-125 spilled SGPRs -> 38-42).
   auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c,
-                            auto tail_hook) {
+                            auto tail_hook, auto rot_c) {
+    constexpr bool ROT = decltype(rot_c)::value;
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     {
       // RING2: NS-2 units ahead, two issued at every other step
       constexpr int AHEAD = RING2 ? NS - 2 : NS - 1;
-      for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(stage(j), ks + S * j);
+      for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(ROT ? stage(j) : sring_lds + j * SB, ks + S * j);
       if constexpr (decltype(fast_c)::value) fast_c.init(AHEAD);  // the steady refills start there
       if (PAGED && AHEAD < mine) prefetch(key0_of(ks + S * AHEAD));
       if (mine > 0) wait_units<LPU, NS - 2>(min(mine, AHEAD) - 1);  // unit 0 landed
@@ -974,10 +982,12 @@ void split_kernel(const SplitArgs a) {
       if (j < 40) TSFA_STAMP(3 + j);
       TSFA_CYC(2);
       if constexpr (RING2) {
-        if (j + NS - 2 < mine) issue_of(stage(j + NS - 2), ks + S * (j + NS - 2));
-        if (j + NS - 1 < mine) issue_of(stage(j + NS - 1), ks + S * (j + NS - 1));
+        if (j + NS - 2 < mine)
+          issue_of(ROT ? stage(j + NS - 2) : sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
+        if (j + NS - 1 < mine)
+          issue_of(ROT ? stage(j + NS - 1) : sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
       } else if (j + NS - 1 < mine) {
-        issue_of(stage(j + NS - 1), ks + S * (j + NS - 1));
+        issue_of(ROT ? stage(j + NS - 1) : sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
       }
       if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
       __builtin_amdgcn_sched_barrier(0);
@@ -1045,8 +1055,8 @@ void split_kernel(const SplitArgs a) {
   };
   // issue_of(lds stage, i) requests run unit i (keys key0_of(i)) into a stage
   auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c,
-                   auto tail_hook) {
-    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c, tail_hook);
+                   auto tail_hook, auto rot_c) {
+    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c, tail_hook, rot_c);
   };
 
   // The chunk's tree state built while its last prefix run streams (below):
@@ -1114,9 +1124,11 @@ void split_kernel(const SplitArgs a) {
     const int n_tu_c = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
     const bool pre_try = TPRE && do_tree && a.tree_pre != 0 && steps_run >= 3;
     int* rps_c = misc + 8;  // row_ptr[qb_lo .. qb_hi + 1]
-    if (pre_try) {
-      if (wave == 0 && lane <= nqbc_c) dma4(a.row_ptr + b * a.ms_row_ptr + qb_lo_c + lane, lds_addr(rps_c));
-      for (int i = tid; i < a.tree_ntok * n_tu_c; i += kWaves * 64) masks[i] = 0u;
+    if constexpr (TPRE) {
+      if (pre_try) {
+        if (wave == 0 && lane <= nqbc_c) dma4(a.row_ptr + b * a.ms_row_ptr + qb_lo_c + lane, lds_addr(rps_c));
+        for (int i = tid; i < a.tree_ntok * n_tu_c; i += kWaves * 64) masks[i] = 0u;
+      }
     }
     // Paged runs of full prefix units: the run's page ids (list positions
     // pg_lo .. pg_lo + n_pg - 1, clamped like page_entry / clamp_page) leave
@@ -1152,9 +1164,11 @@ void split_kernel(const SplitArgs a) {
     TSFA_STAMP(1);
     read_q();
     if (QS > 1) sync_lds();
-    if (pre_try) {
-      const int e_b = rps_c[0], e_e = rps_c[nqbc_c];
-      pre_tree = e_e >= e_b && e_e - e_b <= 64;  // one lane per CSR entry
+    if constexpr (TPRE) {
+      if (pre_try) {
+        const int e_b = rps_c[0], e_e = rps_c[nqbc_c];
+        pre_tree = e_e >= e_b && e_e - e_b <= 64;  // one lane per CSR entry
+      }
     }
     // LDS of the prebuilt state: entry i's tree block at csr_tb[i], its kind
     // byte at csr_bt4 + i, its offset (MIXED) at csr_of[i]
@@ -1224,7 +1238,7 @@ void split_kernel(const SplitArgs a) {
                    lds_addr(masks + u * NT + (tg - tok_lo)));
       }
     };
-    auto tree_hook = [&](int j) {
+    auto tree_hook_tpre = [&](int j) {
       if (!pre_tree) return;
       const int e_b = rps_c[0], cnt = rps_c[nqbc_c] - e_b;
       const int wpr = tBN / kUnitKeys, NT = a.tree_ntok, tkl = a.tree_key_limit;
@@ -1284,6 +1298,10 @@ void split_kernel(const SplitArgs a) {
         }
       }
     };
+    // (only the instances that carry the prebuilt path compile it at all)
+    auto tree_hook = [&](int j) {
+      if constexpr (TPRE) tree_hook_tpre(j);
+    };
     // Steady refills (FAST, rotation off): the next unit's row pointer and
     // ring stage advance by S units and one stage per refill.
     const char* seq_rows = nullptr;
@@ -1339,7 +1357,8 @@ void split_kernel(const SplitArgs a) {
           else return P - key0_of(i) < kUnitKeys;
         },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix,
-        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next}, tree_hook);
+        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next}, tree_hook,
+        std::false_type{});
   }
   if (do_tree) {
     // Tree units.  With pre_tree the chunk's state, visible-unit list and
@@ -1348,39 +1367,42 @@ void split_kernel(const SplitArgs a) {
     // stages after that run's last (stage_rot).  Otherwise the state is
     // built here (after a prefix run: its ring reads and loads done, the
     // block states reuse the ring; Q already in registers) and the mask
-    // words (word token * vt_max + unit of the batch) batch by batch.  One
-    // unit loop serves both (a second copy of it spills).
-    const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-    const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
-    const int ntok = tok_hi - tok_lo + 1;
-    const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
-    const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
-    const int32_t* ci = a.col_idx + b * a.ms_col_idx;
-    const int8_t* bt = a.blk_type + b * a.ms_blk_type;
-    const int32_t* pl = a.payload + b * a.ms_payload;
-    const int32_t* of = a.offset + b * a.ms_offset;
-    int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
-    int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
-    // Block states of the chunk's q-blocks in two parallel round trips: the
-    // row_ptr window, then every CSR entry of those rows at once.
-    auto build_state = [&]() {
-      for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
-      if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
-      sync_lds();
-      const int e_begin = rps[0], e_end = rps[nqbc];
-      for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
-        int qq = 0;
-        while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
-        const int tb = ci[e];
-        // a block of any kind but MIXED is FULL (tree_sparse_flashattn.py:313-318)
-        if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
-      }
-      sync_lds();
-    };
-    if (!pre_tree) {
+    // words (word token * vt_max + unit of the batch) batch by batch.
+    // The unit loop in two forms, each branch with its own copy of the
+    // block-state code: written once for both (shared lambdas, or one loop
+    // with the prebuilt path switched off at run time), the instances
+    // without the prebuilt path spill more scalars (the paged page-table
+    // kernel: 31 -> 90 spilled SGPRs, 254 reloads in its checked-step loop).
+    if constexpr (!TPRE) {
       if (is_tree) load_q();
       else sync_all();
       TSFA_STAMP(43);
+      const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
+      const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
+      const int ntok = tok_hi - tok_lo + 1;
+      const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
+      const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
+      const int32_t* ci = a.col_idx + b * a.ms_col_idx;
+      const int8_t* bt = a.blk_type + b * a.ms_blk_type;
+      const int32_t* pl = a.payload + b * a.ms_payload;
+      const int32_t* of = a.offset + b * a.ms_offset;
+      int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
+      int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
+      // Block states of the chunk's q-blocks in two parallel round trips: the
+      // row_ptr window, then every CSR entry of those rows at once.
+      auto build_state = [&]() {
+        for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
+        if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
+        sync_lds();
+        const int e_begin = rps[0], e_end = rps[nqbc];
+        for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
+          int qq = 0;
+          while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
+          const int tb = ci[e];
+          if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
+        }
+        sync_lds();
+      };
       build_state();
       TSFA_STAMP(44);
       // Tree units holding a key some row of the chunk can see, compacted.
@@ -1409,16 +1431,9 @@ void split_kernel(const SplitArgs a) {
       }
       sync_lds();
       TSFA_STAMP(45);
-    }
-    const int n_vis = misc[0];
-    const int bsz = pre_tree ? n_vis : a.vt_max;  // units per batch of mask words
-    if (pre_tree) {
-      stage_rot = run_mine;
-      if (wave == 0) vm_wait<0>();  // its payload words, before the tree loop's first barrier
-    }
-    for (int vb0 = 0; vb0 < n_vis; vb0 += bsz) {
-      const int nb = min(bsz, n_vis - vb0);
-      if (!pre_tree) {
+      const int n_vis = misc[0];
+      for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
+        const int nb = min(a.vt_max, n_vis - vb0);
         if (vb0 > 0) build_state();
         // Per-token visibility word of each unit of the batch, from two 16-key
         // groups (BN is a multiple of 16, so a group never straddles blocks).
@@ -1444,22 +1459,134 @@ void split_kernel(const SplitArgs a) {
           reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
         }
         sync_lds();
+        TSFA_STAMP(46);
+        auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
+        units(
+            nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
+            [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [](int) {},
+            std::false_type{});
+        sync_all();  // ring and masks free for the next batch
+        TSFA_STAMP(47);
       }
-      TSFA_STAMP(46);
-      const int mt = nb > ks ? (nb - ks + S - 1) / S : 0;
-      auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
-      units(
-          nb, pre_tree ? min(mt, NS - 1) : 0, tree_key0, [&](int) { return true; },
-          [&](int i) {
-            // prebuilt words are payload words, cut here at the tree key
-            // limit; words built after the run are cut already
-            const int u = vis[vb0 + i], lim = a.tree_key_limit - u * kUnitKeys;
-            const uint32_t w = masks[pre_tree ? u * a.tree_ntok + row_tt : row_tt * a.vt_max + i];
-            return TPRE && lim < 32 ? w & ((1u << lim) - 1u) : w;
-          },
-          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [](int) {});
-      sync_all();  // ring and masks free for the next batch
-      TSFA_STAMP(47);
+    } else {
+      const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
+      const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
+      const int ntok = tok_hi - tok_lo + 1;
+      const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
+      const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
+      const int32_t* ci = a.col_idx + b * a.ms_col_idx;
+      const int8_t* bt = a.blk_type + b * a.ms_blk_type;
+      const int32_t* pl = a.payload + b * a.ms_payload;
+      const int32_t* of = a.offset + b * a.ms_offset;
+      int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
+      int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
+      // Block states of the chunk's q-blocks in two parallel round trips: the
+      // row_ptr window, then every CSR entry of those rows at once.
+      auto build_state = [&]() {
+        for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
+        if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
+        sync_lds();
+        const int e_begin = rps[0], e_end = rps[nqbc];
+        for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
+          int qq = 0;
+          while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
+          const int tb = ci[e];
+          // a block of any kind but MIXED is FULL (tree_sparse_flashattn.py:313-318)
+          if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
+        }
+        sync_lds();
+      };
+      // The visible tree units of the chunk: its block states, then the tree
+      // units holding a key some row of the chunk can see, compacted.
+      auto list_visible = [&]() {
+        if (is_tree) load_q();
+        else sync_all();
+        TSFA_STAMP(43);
+        build_state();
+        TSFA_STAMP(44);
+        const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
+        for (int i = tid; i < n_tu; i += kWaves * 64) vis[i] = 0;
+        sync_lds();
+        for (int i = tid; i < nqbc * ntb; i += kWaves * 64) {
+          if (st[i] != 0) {
+            const int tb = i % ntb;
+            const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
+            for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
+          }
+        }
+        sync_lds();
+        if (wave == 0) {
+          int nv = 0;
+          for (int base = 0; base < n_tu; base += 64) {
+            const int idx = base + lane;
+            const bool f = idx < n_tu && vis[idx] != 0;
+            const uint64_t bal = __ballot(f);
+            const int pre = __popcll(bal & ((1ull << lane) - 1ull));
+            if (f) vis[nv + pre] = idx;
+            nv += __popcll(bal);
+          }
+          if (lane == 0) misc[0] = nv;
+        }
+        sync_lds();
+        TSFA_STAMP(45);
+      };
+      // Per-token visibility word of each unit of the batch vb0 .. vb0+nb-1
+      // (word token * vt_max + unit), from two 16-key groups (BN is a multiple
+      // of 16, so a group never straddles blocks).
+      auto batch_words = [&](int vb0, int nb) {
+        for (int it = tid; it < ntok * nb * 2; it += kWaves * 64) {
+          const int q2 = it & 1, jt = it >> 1;
+          const int j = jt % nb, tt = jt / nb;
+          const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
+          const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
+          uint32_t bits = 0;
+          if (c0 < a.tree_key_limit) {
+            const int tb = c0 / BN;
+            const int e = st[(qb - qb_lo) * ntb + tb];
+            if (e < 0) {
+              bits = 0xffffu;
+            } else if (e > 0) {
+              const int flat = tl * BN + (c0 - tb * BN);  // multiple of 16: never straddles a word
+              bits = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 0xffffu;
+            }
+            const int valid = a.tree_key_limit - c0;
+            if (valid < 16) bits &= (1u << valid) - 1u;
+          }
+          // two 16-bit halves assembled through LDS: the q2 = 1 half lands in the high bits
+          reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
+        }
+        sync_lds();
+      };
+      if (!pre_tree) list_visible();
+      const int n_vis = misc[0];
+      const int bsz = pre_tree ? n_vis : a.vt_max;  // units per batch of mask words
+      if (pre_tree) {
+        stage_rot = run_mine;
+        if (wave == 0) vm_wait<0>();  // its payload words, before the tree loop's first barrier
+      }
+      for (int vb0 = 0; vb0 < n_vis; vb0 += bsz) {
+        const int nb = min(bsz, n_vis - vb0);
+        if (!pre_tree) {
+          if (vb0 > 0) build_state();
+          batch_words(vb0, nb);
+        }
+        TSFA_STAMP(46);
+        const int mt = nb > ks ? (nb - ks + S - 1) / S : 0;
+        auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
+        units(
+            nb, pre_tree ? min(mt, NS - 1) : 0, tree_key0, [&](int) { return true; },
+            [&](int i) {
+              // prebuilt words are payload words, cut here at the tree key
+              // limit; words built after the run are cut already
+              const int u = vis[vb0 + i], lim = a.tree_key_limit - u * kUnitKeys;
+              const uint32_t w = masks[pre_tree ? u * a.tree_ntok + row_tt : row_tt * a.vt_max + i];
+              return lim < 32 ? w & ((1u << lim) - 1u) : w;
+            },
+            [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [](int) {},
+            std::true_type{});
+        sync_all();  // ring and masks free for the next batch
+        TSFA_STAMP(47);
+      }
     }
   }
 
