@@ -152,15 +152,6 @@ struct SplitArgs {
   uint32_t cps_b32, crs_b32;  // its page and row strides in bytes
   int item_order;  // within an XCD: 0 natural, 1 prefix runs first, 2 tree items first
   int fold_tree;   // no tree items: the last prefix split of each chunk also runs the tree units
-  // fold_tree runs build the chunk's tree state while the prefix streams
-  // (rings that meet every step, BN a multiple of 32, at most 64 tree units,
-  // tree_ntok * tree units <= kMaskWords); tree_ntok bounds the tokens of
-  // one chunk
-  int tree_pre, tree_ntok;
-  // the offset array has an entry for every CSR entry (one tree per
-  // sequence in capacity layout, offset stride = col_idx stride): offsets
-  // are read with the CSR entries, not after their kinds
-  int tree_of_dense;
   // One-slot plans with O contiguous [B, Hq, q_len, D] and no LSE asked: the
   // split kernel writes O itself (ws_o is O; split_kernel<..., FAST | 4>)
   // and no combine runs.  Host-side only.
@@ -195,8 +186,8 @@ __device__ inline void dma16(const void* src, uint32_t lds_in) {
                : "memory", "m0");
 }
 // 4 bytes per lane HBM -> LDS (global_load_lds_dword): active lane i's dword
-// lands at lds_base + 4*i; inactive lanes write nothing.  Small metadata
-// reads that complete in order with the ring's unit loads.
+// lands at lds_base + 4*i; inactive lanes write nothing.  Small reads
+// (page ids) that complete in order with the ring's unit loads.
 __device__ inline void dma4(const void* src, uint32_t lds_in) {
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_in);
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
@@ -559,19 +550,8 @@ void split_kernel(const SplitArgs a) {
   const uint32_t sring_lds = __builtin_amdgcn_readfirstlane(lds_addr(sring));
   const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
   constexpr bool RING2 = NS >= 8;  // ring loop meets every other step
-  // LDS address of the ring stage of the stream's unit j (a run whose first
-  // units were requested into the stages a previous run left free starts at
-  // stage stage_rot; 0, a constant the compiler folds, for the prefix runs)
-  int stage_rot = 0;
-  // The folded tree state built during the run (below) is compiled into the
-  // one-slot instances only (DIRECT: where the planner folds the tree by
-  // default): in the others its scalars spill into the run's tail loop
-  // whether or not it runs.
-  constexpr bool TPRE = !RING2 && DIRECT;
-  auto stage = [&](int j) -> uint32_t {
-    if constexpr (TPRE) return sring_lds + (uint32_t)(((j + stage_rot) & (NS - 1)) * SB);
-    else return sring_lds + (uint32_t)((j & (NS - 1)) * SB);
-  };
+  // LDS address of the ring stage of the stream's unit j
+  auto stage = [&](int j) { return sring_lds + (uint32_t)((j & (NS - 1)) * SB); };
   TSFA_CYC_DECL
 
   // The stream's RG waves move equal shares of each unit: the first half of
@@ -904,21 +884,16 @@ void split_kernel(const SplitArgs a) {
     }
     if constexpr (NEXT) TSFA_CYC(1);
   };
-  // tail_hook(j) runs after the barrier of every step j past the unchecked
-  // steady state (each wave, all of them at the same barriers).  rot_c:
-  // the run starts at ring stage stage_rot (the prebuilt tree units);
-  // otherwise requests address their stages as j * SB / (j % NS) * SB,
-  // forms that leave the paged instances far fewer scalar spills than the
-  // masked one (two-stream paged kernels: 105-125 spilled SGPRs -> 38-42).
-  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c,
-                            auto tail_hook, auto rot_c) {
-    constexpr bool ROT = decltype(rot_c)::value;
+  // (requests address their stages as j * SB and (j % NS) * SB: the masked
+  // form of stage() there left the two-stream paged kernels 105-125
+  // spilled SGPRs instead of 38-42)
+  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     {
       // RING2: NS-2 units ahead, two issued at every other step
       constexpr int AHEAD = RING2 ? NS - 2 : NS - 1;
-      for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(ROT ? stage(j) : sring_lds + j * SB, ks + S * j);
+      for (int j = pre; j < AHEAD && j < mine; ++j) issue_of(sring_lds + j * SB, ks + S * j);
       if constexpr (decltype(fast_c)::value) fast_c.init(AHEAD);  // the steady refills start there
       if (PAGED && AHEAD < mine) prefetch(key0_of(ks + S * AHEAD));
       if (mine > 0) wait_units<LPU, NS - 2>(min(mine, AHEAD) - 1);  // unit 0 landed
@@ -982,12 +957,10 @@ void split_kernel(const SplitArgs a) {
       if (j < 40) TSFA_STAMP(3 + j);
       TSFA_CYC(2);
       if constexpr (RING2) {
-        if (j + NS - 2 < mine)
-          issue_of(ROT ? stage(j + NS - 2) : sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
-        if (j + NS - 1 < mine)
-          issue_of(ROT ? stage(j + NS - 1) : sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+        if (j + NS - 2 < mine) issue_of(sring_lds + ((j + NS - 2) % NS) * SB, ks + S * (j + NS - 2));
+        if (j + NS - 1 < mine) issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
       } else if (j + NS - 1 < mine) {
-        issue_of(ROT ? stage(j + NS - 1) : sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
+        issue_of(sring_lds + ((j + NS - 1) % NS) * SB, ks + S * (j + NS - 1));
       }
       if (PAGED && j + NS < mine) prefetch(key0_of(ks + S * (j + NS)));
       __builtin_amdgcn_sched_barrier(0);
@@ -1043,7 +1016,6 @@ void split_kernel(const SplitArgs a) {
     }
     for (int j = j0; j < steps; ++j) {
       ring_step(j);
-      tail_hook(j);
       if (j + 1 < mine && active) {
         pipe_iter(j, ks + S * j, std::true_type{}, s_cur, s_next, masked_of, mask_of);
         s_cur = s_next;
@@ -1054,15 +1026,10 @@ void split_kernel(const SplitArgs a) {
     if (mine > 0 && active) pipe_iter(mine - 1, ks + S * (mine - 1), std::false_type{}, s_cur, s_cur, masked_of, mask_of);
   };
   // issue_of(lds stage, i) requests run unit i (keys key0_of(i)) into a stage
-  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c,
-                   auto tail_hook, auto rot_c) {
-    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c, tail_hook, rot_c);
+  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
+    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c);
   };
 
-  // The chunk's tree state built while its last prefix run streams (below):
-  // pre_tree when it was, run_mine the stream's units in that run.
-  bool pre_tree = false;
-  int run_mine = 0;
   if (!is_tree) {
     // Prefix run: units [u_lo, u_lo + n) of keys [0, prefix_len); the last
     // unit of the prefix may be partial.
@@ -1104,32 +1071,6 @@ void split_kernel(const SplitArgs a) {
     // (same-box A/B; one unit: in between).
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int pre = min(mine, min(NS - QS, 2));
-    run_mine = mine;
-    // Tree state while the run streams (the run that carries the chunk's
-    // tree units, rings that meet every step): the chunk's row_ptr window
-    // leaves with Q; at the run's last three barriers (below) the CSR
-    // entries, the offsets of the MIXED ones (the offset array may be empty
-    // when no block is MIXED, tree_sparse_flashattn.py:142-147, so unless
-    // every entry has an offset only MIXED entries are read, after their
-    // kinds) and every payload word the chunk's tokens use are requested,
-    // the payload straight into the mask table (word u * tree_ntok + token:
-    // unit u's 32 keys, BN a multiple of 32), and the streams request their
-    // first tree units into the ring stages the run has left.  The tree
-    // units then start right after the run instead of after three dependent
-    // metadata round trips and a ring prologue of their own.
-    const int steps_run = (n + S - 1) / S;
-    const int tBM = a.block_m, tBN = a.block_n;
-    const int tok_hi_c = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);
-    const int qb_lo_c = tok_lo / tBM, nqbc_c = tok_hi_c / tBM - qb_lo_c + 1;
-    const int n_tu_c = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
-    const bool pre_try = TPRE && do_tree && a.tree_pre != 0 && steps_run >= 3;
-    int* rps_c = misc + 8;  // row_ptr[qb_lo .. qb_hi + 1]
-    if constexpr (TPRE) {
-      if (pre_try) {
-        if (wave == 0 && lane <= nqbc_c) dma4(a.row_ptr + b * a.ms_row_ptr + qb_lo_c + lane, lds_addr(rps_c));
-        for (int i = tid; i < a.tree_ntok * n_tu_c; i += kWaves * 64) masks[i] = 0u;
-      }
-    }
     // Paged runs of full prefix units: the run's page ids (list positions
     // pg_lo .. pg_lo + n_pg - 1, clamped like page_entry / clamp_page) leave
     // HBM with Q into an LDS table, so a steady refill takes its page from
@@ -1164,144 +1105,6 @@ void split_kernel(const SplitArgs a) {
     TSFA_STAMP(1);
     read_q();
     if (QS > 1) sync_lds();
-    if constexpr (TPRE) {
-      if (pre_try) {
-        const int e_b = rps_c[0], e_e = rps_c[nqbc_c];
-        pre_tree = e_e >= e_b && e_e - e_b <= 64;  // one lane per CSR entry
-      }
-    }
-    // LDS of the prebuilt state: entry i's tree block at csr_tb[i], its kind
-    // byte at csr_bt4 + i, its offset (MIXED) at csr_of[i]
-    int* csr_tb = misc + 80;
-    int* csr_bt4 = misc + 144;  // the dwords holding the entries' kind bytes
-    int* csr_of = misc + 168;
-    static_assert(168 + 64 <= kMiscInts && 8 + 64 <= 80, "prebuilt tree state in the LDS scalars");
-    const int32_t* ci_c = a.col_idx + b * a.ms_col_idx;
-    const int8_t* bt_c = a.blk_type + b * a.ms_blk_type;
-    // lane i (< cnt): entry i's tree block, kind and q-block row of the
-    // chunk; whether the entry names a tree block of the mask (others are
-    // skipped).  One LDS round trip: the q-block row is counted from the
-    // row_ptr window held one entry per lane.
-    auto csr_entry = [&](int e_b, int cnt, int& tb, int& kind, int& qq) {
-      const int rpl = lane <= nqbc_c ? rps_c[lane] : 0;
-      tb = lane < cnt ? csr_tb[lane] : -1;
-      kind = lane < cnt ? reinterpret_cast<const int8_t*>(csr_bt4)[(reinterpret_cast<uintptr_t>(bt_c + e_b) & 3) + lane]
-                        : 0;
-      qq = 0;
-      for (int i = 1; i < nqbc_c; ++i) qq += __builtin_amdgcn_readlane(rpl, i) <= e_b + lane ? 1 : 0;
-      return lane < cnt && tb >= 0 && tb < a.n_tree_blocks;
-    };
-    // The tree units some row of the chunk can see, one bit each (at most 64
-    // tree units): every unit of every block an entry names, below the tree
-    // key limit.
-    auto unit_mask = [&](bool ok, int tb, int wpr, int tkl) {
-      uint64_t vm = 0, ob = __ballot(ok);
-      while (ob) {
-        const int i = __builtin_ctzll(ob);
-        ob &= ob - 1;
-        const int tbi = __builtin_amdgcn_readlane(tb, i);
-        const int u0 = tbi * wpr, u1 = (min((tbi + 1) * tBN, tkl) + kUnitKeys - 1) / kUnitKeys;
-        if (u1 > u0) vm |= (u1 - u0 >= 64 ? ~0ull : ((1ull << (u1 - u0)) - 1ull)) << u0;
-      }
-      return vm;
-    };
-    // Three steps before the run ends wave 0 requests the CSR entries (and
-    // their offsets when every entry has one); at the next barrier (its loads
-    // all landed before it) every wave reads them and requests its stream's
-    // first NS - 2 tree units into the stages its run has left, and wave 0
-    // lists the visible units, writes the FULL blocks' words and requests
-    // the payload words (without the offsets yet: the MIXED offsets); at the
-    // last barrier the streams request one more tree unit (the stage of their
-    // unit before last is free then) and wave 0 requests the payload words if
-    // it had to wait for the offsets.  16-sequence decode shape: 51.6 ->
-    // 50.4 us per call (same-box A/B, three rounds); the offsets after the
-    // kinds throughout 51.0; the work spread over three waves, the tree units
-    // requested at the last barrier, 50.6 and noisier.
-    // (wave 0) every payload word the chunk's tokens use, straight into the
-    // mask table: token t's word of unit u is word (t - qb*BM) * BN/32 + u -
-    // tb*BN/32 of its block's bitset
-    auto request_payload = [&](bool ok, int tb, int kind, int qq) {
-      const int wpr = tBN / kUnitKeys, NT = a.tree_ntok, tkl = a.tree_key_limit;
-      const int off = ok && kind == TSFA_MIXED_BLOCK ? csr_of[lane] : 0;
-      const int32_t* pl = a.payload + b * a.ms_payload;
-      uint64_t mb = __ballot(ok && kind == TSFA_MIXED_BLOCK);
-      while (mb) {
-        const int i = __builtin_ctzll(mb);
-        mb &= mb - 1;
-        const int tbi = __builtin_amdgcn_readlane(tb, i), qb = qb_lo_c + __builtin_amdgcn_readlane(qq, i);
-        const int offi = __builtin_amdgcn_readlane(off, i);
-        const int t0 = max(tok_lo, qb * tBM), t1 = min(tok_hi_c, qb * tBM + tBM - 1);
-        for (int u = tbi * wpr; u < (tbi + 1) * wpr && u * kUnitKeys < tkl; ++u)
-          for (int tg = t0; tg <= t1; tg += 64)
-            if (tg + lane <= t1)
-              dma4(pl + offi + (int64_t)(tg + lane - qb * tBM) * wpr + (u - tbi * wpr),
-                   lds_addr(masks + u * NT + (tg - tok_lo)));
-      }
-    };
-    auto tree_hook_tpre = [&](int j) {
-      if (!pre_tree) return;
-      const int e_b = rps_c[0], cnt = rps_c[nqbc_c] - e_b;
-      const int wpr = tBN / kUnitKeys, NT = a.tree_ntok, tkl = a.tree_key_limit;
-      // tree unit jj of the stream (its ks + S*jj-th visible unit) into the
-      // stage the tree loop below gives it (rotated past the run's last)
-      auto issue_tree = [&](int jj, int u) {
-        issue_at(sring_lds + (uint32_t)(((mine + jj) & (NS - 1)) * SB), a.prefix_len + u * kUnitKeys);
-      };
-      if (j == steps_run - 3) {
-        // the CSR entries of the chunk's q-blocks (the kind bytes as the
-        // dwords that hold them: never past the dword of the last entry)
-        if (wave == 0 && cnt > 0) {
-          if (lane < cnt) dma4(ci_c + e_b + lane, lds_addr(csr_tb));
-          if (lane < cnt && a.tree_of_dense) dma4(a.offset + b * a.ms_offset + e_b + lane, lds_addr(csr_of));
-          const uintptr_t d0 = reinterpret_cast<uintptr_t>(bt_c + e_b) & ~(uintptr_t)3;
-          const int nd = (int)(((reinterpret_cast<uintptr_t>(bt_c + e_b + cnt - 1) & ~(uintptr_t)3) - d0) / 4) + 1;
-          if (lane < nd) dma4(reinterpret_cast<const void*>(d0 + 4 * (uintptr_t)lane), lds_addr(csr_bt4));
-        }
-      } else if (j == steps_run - 2) {
-        int tb, kind, qq;
-        const bool ok = csr_entry(e_b, cnt, tb, kind, qq);
-        const uint64_t vm = unit_mask(ok, tb, wpr, tkl);
-        const int n_vis = __popcll(vm), mt = n_vis > ks ? (n_vis - ks + S - 1) / S : 0;
-        for (int jj = 0; jj < min(mt, NS - 2); ++jj) {
-          uint64_t m = vm;
-          for (int k = 0; k < ks + S * jj; ++k) m &= m - 1;
-          issue_tree(jj, __builtin_ctzll(m));
-        }
-        if (wave == 0) {
-          if (a.tree_of_dense) request_payload(ok, tb, kind, qq);
-          if ((vm >> lane) & 1) vis[__popcll(vm & ((1ull << lane) - 1ull))] = lane;
-          if (lane == 0) misc[0] = n_vis;
-          // a block of any kind but MIXED is FULL (tree_sparse_flashattn.py:313-318)
-          uint64_t fb = __ballot(ok && kind != TSFA_MIXED_BLOCK);
-          while (fb) {
-            const int i = __builtin_ctzll(fb);
-            fb &= fb - 1;
-            const int tbi = __builtin_amdgcn_readlane(tb, i), qb = qb_lo_c + __builtin_amdgcn_readlane(qq, i);
-            const int t0 = max(tok_lo, qb * tBM) - tok_lo, t1 = min(tok_hi_c, qb * tBM + tBM - 1) - tok_lo;
-            for (int u = tbi * wpr; u * kUnitKeys < min((tbi + 1) * tBN, tkl); ++u)
-              for (int t = t0 + lane; t <= t1; t += 64) masks[u * NT + t] = 0xffffffffu;
-          }
-          if (!a.tree_of_dense && ok && kind == TSFA_MIXED_BLOCK)
-            dma4(a.offset + b * a.ms_offset + e_b + lane, lds_addr(csr_of));
-        }
-      } else if (j == steps_run - 1) {
-        const int n_vis = misc[0], mt = n_vis > ks ? (n_vis - ks + S - 1) / S : 0;
-        const bool more = mt > NS - 2;
-        if (more) issue_tree(NS - 2, vis[ks + S * (NS - 2)]);
-        if (wave == 0 && !a.tree_of_dense) {
-          // the offsets landed (only the unit just requested is newer)
-          if (more) vm_wait<LPU>();
-          else vm_wait<0>();
-          int tb, kind, qq;
-          const bool ok = csr_entry(e_b, cnt, tb, kind, qq);
-          request_payload(ok, tb, kind, qq);
-        }
-      }
-    };
-    // (only the instances that carry the prebuilt path compile it at all)
-    auto tree_hook = [&](int j) {
-      if constexpr (TPRE) tree_hook_tpre(j);
-    };
     // Steady refills (FAST, rotation off): the next unit's row pointer and
     // ring stage advance by S units and one stage per refill.
     const char* seq_rows = nullptr;
@@ -1357,236 +1160,105 @@ void split_kernel(const SplitArgs a) {
           else return P - key0_of(i) < kUnitKeys;
         },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix,
-        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next}, tree_hook,
-        std::false_type{});
+        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next});
   }
   if (do_tree) {
-    // Tree units.  With pre_tree the chunk's state, visible-unit list and
-    // mask words (word u * tree_ntok + token) were built while its prefix
-    // run streamed, and each stream's first units are in flight in the
-    // stages after that run's last (stage_rot).  Otherwise the state is
-    // built here (after a prefix run: its ring reads and loads done, the
-    // block states reuse the ring; Q already in registers) and the mask
+    // Tree units, after a prefix run (its ring reads and loads done: the
+    // block states reuse the ring; Q already in registers) or as a tree
+    // item: the chunk's block states, its visible tree units, then the mask
     // words (word token * vt_max + unit of the batch) batch by batch.
-    // The unit loop in two forms, each branch with its own copy of the
-    // block-state code: written once for both (shared lambdas, or one loop
-    // with the prebuilt path switched off at run time), the instances
-    // without the prebuilt path spill more scalars (the paged page-table
-    // kernel: 31 -> 90 spilled SGPRs, 254 reloads in its checked-step loop).
-    if constexpr (!TPRE) {
-      if (is_tree) load_q();
-      else sync_all();
-      TSFA_STAMP(43);
-      const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-      const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
-      const int ntok = tok_hi - tok_lo + 1;
-      const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
-      const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
-      const int32_t* ci = a.col_idx + b * a.ms_col_idx;
-      const int8_t* bt = a.blk_type + b * a.ms_blk_type;
-      const int32_t* pl = a.payload + b * a.ms_payload;
-      const int32_t* of = a.offset + b * a.ms_offset;
-      int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
-      int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
-      // Block states of the chunk's q-blocks in two parallel round trips: the
-      // row_ptr window, then every CSR entry of those rows at once.
-      auto build_state = [&]() {
-        for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
-        if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
-        sync_lds();
-        const int e_begin = rps[0], e_end = rps[nqbc];
-        for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
-          int qq = 0;
-          while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
-          const int tb = ci[e];
-          if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
-        }
-        sync_lds();
-      };
-      build_state();
-      TSFA_STAMP(44);
-      // Tree units holding a key some row of the chunk can see, compacted.
-      const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
-      for (int i = tid; i < n_tu; i += kWaves * 64) vis[i] = 0;
+    if (is_tree) load_q();
+    else sync_all();
+    TSFA_STAMP(43);
+    const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
+    const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
+    const int ntok = tok_hi - tok_lo + 1;
+    const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
+    const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
+    const int32_t* ci = a.col_idx + b * a.ms_col_idx;
+    const int8_t* bt = a.blk_type + b * a.ms_blk_type;
+    const int32_t* pl = a.payload + b * a.ms_payload;
+    const int32_t* of = a.offset + b * a.ms_offset;
+    int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
+    int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
+    // Block states of the chunk's q-blocks in two parallel round trips: the
+    // row_ptr window, then every CSR entry of those rows at once.
+    auto build_state = [&]() {
+      for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
+      if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
       sync_lds();
-      for (int i = tid; i < nqbc * ntb; i += kWaves * 64) {
-        if (st[i] != 0) {
-          const int tb = i % ntb;
-          const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
-          for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
-        }
+      const int e_begin = rps[0], e_end = rps[nqbc];
+      for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
+        int qq = 0;
+        while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
+        const int tb = ci[e];
+        if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
       }
       sync_lds();
-      if (wave == 0) {
-        int nv = 0;
-        for (int base = 0; base < n_tu; base += 64) {
-          const int idx = base + lane;
-          const bool f = idx < n_tu && vis[idx] != 0;
-          const uint64_t bal = __ballot(f);
-          const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-          if (f) vis[nv + pre] = idx;
-          nv += __popcll(bal);
+    };
+    build_state();
+    TSFA_STAMP(44);
+    // Tree units holding a key some row of the chunk can see, compacted.
+    const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
+    for (int i = tid; i < n_tu; i += kWaves * 64) vis[i] = 0;
+    sync_lds();
+    for (int i = tid; i < nqbc * ntb; i += kWaves * 64) {
+      if (st[i] != 0) {
+        const int tb = i % ntb;
+        const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
+        for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
+      }
+    }
+    sync_lds();
+    if (wave == 0) {
+      int nv = 0;
+      for (int base = 0; base < n_tu; base += 64) {
+        const int idx = base + lane;
+        const bool f = idx < n_tu && vis[idx] != 0;
+        const uint64_t bal = __ballot(f);
+        const int pre = __popcll(bal & ((1ull << lane) - 1ull));
+        if (f) vis[nv + pre] = idx;
+        nv += __popcll(bal);
+      }
+      if (lane == 0) misc[0] = nv;
+    }
+    sync_lds();
+    TSFA_STAMP(45);
+    const int n_vis = misc[0];
+    for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
+      const int nb = min(a.vt_max, n_vis - vb0);
+      if (vb0 > 0) build_state();
+      // Per-token visibility word of each unit of the batch, from two 16-key
+      // groups (BN is a multiple of 16, so a group never straddles blocks).
+      for (int it = tid; it < ntok * nb * 2; it += kWaves * 64) {
+        const int q2 = it & 1, jt = it >> 1;
+        const int j = jt % nb, tt = jt / nb;
+        const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
+        const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
+        uint32_t bits = 0;
+        if (c0 < a.tree_key_limit) {
+          const int tb = c0 / BN;
+          const int e = st[(qb - qb_lo) * ntb + tb];
+          if (e < 0) {
+            bits = 0xffffu;
+          } else if (e > 0) {
+            const int flat = tl * BN + (c0 - tb * BN);  // multiple of 16: never straddles a word
+            bits = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 0xffffu;
+          }
+          const int valid = a.tree_key_limit - c0;
+          if (valid < 16) bits &= (1u << valid) - 1u;
         }
-        if (lane == 0) misc[0] = nv;
+        // two 16-bit halves assembled through LDS: the q2 = 1 half lands in the high bits
+        reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
       }
       sync_lds();
-      TSFA_STAMP(45);
-      const int n_vis = misc[0];
-      for (int vb0 = 0; vb0 < n_vis; vb0 += a.vt_max) {
-        const int nb = min(a.vt_max, n_vis - vb0);
-        if (vb0 > 0) build_state();
-        // Per-token visibility word of each unit of the batch, from two 16-key
-        // groups (BN is a multiple of 16, so a group never straddles blocks).
-        for (int it = tid; it < ntok * nb * 2; it += kWaves * 64) {
-          const int q2 = it & 1, jt = it >> 1;
-          const int j = jt % nb, tt = jt / nb;
-          const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
-          const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
-          uint32_t bits = 0;
-          if (c0 < a.tree_key_limit) {
-            const int tb = c0 / BN;
-            const int e = st[(qb - qb_lo) * ntb + tb];
-            if (e < 0) {
-              bits = 0xffffu;
-            } else if (e > 0) {
-              const int flat = tl * BN + (c0 - tb * BN);  // multiple of 16: never straddles a word
-              bits = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 0xffffu;
-            }
-            const int valid = a.tree_key_limit - c0;
-            if (valid < 16) bits &= (1u << valid) - 1u;
-          }
-          // two 16-bit halves assembled through LDS: the q2 = 1 half lands in the high bits
-          reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
-        }
-        sync_lds();
-        TSFA_STAMP(46);
-        auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
-        units(
-            nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
-            [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [](int) {},
-            std::false_type{});
-        sync_all();  // ring and masks free for the next batch
-        TSFA_STAMP(47);
-      }
-    } else {
-      const int P = a.prefix_len, BM = a.block_m, BN = a.block_n, ntb = a.n_tree_blocks;
-      const int tok_hi = (int)fdiv(row0 + rows_chunk - 1, a.fd_group);  // tokens tok_lo .. tok_hi
-      const int ntok = tok_hi - tok_lo + 1;
-      const int qb_lo = tok_lo / BM, qb_hi = tok_hi / BM, nqbc = qb_hi - qb_lo + 1;
-      const int32_t* rp = a.row_ptr + b * a.ms_row_ptr;
-      const int32_t* ci = a.col_idx + b * a.ms_col_idx;
-      const int8_t* bt = a.blk_type + b * a.ms_blk_type;
-      const int32_t* pl = a.payload + b * a.ms_payload;
-      const int32_t* of = a.offset + b * a.ms_offset;
-      int* st = reinterpret_cast<int*>(ring);  // [nqbc][ntb]: 0 ZERO, -1 FULL, 1+offset MIXED
-      int* rps = misc + 8;                     // row_ptr[qb_lo .. qb_hi+1]
-      // Block states of the chunk's q-blocks in two parallel round trips: the
-      // row_ptr window, then every CSR entry of those rows at once.
-      auto build_state = [&]() {
-        for (int i = tid; i < nqbc * ntb; i += kWaves * 64) st[i] = 0;
-        if (tid <= nqbc) rps[tid] = rp[qb_lo + tid];
-        sync_lds();
-        const int e_begin = rps[0], e_end = rps[nqbc];
-        for (int e = e_begin + tid; e < e_end; e += kWaves * 64) {
-          int qq = 0;
-          while (qq + 1 < nqbc && rps[qq + 1] <= e) ++qq;
-          const int tb = ci[e];
-          // a block of any kind but MIXED is FULL (tree_sparse_flashattn.py:313-318)
-          if (tb >= 0 && tb < ntb) st[qq * ntb + tb] = (bt[e] != TSFA_MIXED_BLOCK) ? -1 : (of[e] + 1);
-        }
-        sync_lds();
-      };
-      // The visible tree units of the chunk: its block states, then the tree
-      // units holding a key some row of the chunk can see, compacted.
-      auto list_visible = [&]() {
-        if (is_tree) load_q();
-        else sync_all();
-        TSFA_STAMP(43);
-        build_state();
-        TSFA_STAMP(44);
-        const int n_tu = (a.tree_key_limit + kUnitKeys - 1) / kUnitKeys;
-        for (int i = tid; i < n_tu; i += kWaves * 64) vis[i] = 0;
-        sync_lds();
-        for (int i = tid; i < nqbc * ntb; i += kWaves * 64) {
-          if (st[i] != 0) {
-            const int tb = i % ntb;
-            const int c_first = tb * BN, c_last = min(tb * BN + BN, a.tree_key_limit) - 1;
-            for (int u = c_first / kUnitKeys; u <= c_last / kUnitKeys; ++u) vis[u] = 1;
-          }
-        }
-        sync_lds();
-        if (wave == 0) {
-          int nv = 0;
-          for (int base = 0; base < n_tu; base += 64) {
-            const int idx = base + lane;
-            const bool f = idx < n_tu && vis[idx] != 0;
-            const uint64_t bal = __ballot(f);
-            const int pre = __popcll(bal & ((1ull << lane) - 1ull));
-            if (f) vis[nv + pre] = idx;
-            nv += __popcll(bal);
-          }
-          if (lane == 0) misc[0] = nv;
-        }
-        sync_lds();
-        TSFA_STAMP(45);
-      };
-      // Per-token visibility word of each unit of the batch vb0 .. vb0+nb-1
-      // (word token * vt_max + unit), from two 16-key groups (BN is a multiple
-      // of 16, so a group never straddles blocks).
-      auto batch_words = [&](int vb0, int nb) {
-        for (int it = tid; it < ntok * nb * 2; it += kWaves * 64) {
-          const int q2 = it & 1, jt = it >> 1;
-          const int j = jt % nb, tt = jt / nb;
-          const int t = tok_lo + tt, qb = t / BM, tl = t - qb * BM;
-          const int c0 = vis[vb0 + j] * kUnitKeys + q2 * 16;
-          uint32_t bits = 0;
-          if (c0 < a.tree_key_limit) {
-            const int tb = c0 / BN;
-            const int e = st[(qb - qb_lo) * ntb + tb];
-            if (e < 0) {
-              bits = 0xffffu;
-            } else if (e > 0) {
-              const int flat = tl * BN + (c0 - tb * BN);  // multiple of 16: never straddles a word
-              bits = ((uint32_t)pl[e - 1 + (flat >> 5)] >> (flat & 31)) & 0xffffu;
-            }
-            const int valid = a.tree_key_limit - c0;
-            if (valid < 16) bits &= (1u << valid) - 1u;
-          }
-          // two 16-bit halves assembled through LDS: the q2 = 1 half lands in the high bits
-          reinterpret_cast<uint16_t*>(masks)[(tt * a.vt_max + j) * 2 + q2] = (uint16_t)bits;
-        }
-        sync_lds();
-      };
-      if (!pre_tree) list_visible();
-      const int n_vis = misc[0];
-      const int bsz = pre_tree ? n_vis : a.vt_max;  // units per batch of mask words
-      if (pre_tree) {
-        stage_rot = run_mine;
-        if (wave == 0) vm_wait<0>();  // its payload words, before the tree loop's first barrier
-      }
-      for (int vb0 = 0; vb0 < n_vis; vb0 += bsz) {
-        const int nb = min(bsz, n_vis - vb0);
-        if (!pre_tree) {
-          if (vb0 > 0) build_state();
-          batch_words(vb0, nb);
-        }
-        TSFA_STAMP(46);
-        const int mt = nb > ks ? (nb - ks + S - 1) / S : 0;
-        auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
-        units(
-            nb, pre_tree ? min(mt, NS - 1) : 0, tree_key0, [&](int) { return true; },
-            [&](int i) {
-              // prebuilt words are payload words, cut here at the tree key
-              // limit; words built after the run are cut already
-              const int u = vis[vb0 + i], lim = a.tree_key_limit - u * kUnitKeys;
-              const uint32_t w = masks[pre_tree ? u * a.tree_ntok + row_tt : row_tt * a.vt_max + i];
-              return lim < 32 ? w & ((1u << lim) - 1u) : w;
-            },
-            [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [](int) {},
-            std::true_type{});
-        sync_all();  // ring and masks free for the next batch
-        TSFA_STAMP(47);
-      }
+      TSFA_STAMP(46);
+      auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
+      units(
+          nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
+          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{});
+      sync_all();  // ring and masks free for the next batch
+      TSFA_STAMP(47);
     }
   }
 
@@ -2753,19 +2425,6 @@ int fwd_impl(const void* q, const KvSource& kv, void* o, float* lse, const int32
   const int order = cfg.item_order;
   sa.item_order = order >= 0 && order <= 2 ? order : ((int64_t)p.n_items <= 4LL * cus ? 1 : 0);
   sa.fold_tree = p.fold_tree;
-  // Folded tree units: their state and mask words are built while the run
-  // streams when the mask words of every tree unit for the chunk's tokens
-  // fit the mask table (TSFA_TREE_PRE=0 builds them after the run).  Only
-  // the one-slot kernel that writes O (split_kernel<..., FAST | 4>, two key
-  // streams at head_dim 128) carries this path; the other instances ignore
-  // the flag and build the state after the run.
-  sa.tree_ntok = (int)chunk_tokens(p.rows_per_chunk, gqa_group_size);
-  const int64_t n_tree_units = ((int64_t)std::max(p.tree_key_limit, 0) + kUnitKeys - 1) / kUnitKeys;
-  sa.tree_of_dense = meta_seq_stride[4] != 0 && meta_seq_stride[4] == meta_seq_stride[1] ? 1 : 0;
-  sa.tree_pre = p.fold_tree && cfg.tree_pre != 0 && block_n % kUnitKeys == 0 && n_tree_units <= 64 &&
-                        (int64_t)sa.tree_ntok * n_tree_units <= kMaskWords
-                    ? 1
-                    : 0;
   // folded: the last run of each chunk carries the tree units, the longest
   // items, so those go first (longest first)
   if (p.fold_tree && order < 0) sa.item_order = sa.item_order ? 2 : 0;

@@ -45,7 +45,6 @@ Config read_config() {
   c.meta_small = env_int("TSFA_META_SMALL", 1);
   c.bwd_concurrent = env_int("TSFA_BWD_CONCURRENT", 1);
   c.bench_hooks = env_int("TSFA_BENCH_HOOKS", 0);
-  c.tree_pre = env_int("TSFA_TREE_PRE", 1);
   c.generation = 0;
   return c;
 }

@@ -53,7 +53,6 @@ struct Config {
   int meta_small;      // TSFA_META_SMALL: 0 always two metadata launches
   int bwd_concurrent;  // TSFA_BWD_CONCURRENT: 0 keeps the backward on one stream
   int bench_hooks;     // TSFA_BENCH_HOOKS: 1 unlocks tsfa_fwd_set_kernel_mask
-  int tree_pre;        // TSFA_TREE_PRE: 0 builds folded tree state after the prefix run
   int generation;      // bumped by every reload (keys of memoised plans)
 };
 // A copy of the switches, taken under the lock that config_reload holds, so

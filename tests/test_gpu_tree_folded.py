@@ -1,16 +1,13 @@
-"""Folded tree units whose state is built while the prefix run streams.
+"""Folded tree units, and block kinds other than MIXED.
 
-When the one prefix run of a row chunk also runs the chunk's tree units (the
-folded one-slot plan, whose kernel writes O) and its rings meet every step
-(two key streams at head_dim 128), the chunk's CSR entries, MIXED offsets and
-payload words are read during the run's last three steps and the first tree
-units are requested into the ring stages the run leaves free.  The tree units then run the same unit loop
-in the same order as when their state is built after the run
-(TSFA_TREE_PRE=0), so the two must agree bit for bit, and both must match the
-fp32 dense+mask oracle.  Chunks whose rows hold more than 64 CSR entries, and
-runs of fewer than three steps, build the state after the run inside the same
-launch; so do folded plans of several slots (their kernel does not carry the
-prebuilt path).
+When a row chunk's prefix run also runs the chunk's tree units (the folded
+plan: one slot, whose kernel writes O, or several slots with the tree in the
+last), the chunk's block states, visible tree units and mask words are built
+after the run inside the same launch.  These cases run such plans against the
+fp32 dense+mask oracle (per-sequence trees in capacity layout, BN 16 to 128,
+FULL and MIXED blocks, FULL only with an empty offset array, chunks of more
+than 64 CSR entries, runs of one step, 128-token q-blocks) and through
+the paged cache, bit-exact against the contiguous call.
 
 Also here: a block kind other than MIXED (1) is FULL, as in the reference
 (tree_sparse_flashattn.py:313-318: only blk_type == 1 reads the bitset), in
@@ -73,12 +70,12 @@ CASES = [
     (1, 8, 2, 64, 1024, BF, 16, 64, "ones", False),    # FULL blocks only, empty offset array
     (1, 2, 2, 512, 1024, FP, 16, 32, "chain", False),  # the last chunks hold > 64 CSR entries
     (1, 2, 2, 256, 512, BF, 128, 64, "random", False),  # 128 tokens of one q-block per chunk
-    (2, 8, 2, 40, 64, FP, 16, 32, "kary", False),      # two prefix units: runs too short
+    (2, 8, 2, 40, 64, FP, 16, 32, "kary", False),      # two prefix units: one step per run
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"t{i}" for i in range(len(CASES))])
-def test_prebuilt_tree_state_matches_state_built_after_the_run(case, monkeypatch):
+def test_folded_one_slot_plans(case, monkeypatch):
     b, hq, hkv, t, p, dtype, bm, bn, kind, per_seq = case
     # one run per chunk over the whole prefix: the one-slot plan
     for key, val in ONE_SLOT.items():
@@ -86,7 +83,7 @@ def test_prebuilt_tree_state_matches_state_built_after_the_run(case, monkeypatch
     plan = _lib.fwd_plan(b, hq, hkv, t, p + t, p, 128)
     # the folded one-slot plan with rings that meet every step (4 stages of 2 streams)
     assert plan["fold_tree"] == 1 and plan["slots"] == 1 and plan["ring_stages"] == 4, plan
-    print(f"[prebuilt] case {case} plan {plan}", flush=True)
+    print(f"[folded] case {case} plan {plan}", flush=True)
     rng = np.random.default_rng(t + p + bm)
     if per_seq:
         mask = torch.from_numpy(np.stack([_tree(kind, t, rng) for _ in range(b)]))
@@ -95,20 +92,13 @@ def test_prebuilt_tree_state_matches_state_built_after_the_run(case, monkeypatch
         mask = torch.from_numpy(_tree(kind, t, rng))
         meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, bm, bn)
     q, k, v = _qkv(b, hq, hkv, t, p, 128, dtype, seed=t + p)
-    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
-    outs = {}
-    for pre in ("1", "0"):
-        monkeypatch.setenv("TSFA_TREE_PRE", pre)
-        outs[pre] = _fwd_nan_filled(qd, kd, vd, meta)
-        torch.cuda.synchronize()
-    assert torch.equal(torch.isnan(outs["1"]), torch.isnan(outs["0"]))
-    assert torch.equal(outs["1"].nan_to_num(0.0), outs["0"].nan_to_num(0.0)), \
-        f"max diff {float((outs['1'].float() - outs['0'].float()).nan_to_num(0).abs().max()):.3e}"
-    assert_close_to_oracle(outs["1"], oracle_out(q, k, v, mask, p), dtype,
+    out = _fwd_nan_filled(q.cuda(), k.cuda(), v.cuda(), meta)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype,
                            half_ulps=storage_roundings(q, k, p) if p < 256 else 0)
 
 
-def test_prebuilt_tree_state_paged(monkeypatch):
+def test_folded_one_slot_paged(monkeypatch):
     # the paged kernel takes the same folded path (its tree units through the
     # page table); paged and contiguous agree bit for bit
     for key, val in ONE_SLOT.items():
@@ -127,9 +117,9 @@ def test_prebuilt_tree_state_paged(monkeypatch):
     assert_close_to_oracle(out_p, oracle_out(q, k, v, mask, p), dtype)
 
 
-def test_multi_slot_folded_plans_build_the_state_after_the_run(monkeypatch):
-    # folded plans of several slots run the kernel without the prebuilt path:
-    # the flag changes nothing there, and both match the oracle
+def test_folded_multi_slot_plans(monkeypatch):
+    # folded plans of several slots: the tree units in the last run, partials
+    # merged by the combine
     for key, val in {"TSFA_FOLD_TREE": "1", "TSFA_STREAMS": "2", "TSFA_PREFIX_UNITS_PER_SPLIT": "16"}.items():
         monkeypatch.setenv(key, val)
     b, hq, hkv, t, p, dtype, bm, bn = 2, 8, 2, 64, 1024, BF, 16, 64
@@ -139,14 +129,9 @@ def test_multi_slot_folded_plans_build_the_state_after_the_run(monkeypatch):
     mask = torch.from_numpy(_tree("eagle", t, rng))
     meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, bm, bn)
     q, k, v = _qkv(b, hq, hkv, t, p, 128, dtype, seed=17)
-    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
-    outs = {}
-    for pre in ("1", "0"):
-        monkeypatch.setenv("TSFA_TREE_PRE", pre)
-        outs[pre] = _fwd_nan_filled(qd, kd, vd, meta)
-        torch.cuda.synchronize()
-    assert torch.equal(outs["1"], outs["0"])
-    assert_close_to_oracle(outs["1"], oracle_out(q, k, v, mask, p), dtype)
+    out = _fwd_nan_filled(q.cuda(), k.cuda(), v.cuda(), meta)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype)
 
 
 def _with_kind_two(mask, meta, t, bm, bn, n_change, seed):
@@ -171,7 +156,7 @@ def _with_kind_two(mask, meta, t, bm, bn, n_change, seed):
     return changed, full, dense
 
 
-# the folded tree state built during the run (BN 32), separate tree items,
+# the folded one-slot plan (BN 32), separate tree items,
 # the generic kernel (head_dim 256) and the 64-wide kernel
 @pytest.mark.parametrize("d,p,bn,fold", [(128, 2048, 32, "1"), (128, 300, 16, "0"), (256, 300, 16, None),
                                          (64, 100, 16, None)])
