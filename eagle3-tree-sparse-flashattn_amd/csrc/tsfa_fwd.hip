@@ -469,10 +469,11 @@ template <bool V, typename I = int, typename N = int> struct FastSeq {
 };
 
 // S key streams of kWaves/S waves: a chunk is 32*kWaves/S rows.  FAST (every
-// prefix unit full; 1: plain loads, 2: non-temporal K/V loads; paged runs
-// choose the hint at run time and take 1): prefix runs skip the per-unit
-// mask test, contiguous ring runs issue every unit by the run-base path, and
-// the steady ring steps use a fixed wait count.
+// prefix unit within kv_len; 1: plain loads, 2: non-temporal K/V loads; paged
+// runs choose the hint at run time and take 1): prefix runs skip the per-unit
+// mask test (only a run's last unit can be the prefix's partial one, tested
+// once after the loop), contiguous ring runs issue every unit by the
+// run-base path, and the steady ring steps use a fixed wait count.
 template <typename T, int D, int S, bool PAGED, bool C32 = false, int FAST = 0>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void split_kernel(const SplitArgs a) {
@@ -887,7 +888,10 @@ void split_kernel(const SplitArgs a) {
   // (requests address their stages as j * SB and (j % NS) * SB: the masked
   // form of stage() there left the two-stream paged kernels 105-125
   // spilled SGPRs instead of 38-42)
-  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
+  // masked_last_of tests the stream's last unit, which the loops below never
+  // process (a prefix run's partial last unit, on the unchecked steps too)
+  auto run_units_pipe = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c,
+                            auto masked_last_of) {
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int steps = (n + S - 1) / S;
     {
@@ -1023,11 +1027,13 @@ void split_kernel(const SplitArgs a) {
     }
     // The stream's last unit: its V^T stage landed before barrier mine-2 and
     // no later load targets it (a load into it would be of unit >= mine).
-    if (mine > 0 && active) pipe_iter(mine - 1, ks + S * (mine - 1), std::false_type{}, s_cur, s_cur, masked_of, mask_of);
+    if (mine > 0 && active)
+      pipe_iter(mine - 1, ks + S * (mine - 1), std::false_type{}, s_cur, s_cur, masked_last_of, mask_of);
   };
   // issue_of(lds stage, i) requests run unit i (keys key0_of(i)) into a stage
-  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c) {
-    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c);
+  auto units = [&](int n, int pre, auto key0_of, auto masked_of, auto mask_of, auto issue_of, auto fast_c,
+                   auto masked_last_of) {
+    run_units_pipe(n, pre, key0_of, masked_of, mask_of, issue_of, fast_c, masked_last_of);
   };
 
   if (!is_tree) {
@@ -1071,7 +1077,7 @@ void split_kernel(const SplitArgs a) {
     // (same-box A/B; one unit: in between).
     const int mine = n > ks ? (n - ks + S - 1) / S : 0;
     const int pre = min(mine, min(NS - QS, 2));
-    // Paged runs of full prefix units: the run's page ids (list positions
+    // Paged runs on the unchecked steps: the run's page ids (list positions
     // pg_lo .. pg_lo + n_pg - 1, clamped like page_entry / clamp_page) leave
     // HBM with Q into an LDS table, so a steady refill takes its page from
     // one LDS read a step ahead and a product, instead of the page-table
@@ -1160,7 +1166,10 @@ void split_kernel(const SplitArgs a) {
           else return P - key0_of(i) < kUnitKeys;
         },
         [&](int i) { return (1u << (P - key0_of(i))) - 1u; }, issue_prefix,
-        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next});
+        FastSeq<FM != 0, decltype(seq_init), decltype(seq_next)>{seq_init, seq_next},
+        // the prefix's partial last unit (the last unit of its run: with the
+        // unchecked steps too, its keys past the prefix are masked here)
+        [&](int i) { return P - key0_of(i) < kUnitKeys; });
   }
   if (do_tree) {
     // Tree units, after a prefix run (its ring reads and loads done: the
@@ -1256,7 +1265,7 @@ void split_kernel(const SplitArgs a) {
       auto tree_key0 = [&](int i) { return P + vis[vb0 + i] * kUnitKeys; };
       units(
           nb, 0, tree_key0, [&](int) { return true; }, [&](int i) { return masks[row_tt * a.vt_max + i]; },
-          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{});
+          [&](uint32_t sb, int i) { issue_at(sb, tree_key0(i)); }, FastSeq<false>{}, [&](int) { return true; });
       sync_all();  // ring and masks free for the next batch
       TSFA_STAMP(47);
     }
@@ -1519,14 +1528,20 @@ int launch_split(const SplitArgs& args, const Plan& p, hipStream_t stream) {
 // launches (bit 0 split-KV, bit 1 combine).
 thread_local int g_kernel_mask = 3;
 
-// Contiguous calls whose prefix units are all full take the kernel with the
-// unchecked prefix ring steps (split_kernel<..., FAST>): 1 with plain K/V
+// The unchecked prefix ring steps load every prefix unit whole: the last,
+// partial one too (its keys past the prefix are masked at the end of its
+// run), so they need the prefix rounded up to whole units within kv_len.
+inline bool prefix_units_in_kv(const SplitArgs& sa) {
+  return ((int64_t)sa.prefix_len + kUnitKeys - 1) / kUnitKeys * kUnitKeys <= (int64_t)sa.kv_len;
+}
+
+// Contiguous calls whose prefix units lie within kv_len take the kernel with
+// the unchecked prefix ring steps (split_kernel<..., FAST>): 1 with plain K/V
 // loads, 2 with non-temporal ones (instantiated for two streams, where the
-// planner asks for them); 0 keeps the checked steps.  Every prefix unit lies
-// below kv_len (prefix_len <= kv_len), and the run-base path needs a row
-// stride of at least D in both K and V.
+// planner asks for them); 0 keeps the checked steps.  The run-base path
+// needs a row stride of at least D in both K and V.
 template <int D> inline int fast_ring(const SplitArgs& sa, const Plan& p, const Config& cfg) {
-  if (cfg.fast_ring == 0 || sa.prefix_len % kUnitKeys != 0 || sa.skn < D || sa.svn < D) return 0;
+  if (cfg.fast_ring == 0 || !prefix_units_in_kv(sa) || sa.skn < D || sa.svn < D) return 0;
   if (!sa.kv_nt) return 1;
   return p.streams == 2 ? 2 : 0;
 }
@@ -1539,7 +1554,7 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   // contiguous: the unchecked-step flavour, +4 for the kernel that writes O
   // itself (one-slot plans, with the unchecked steps only): then its
   // "partial" goes straight to O and the combine is not launched
-  const bool fp = cfg.fast_ring != 0 && sa_in.prefix_len % kUnitKeys == 0;
+  const bool fp = cfg.fast_ring != 0 && prefix_units_in_kv(sa_in);
   const int fm0 = PAGED ? (fp ? 1 : 0) : fast_ring<D>(sa_in, p, cfg);
   const int fm = fm0 != 0 && sa_in.direct_out ? fm0 | 4 : fm0;
   SplitArgs sa = sa_in;
@@ -1562,8 +1577,9 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   }
   if (g_kernel_mask & 1) {
     int st;
-    // paged: the unchecked steps need only full prefix units (the page-table
-    // path serves every refill); FAST 5 also writes O (one-slot plans)
+    // paged: the unchecked steps need only the prefix units within kv_len
+    // (the page-table path serves every refill); FAST 5 also writes O
+    // (one-slot plans)
     if constexpr (PAGED)
       st = (sa.cache32 && p.streams == 2)
                ? (fm == 5   ? (ptab ? launch_split<T, D, 2, true, true, D == 128 ? 13 : 5>(sa, pt, stream)
