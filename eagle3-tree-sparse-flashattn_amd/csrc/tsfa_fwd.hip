@@ -1560,9 +1560,11 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
   SplitArgs sa = sa_in;
   if (fm & 4) sa.ws_o = ca.o;
   // paged, head_dim 128, unchecked steps, one key stream (or two with a
-  // cache below 4 GB): the instance that takes the steady refills' pages
-  // from an LDS table of the run's page ids (FAST | 8), when every run spans
-  // at most kPageTabInts pages and the cache's rows take the row-base path
+  // cache below 4 GB, or two writing O): the instance that takes the steady
+  // refills' pages from an LDS table of the run's page ids (FAST | 8), when
+  // every run spans at most kPageTabInts pages and the cache's rows take the
+  // row-base path.  (Two streams over a larger cache with partials: that
+  // instance spilled 107 SGPRs, 589 reloads in its checked-step loop.)
   bool ptab = false;
   Plan pt = p;
   if constexpr (PAGED && D == 128) {
@@ -1571,7 +1573,7 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
     // keys, so it spans ceil(keys / page) pages, one more with larger pages
     const int64_t ps = (int64_t)1 << sa.page_shift;
     const int64_t run_pages = ((int64_t)p.units_per_split * kUnitKeys + ps - 1) / ps + (ps > kUnitKeys ? 1 : 0);
-    ptab = (p.streams == 1 || sa.cache32) && fm != 0 && run_pages <= kPageTabInts &&
+    ptab = (p.streams == 1 || sa.cache32 || fm == 5) && fm != 0 && run_pages <= kPageTabInts &&
            sa.crs >= D && device_max_lds_per_block(&max_lds) == TSFA_OK && (size_t)max_lds >= kPagedLdsBytes;
     pt.lds_bytes = kPagedLdsBytes;
   }
@@ -1587,7 +1589,8 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
                   : fm == 1 ? (ptab ? launch_split<T, D, 2, true, true, D == 128 ? 9 : 1>(sa, pt, stream)
                                     : launch_split<T, D, 2, true, true, 1>(sa, p, stream))
                             : launch_split<T, D, 2, true, true>(sa, p, stream))
-           : p.streams == 2 ? (fm == 5   ? launch_split<T, D, 2, true, false, 5>(sa, p, stream)
+           : p.streams == 2 ? (fm == 5   ? (ptab ? launch_split<T, D, 2, true, false, D == 128 ? 13 : 5>(sa, pt, stream)
+                                                 : launch_split<T, D, 2, true, false, 5>(sa, p, stream))
                                : fm == 1 ? launch_split<T, D, 2, true, false, 1>(sa, p, stream)
                                          : launch_split<T, D, 2, true, false>(sa, p, stream))
                             : (fm == 5   ? (ptab ? launch_split<T, D, 1, true, false, D == 128 ? 13 : 5>(sa, pt, stream)

@@ -98,22 +98,25 @@ def test_paged_64bit_offsets(case, monkeypatch):
 
 
 # Runs of at least 32 units (one key stream, or two with a cache below
-# 4 GB) take the instance that reads each run's page ids into an LDS table
-# with Q and refills from it (head_dim 128); runs of 64 units (two runs and
-# the combine) and of 128 with the tree folded in (one slot: the kernel
-# writes O), pages of 16 (two per unit) and 64 keys, both cache layouts, CSR
-# and dense page lists.
-@pytest.mark.parametrize("streams,ups,page_size,layout,dense", [
-    ("1", 64, 16, "NHD", False), ("1", 128, 64, "HND", True), ("1", 128, 16, "HND", False),
-    ("2", 64, 16, "NHD", False), ("2", 128, 32, "HND", True)])
-def test_paged_page_table_runs(streams, ups, page_size, layout, dense, monkeypatch):
-    env = {"TSFA_STREAMS": streams, "TSFA_PREFIX_UNITS_PER_SPLIT": str(ups)}
+# 4 GB or writing O) take the instance that reads each run's page ids into
+# an LDS table with Q and refills from it (head_dim 128); runs of 64 units
+# (two runs and the combine) and of 128 with the tree folded in (one slot:
+# the kernel writes O), pages of 16 (two per unit) and 64 keys, both cache
+# layouts, CSR and dense page lists, 32- and 64-bit page offsets (the latter
+# with partials: the general refill path).
+@pytest.mark.parametrize("streams,ups,page_size,layout,dense,paged32", [
+    ("1", 64, 16, "NHD", False, "1"), ("1", 128, 64, "HND", True, "1"), ("1", 128, 16, "HND", False, "1"),
+    ("2", 64, 16, "NHD", False, "1"), ("2", 128, 32, "HND", True, "1"),
+    ("2", 128, 16, "NHD", False, "0"), ("2", 64, 16, "NHD", False, "0")])
+def test_paged_page_table_runs(streams, ups, page_size, layout, dense, paged32, monkeypatch):
+    env = {"TSFA_STREAMS": streams, "TSFA_PREFIX_UNITS_PER_SPLIT": str(ups), "TSFA_PAGED32": paged32}
     if ups == 128:
         env["TSFA_FOLD_TREE"] = "1"
     for key, val in env.items():
         monkeypatch.setenv(key, val)
     b, hq, hkv, t, p, d, dtype = 2, 8, 2, 64, 4096, 128, BF
-    print(f"[paged] page table streams {streams} ups {ups} page_size {page_size} {layout} dense {dense}", flush=True)
+    print(f"[paged] page table streams {streams} ups {ups} page_size {page_size} {layout} dense {dense} "
+          f"paged32 {paged32}", flush=True)
     rng = np.random.default_rng(ups + page_size)
     mask = torch.from_numpy(_tree("random", t, rng))
     q, k, v = _qkv(b, hq, hkv, t, p, d, dtype, seed=ups)
