@@ -125,6 +125,29 @@ def test_paged_page_table_runs(streams, ups, page_size, layout, dense, paged32, 
     assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype)
 
 
+
+# A prefix with a partial last unit takes the unchecked steps on the paged
+# kernels too (the page-id table where it applies): two streams over 32- and
+# 64-bit offsets, with partials and one-slot (the kernel that writes O), and
+# one stream; each bit-exact against the contiguous call and within the bar
+# of the oracle.
+@pytest.mark.parametrize("streams,ups,paged32,p", [
+    ("2", 24, "1", 2047), ("2", 128, "0", 2017), ("2", 24, "0", 2047), ("1", 24, "0", 2017)])
+def test_paged_partial_last_unit(streams, ups, paged32, p, monkeypatch):
+    env = {"TSFA_STREAMS": streams, "TSFA_PREFIX_UNITS_PER_SPLIT": str(ups), "TSFA_PAGED32": paged32}
+    if ups == 128:
+        env["TSFA_FOLD_TREE"] = "1"
+    for key, val in env.items():
+        monkeypatch.setenv(key, val)
+    b, hq, hkv, t, d, dtype = 2, 8, 2, 64, 128, BF
+    print(f"[paged] partial last unit streams {streams} ups {ups} paged32 {paged32} p {p}", flush=True)
+    rng = np.random.default_rng(p + ups)
+    mask = torch.from_numpy(_tree("random", t, rng))
+    q, k, v = _qkv(b, hq, hkv, t, p, d, dtype, seed=p)
+    meta = tsf.prepare_tree_sparse_metadata(mask.cuda(), p, 64, 64)
+    out = _paged_vs_contiguous(q, k, v, meta, 16, "NHD", False, seed=p)
+    assert_close_to_oracle(out, oracle_out(q, k, v, mask, p), dtype)
+
 @pytest.mark.parametrize("page_size", [16, 64])
 def test_paged_workload_llama3_8b(page_size):
     w = configs.WORKLOADS["llama3-8b-eagle64-p4096"]
