@@ -1139,8 +1139,9 @@ void split_kernel(const SplitArgs a) {
         const char* rowp;
         if constexpr (C32)
           rowp = reinterpret_cast<const char*>(dbase) + ((uint32_t)pid * a.cps_b32 + (uint32_t)(seq_kw & pmask) * a.crs_b32);
-        else
-          rowp = reinterpret_cast<const char*>(dbase + (int64_t)pid * a.cps + (int64_t)(seq_kw & pmask) * a.crs);
+        else  // 64-bit page offset, 32-bit strides (the host checked that they fit)
+          rowp = reinterpret_cast<const char*>(dbase) + ((uint64_t)(uint32_t)pid * a.cps_b32 +
+                                                         (uint32_t)(seq_kw & pmask) * a.crs_b32);
         if (kv_nt) dma_rows<LPU, true>(rowp, doff, sring_lds + seq_stage + m0_off);
         else dma_rows<LPU, false>(rowp, doff, sring_lds + seq_stage + m0_off);
         seq_stage = (seq_stage + SB) & (uint32_t)(NS * SB - 1);
@@ -1573,7 +1574,10 @@ int launch_all(const SplitArgs& sa_in, const CombineArgs& ca, const Plan& p, con
     // keys, so it spans ceil(keys / page) pages, one more with larger pages
     const int64_t ps = (int64_t)1 << sa.page_shift;
     const int64_t run_pages = ((int64_t)p.units_per_split * kUnitKeys + ps - 1) / ps + (ps > kUnitKeys ? 1 : 0);
-    ptab = (p.streams == 1 || sa.cache32 || fm == 5) && fm != 0 && run_pages <= kPageTabInts &&
+    // (its 64-bit refills take the page and row strides in 32-bit bytes)
+    const bool strides32 = sa.cache32 || ((uint64_t)sa.cps * 2 < (1ull << 32) &&
+                                          (uint64_t)ps * (uint64_t)sa.crs * 2 < (1ull << 32));
+    ptab = (p.streams == 1 || sa.cache32 || fm == 5) && strides32 && fm != 0 && run_pages <= kPageTabInts &&
            sa.crs >= D && device_max_lds_per_block(&max_lds) == TSFA_OK && (size_t)max_lds >= kPagedLdsBytes;
     pt.lds_bytes = kPagedLdsBytes;
   }

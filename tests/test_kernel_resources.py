@@ -34,7 +34,7 @@ SPLIT_CEILINGS = {
     # paged, 32-bit offsets (two streams) and 64-bit (two streams, one stream)
     (2, True, True, 9): 35, (2, True, True, 13): 36, (2, True, True, 1): 43, (2, True, True, 5): 39,
     (2, True, True, 0): 46, (2, True, False, 13): 34, (2, True, False, 1): 42, (2, True, False, 5): 38,
-    (2, True, False, 0): 64, (1, True, False, 9): 38, (1, True, False, 13): 38, (1, True, False, 1): 56,
+    (2, True, False, 0): 64, (1, True, False, 9): 43, (1, True, False, 13): 38, (1, True, False, 1): 56,
     (1, True, False, 5): 33, (1, True, False, 0): 33,
 }
 SPLIT_RE = re.compile(r"_ZN4tsfa3fwd12split_kernelI(DF16b|DF16_)Li128ELi(\d)ELb(\d)ELb(\d)ELi(\d+)EEEvNS0_9SplitArgsE")
