@@ -69,7 +69,12 @@ def _run_and_check(q, k, v, do, mask, p, bm, bn, dtype, sm_scale=None, batched=F
     else:
         meta = tsf.prepare_tree_sparse_metadata(mask.to(dev), p, bm, bn)
     o, lse = tsf.tree_sparse_attention_fwd(qd, kd, vd, meta, sm_scale=sm_scale, return_lse=True)
-    dq, dk, dv = tsf.tree_sparse_attention_bwd(qd, kd, vd, o, lse, dod, meta, sm_scale=sm_scale)
+    # the gradients start as NaN, so a work item that is skipped or mapped to
+    # the wrong rows / keys (keys no row sees included: their dK, dV are 0)
+    # leaves NaN for _check to find instead of a stale correct value
+    dq, dk, dv = (torch.full_like(x, float("nan")) for x in (qd, kd, vd))
+    got = tsf.tree_sparse_attention_bwd(qd, kd, vd, o, lse, dod, meta, sm_scale=sm_scale, dq=dq, dk=dk, dv=dv)
+    assert all(g is x for g, x in zip(got, (dq, dk, dv)))
     torch.cuda.synchronize()
     rq, rk, rv, rlse = attention_grads(q, k, v, mask, p, do, scale=sm_scale, head_chunk=8)
     fin = torch.isfinite(rlse)
