@@ -60,9 +60,12 @@ def _paged_vs_contiguous(q, k, v, meta, page_size, layout, dense, seed):
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     cache, indptr, indices = configs.make_paged_kv(kd, vd, page_size, layout=layout, seed=seed, spare_pages=3,
                                                    dense_table=dense)
-    out_c = tsf.tree_sparse_attention_fwd(qd, kd, vd, meta)
+    # both outputs (and the contiguous call's workspace) start as NaN, so a
+    # work item that is skipped or mis-mapped cannot pass on a stale value
+    ws = torch.full((max(tsf.fwd_workspace_bytes(qd, kd, meta), 1),), 0xFF, dtype=torch.uint8, device=dev)
+    out_c = tsf.tree_sparse_attention_fwd(qd, kd, vd, meta, out=torch.full_like(qd, float("nan")), workspace=ws)
     out_p = tsf.tree_sparse_attention_fwd_paged(qd, cache, indices, meta, kv_len=k.shape[2], kv_indptr=indptr,
-                                                kv_layout=layout)
+                                                kv_layout=layout, out=torch.full_like(qd, float("nan")))
     torch.cuda.synchronize()
     assert torch.equal(torch.isnan(out_p), torch.isnan(out_c))
     assert torch.equal(out_p.nan_to_num(0.0), out_c.nan_to_num(0.0)), \
@@ -166,6 +169,8 @@ def test_paged_per_sequence_trees():
     mask = configs.make_tree_mask(w)
     meta = tsf.prepare_tree_sparse_metadata_batched(mask.cuda(), w.prefix_len, w.block_m, w.block_n)
     out = _paged_vs_contiguous(q, k, v, meta, 16, "HND", False, seed=3)
+    # every row sees the prefix: the heads the oracle skips must be written too
+    assert not torch.isnan(out).any()
     heads = (0, 7, 21, 31)
     ref = oracle_out(q, k, v, mask, w.prefix_len, heads=heads)
     assert_close_to_oracle(out, ref, w.dtype, heads=heads)
